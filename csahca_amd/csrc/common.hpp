@@ -1,0 +1,156 @@
+// common.hpp -- shared device helpers and host-side error plumbing for libcsahca.
+//
+// Written for gfx950 (CDNA4): 64-lane wavefronts, 16-byte global loads, fp32
+// math in VALU.  Softmax state is kept in the base-2 domain (scores pre-scaled
+// by log2(e)) so every exponential is one v_exp_f32.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "csahca.h"
+
+namespace csahca {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// Storage types
+// ---------------------------------------------------------------------------
+struct bf16 {
+  uint16_t bits;
+};
+using f16 = _Float16;
+
+__device__ __forceinline__ float bf16_bits_to_float(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+
+// fp32 -> bf16 with round-to-nearest-even (NaN stays NaN).
+__device__ __forceinline__ uint16_t float_to_bf16_bits(float x) {
+  uint32_t u = __float_as_uint(x);
+  if ((u & 0x7f800000u) == 0x7f800000u) {
+    if (u & 0x007fffffu) u |= 0x00400000u;
+    return static_cast<uint16_t>(u >> 16);
+  }
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(double x) { return static_cast<float>(x); }
+__device__ __forceinline__ float to_f32(f16 x) { return static_cast<float>(x); }
+__device__ __forceinline__ float to_f32(bf16 x) { return bf16_bits_to_float(x.bits); }
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float x);
+template <>
+__device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <>
+__device__ __forceinline__ double from_f32<double>(float x) { return static_cast<double>(x); }
+template <>
+__device__ __forceinline__ f16 from_f32<f16>(float x) { return static_cast<f16>(x); }
+template <>
+__device__ __forceinline__ bf16 from_f32<bf16>(float x) { return bf16{float_to_bf16_bits(x)}; }
+
+// Number of T elements in one 16-byte load.
+template <typename T>
+struct Vec16 {
+  static constexpr int N = 16 / static_cast<int>(sizeof(T));
+};
+
+// Load 16 bytes (N elements of T) and widen to fp32.  p must be 16-byte aligned.
+template <typename T>
+__device__ __forceinline__ void load16(const T* __restrict__ p, float* out);
+
+template <>
+__device__ __forceinline__ void load16<bf16>(const bf16* __restrict__ p, float* out) {
+  const uint4 w = *reinterpret_cast<const uint4*>(p);
+  const uint32_t v[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = __uint_as_float(v[i] << 16);
+    out[2 * i + 1] = __uint_as_float(v[i] & 0xffff0000u);
+  }
+}
+
+template <>
+__device__ __forceinline__ void load16<f16>(const f16* __restrict__ p, float* out) {
+  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+  const h8 w = *reinterpret_cast<const h8*>(p);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) out[i] = static_cast<float>(w[i]);
+}
+
+template <>
+__device__ __forceinline__ void load16<float>(const float* __restrict__ p, float* out) {
+  const float4 w = *reinterpret_cast<const float4*>(p);
+  out[0] = w.x;
+  out[1] = w.y;
+  out[2] = w.z;
+  out[3] = w.w;
+}
+
+template <>
+__device__ __forceinline__ void load16<double>(const double* __restrict__ p, float* out) {
+  const double2 w = *reinterpret_cast<const double2*>(p);
+  out[0] = static_cast<float>(w.x);
+  out[1] = static_cast<float>(w.y);
+}
+
+// Store N = 16/sizeof(T) values; p 16-byte aligned.
+template <typename T>
+__device__ __forceinline__ void store16(T* __restrict__ p, const float* v) {
+  constexpr int N = Vec16<T>::N;
+#pragma unroll
+  for (int i = 0; i < N; ++i) p[i] = from_f32<T>(v[i]);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Butterfly sums / maxima over lane groups (masks are XOR distances).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// Host helpers
+// ---------------------------------------------------------------------------
+int fail(int code, const char* msg);
+int fail_hip(hipError_t err, const char* where);
+void clear_error();
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+inline bool valid_dtype(int dt) {
+  return dt == CSAHCA_F32 || dt == CSAHCA_F16 || dt == CSAHCA_BF16 || dt == CSAHCA_F64;
+}
+
+// Dispatch a callable templated on the storage type.
+template <typename F>
+int dispatch_dtype(int dtype, F&& f) {
+  switch (dtype) {
+    case CSAHCA_BF16: return f(bf16{});
+    case CSAHCA_F16: return f(f16{});
+    case CSAHCA_F32: return f(float{});
+    case CSAHCA_F64: return f(double{});
+    default: return fail(CSAHCA_ERR_ARGUMENT, "unsupported dtype");
+  }
+}
+
+#define CSAHCA_REQUIRE(cond, msg)                                   \
+  do {                                                              \
+    if (!(cond)) return ::csahca::fail(CSAHCA_ERR_ARGUMENT, (msg)); \
+  } while (0)
+
+#define CSAHCA_LAUNCH_CHECK(where)                                 \
+  do {                                                             \
+    hipError_t e_ = hipGetLastError();                             \
+    if (e_ != hipSuccess) return ::csahca::fail_hip(e_, (where));  \
+  } while (0)
+
+}  // namespace csahca

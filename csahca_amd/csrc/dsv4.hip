@@ -1,0 +1,512 @@
+// dsv4.hip -- DSV4 MQA decode over the paged FP8 latent cache, for gfx950.
+//
+// Cache layout (hybrid_attention/dsv4_correctness.py:10-21,
+// csrc/dsv4_attention.cu:13-19): page p at byte p*bpp; page_size token rows of
+// 576 bytes (448 OCP e4m3 "nope" + 64 bf16 "rope"), then page_size scale rows
+// of 8 bytes (7 UE8M0 exponents: nope value = e4m3 * 2^(byte-127)).
+//
+// Kernel design: the latent row of a slot is shared by every query head (MQA,
+// V = K).  A work item is one wavefront over (query, group of HG heads, tile
+// of slots): it fetches each slot's row ONCE (lanes 0..55 take 8 fp8 bytes +
+// their tile's scale byte, lanes 56..63 take 16 bytes of rope), dequantises
+// into 8 fp32 registers per lane, and updates the online softmax of all HG
+// heads from those registers.  Partials (m, l, acc[512]) per (query, head,
+// tile) are merged by dsv4_merge_kernel, which also folds the attention sink
+// in as a virtual token of logit `sink` and value 0.
+#include "common.hpp"
+
+#include <algorithm>
+#include <climits>
+
+namespace csahca {
+namespace {
+
+constexpr int kNope = 448;
+constexpr int kRope = 64;
+constexpr int kDim = kNope + kRope;
+constexpr int kRowBytes = kNope + 2 * kRope;  // 576
+constexpr int kScaleTiles = kNope / 64;       // 7
+constexpr int kScaleBytes = kScaleTiles + 1;  // 8
+constexpr int kHeadGroup = 8;                 // heads per work item
+
+// OCP e4m3fn byte -> fp32 from the format definition (bias 7; exponent field 0
+// is subnormal m * 2^-9; S.1111.111 is NaN).
+__device__ __forceinline__ float e4m3_to_f32(uint32_t b) {
+  const uint32_t e = (b >> 3) & 15u;
+  const uint32_t m = b & 7u;
+  float mag = e ? __uint_as_float(((e + 120u) << 23) | (m << 20)) : static_cast<float>(m) * 0x1p-9f;
+  mag = ((b & 0x7fu) == 0x7fu) ? __builtin_nanf("") : mag;
+  return (b & 0x80u) ? -mag : mag;
+}
+
+// UE8M0 exponent byte -> 2^(byte-127).
+__device__ __forceinline__ float ue8m0_to_f32(uint32_t s) {
+  return s ? __uint_as_float(s << 23) : 0x1p-127f;
+}
+
+// Resolve slot s of a query to a row pointer (nullptr if the slot is skipped).
+struct CacheView {
+  const uint8_t* base;
+  int64_t num_pages;
+  int64_t bpp;
+  int page_size;
+};
+
+__device__ __forceinline__ const uint8_t* row_ptr(const CacheView& c, int32_t loc,
+                                                  const uint8_t** scale_row) {
+  if (loc < 0) return nullptr;
+  const int64_t page = loc / c.page_size;
+  if (page >= c.num_pages) return nullptr;
+  const int64_t in_page = loc - page * c.page_size;
+  const uint8_t* pg = c.base + page * c.bpp;
+  *scale_row = pg + static_cast<int64_t>(c.page_size) * kRowBytes + in_page * kScaleBytes;
+  return pg + in_page * kRowBytes;
+}
+
+// Dequantise this lane's 8 columns of a token row (columns 8*lane .. 8*lane+7).
+template <bool kVec>
+__device__ __forceinline__ void load_row8(const uint8_t* __restrict__ row,
+                                          const uint8_t* __restrict__ srow, int lane, float* kv) {
+  if (lane < kNope / 8) {
+    const float s = ue8m0_to_f32(srow[lane >> 3]);
+    uint32_t lo, hi;
+    if (kVec) {
+      const uint2 w = *reinterpret_cast<const uint2*>(row + 8 * lane);
+      lo = w.x;
+      hi = w.y;
+    } else {
+      const uint8_t* p = row + 8 * lane;
+      lo = p[0] | (p[1] << 8) | (p[2] << 16) | (static_cast<uint32_t>(p[3]) << 24);
+      hi = p[4] | (p[5] << 8) | (p[6] << 16) | (static_cast<uint32_t>(p[7]) << 24);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      kv[i] = e4m3_to_f32((lo >> (8 * i)) & 0xffu) * s;
+      kv[4 + i] = e4m3_to_f32((hi >> (8 * i)) & 0xffu) * s;
+    }
+  } else {
+    const uint8_t* p = row + kNope + 16 * (lane - kNope / 8);
+    uint32_t w[4];
+    if (kVec) {
+      const uint4 v = *reinterpret_cast<const uint4*>(p);
+      w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        w[i] = p[4 * i] | (p[4 * i + 1] << 8) | (p[4 * i + 2] << 16) |
+               (static_cast<uint32_t>(p[4 * i + 3]) << 24);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      kv[2 * i] = __uint_as_float(w[i] << 16);
+      kv[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+}
+
+struct Dsv4Args {
+  CacheView swa;
+  CacheView extra;
+  const int32_t* idx;
+  const int32_t* lens;
+  const int32_t* eidx;
+  const int32_t* elens;
+  float* part_ml;
+  float* part_acc;
+  int heads;
+  int head_groups;
+  int topk_slots;
+  int extra_slots;  // 0 when there is no extra cache
+  int tile;
+  int num_tiles;
+  float qscale;  // softmax_scale * log2(e)
+};
+
+template <typename T, bool kVec>
+__global__ __launch_bounds__(64) void dsv4_tile_kernel(const T* __restrict__ q, Dsv4Args a) {
+  const int lane = threadIdx.x;
+  const int64_t item = blockIdx.x;
+  const int t = static_cast<int>(item % a.num_tiles);
+  const int64_t rest = item / a.num_tiles;
+  const int hg = static_cast<int>(rest % a.head_groups);
+  const int64_t query = rest / a.head_groups;
+  const int h0 = hg * kHeadGroup;
+  const int nh = min(kHeadGroup, a.heads - h0);
+
+  float qr[kHeadGroup][8];
+#pragma unroll
+  for (int h = 0; h < kHeadGroup; ++h) {
+    if (h < nh) {
+      const T* qp = q + ((query * a.heads) + h0 + h) * kDim + 8 * lane;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qr[h][e] = to_f32(qp[e]) * a.qscale;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qr[h][e] = 0.f;
+    }
+  }
+
+  const int n_swa = a.lens ? max(0, min(a.lens[query], a.topk_slots)) : a.topk_slots;
+  const int n_extra =
+      a.extra_slots > 0 ? (a.elens ? max(0, min(a.elens[query], a.extra_slots)) : a.extra_slots) : 0;
+  const int total = a.topk_slots + a.extra_slots;
+  const int s0 = t * a.tile;
+  const int s1 = min(s0 + a.tile, total);
+
+  float m[kHeadGroup], l[kHeadGroup], acc[kHeadGroup][8];
+#pragma unroll
+  for (int h = 0; h < kHeadGroup; ++h) {
+    m[h] = -INFINITY;
+    l[h] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
+  }
+
+  for (int s = s0; s < s1; ++s) {
+    const uint8_t* row;
+    const uint8_t* srow = nullptr;
+    if (s < a.topk_slots) {
+      if (s >= n_swa) continue;
+      row = row_ptr(a.swa, a.idx[query * a.topk_slots + s], &srow);
+    } else {
+      const int j = s - a.topk_slots;
+      if (j >= n_extra) continue;
+      row = row_ptr(a.extra, a.eidx[query * a.extra_slots + j], &srow);
+    }
+    if (row == nullptr) continue;
+    float kv[8];
+    load_row8<kVec>(row, srow, lane, kv);
+    float sc[kHeadGroup];
+#pragma unroll
+    for (int h = 0; h < kHeadGroup; ++h) {
+      float d = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) d = fmaf(qr[h][e], kv[e], d);
+      sc[h] = d;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1)
+#pragma unroll
+      for (int h = 0; h < kHeadGroup; ++h) sc[h] += __shfl_xor(sc[h], off, kWave);
+#pragma unroll
+    for (int h = 0; h < kHeadGroup; ++h) {
+      const float m_new = fmaxf(m[h], sc[h]);
+      const float alpha = fast_exp2(m[h] - m_new);
+      const float p = fast_exp2(sc[h] - m_new);
+      l[h] = l[h] * alpha + p;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(p, kv[e], acc[h][e] * alpha);
+      m[h] = m_new;
+    }
+  }
+
+#pragma unroll
+  for (int h = 0; h < kHeadGroup; ++h) {
+    if (h < nh) {
+      const int64_t p = ((query * a.heads) + h0 + h) * a.num_tiles + t;
+      float* dst = a.part_acc + p * kDim + 8 * lane;
+      *reinterpret_cast<float4*>(dst) = make_float4(acc[h][0], acc[h][1], acc[h][2], acc[h][3]);
+      *reinterpret_cast<float4*>(dst + 4) = make_float4(acc[h][4], acc[h][5], acc[h][6], acc[h][7]);
+      if (lane == 0) {
+        a.part_ml[2 * p] = m[h];
+        a.part_ml[2 * p + 1] = l[h];
+      }
+    }
+  }
+}
+
+// Merge of the tile partials with the sink as a virtual token of logit
+// sink[h] and value 0 (csrc/dsv4_attention.cu:252-269): M = max(sink, m_t),
+// L = 2^(sink-M) + sum_{l_t>0} l_t 2^(m_t-M), out = sum 2^(m_t-M) acc_t / L.
+template <typename T>
+__global__ __launch_bounds__(128) void dsv4_merge_kernel(const float* __restrict__ part_ml,
+                                                         const float* __restrict__ part_acc,
+                                                         const float* __restrict__ sink,
+                                                         T* __restrict__ out, int heads,
+                                                         int num_tiles) {
+  const int64_t qh = blockIdx.x;
+  const int head = static_cast<int>(qh % heads);
+  const float* ml = part_ml + 2 * qh * num_tiles;
+  __shared__ float s_max, s_inv;
+  if (threadIdx.x < kWave) {
+    const float sk = sink ? sink[head] * kLog2e : -INFINITY;
+    float mx = -INFINITY;
+    for (int t = threadIdx.x; t < num_tiles; t += kWave) mx = fmaxf(mx, ml[2 * t]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
+    mx = fmaxf(mx, sk);
+    float L = 0.f;
+    for (int t = threadIdx.x; t < num_tiles; t += kWave) {
+      const float lt = ml[2 * t + 1];
+      if (lt > 0.f) L += lt * fast_exp2(ml[2 * t] - mx);
+    }
+    L = wave_sum(L);
+    if (threadIdx.x == 0) {
+      if (sink) L += fast_exp2(sk - mx);
+      s_max = mx;
+      s_inv = L > 0.f ? 1.f / L : 0.f;
+    }
+  }
+  __syncthreads();
+  const float mx = s_max, inv = s_inv;
+  const float* pa = part_acc + qh * num_tiles * static_cast<int64_t>(kDim);
+  for (int d = threadIdx.x * 4; d < kDim; d += blockDim.x * 4) {
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int t = 0; t < num_tiles; ++t) {
+      const float lt = ml[2 * t + 1];
+      if (lt > 0.f) {
+        const float w = fast_exp2(ml[2 * t] - mx);
+        const float4 v = *reinterpret_cast<const float4*>(pa + static_cast<int64_t>(t) * kDim + d);
+        acc.x = fmaf(w, v.x, acc.x);
+        acc.y = fmaf(w, v.y, acc.y);
+        acc.z = fmaf(w, v.z, acc.z);
+        acc.w = fmaf(w, v.w, acc.w);
+      }
+    }
+    T* o = out + qh * kDim + d;
+    o[0] = from_f32<T>(acc.x * inv);
+    o[1] = from_f32<T>(acc.y * inv);
+    o[2] = from_f32<T>(acc.z * inv);
+    o[3] = from_f32<T>(acc.w * inv);
+  }
+}
+
+// Split selection: tile_size > 0 -> ceil(total/tile) tiles (csrc/dsv4_attention.cu:858-860);
+// automatic -> about 2048 wavefronts over the device, at least 4 slots each.
+void dsv4_tiling(int64_t nq, int64_t heads, int64_t total_slots, int64_t tile_size,
+                 int64_t* tile_out, int64_t* tiles_out) {
+  const int64_t total = std::max<int64_t>(1, total_slots);
+  int64_t tiles;
+  if (tile_size > 0) {
+    tiles = ceil_div(total, tile_size);
+  } else {
+    const int64_t work = std::max<int64_t>(1, nq * ceil_div(std::max<int64_t>(1, heads), kHeadGroup));
+    const int64_t want = std::max<int64_t>(1, ceil_div(2048, work));
+    const int64_t max_tiles = std::max<int64_t>(1, ceil_div(total, 4));
+    tiles = std::min(want, max_tiles);
+  }
+  const int64_t tile = ceil_div(total, tiles);
+  *tile_out = tile;
+  *tiles_out = ceil_div(total, tile);
+}
+
+size_t ws_bytes(int64_t nq, int64_t heads, int64_t tiles) {
+  const size_t ml = static_cast<size_t>(nq * heads * tiles * 2) * sizeof(float);
+  return ((ml + 255) & ~size_t{255}) + static_cast<size_t>(nq * heads * tiles * kDim) * sizeof(float);
+}
+
+struct Dsv4Call {
+  const void* q;
+  int dtype;
+  int64_t nq, heads;
+  CacheView swa, extra;
+  const int32_t* idx;
+  int64_t topk_slots;
+  const int32_t* lens;
+  const int32_t* eidx;
+  int64_t extra_slots;
+  const int32_t* elens;
+  const float* sink;
+  double softmax_scale;
+  int64_t tile_size;
+  void* out;
+  void* workspace;
+  size_t workspace_bytes;
+  void* stream;
+};
+
+int dsv4_run(const Dsv4Call& c) {
+  if (c.nq == 0 || c.heads == 0) return CSAHCA_OK;
+  CSAHCA_REQUIRE(c.q && c.out, "null tensor pointer");
+  CSAHCA_REQUIRE(c.idx || c.topk_slots == 0 || c.nq == 0, "null token_indices pointer");
+  const int64_t total = c.topk_slots + c.extra_slots;
+  CSAHCA_REQUIRE(total <= INT_MAX && c.nq <= INT_MAX && c.heads <= INT_MAX, "too many slots");
+  int64_t tile, tiles;
+  dsv4_tiling(c.nq, c.heads, total, c.tile_size, &tile, &tiles);
+  const int64_t head_groups = ceil_div(c.heads, kHeadGroup);
+  CSAHCA_REQUIRE(c.nq * head_groups * tiles <= INT32_MAX, "too many DSV4 work items");
+  const size_t need = ws_bytes(c.nq, c.heads, tiles);
+  if (c.workspace == nullptr || c.workspace_bytes < need)
+    return fail(CSAHCA_ERR_WORKSPACE, "workspace too small for dsv4 decode");
+  Dsv4Args a;
+  a.swa = c.swa;
+  a.extra = c.extra;
+  a.idx = c.idx;
+  a.lens = c.lens;
+  a.eidx = c.eidx;
+  a.elens = c.elens;
+  a.part_ml = static_cast<float*>(c.workspace);
+  const size_t ml = static_cast<size_t>(c.nq * c.heads * tiles * 2) * sizeof(float);
+  a.part_acc = reinterpret_cast<float*>(static_cast<char*>(c.workspace) + ((ml + 255) & ~size_t{255}));
+  a.heads = static_cast<int>(c.heads);
+  a.head_groups = static_cast<int>(head_groups);
+  a.topk_slots = static_cast<int>(c.topk_slots);
+  a.extra_slots = static_cast<int>(c.extra_slots);
+  a.tile = static_cast<int>(tile);
+  a.num_tiles = static_cast<int>(tiles);
+  a.qscale = static_cast<float>(c.softmax_scale) * kLog2e;
+  const bool vec = reinterpret_cast<uintptr_t>(c.swa.base) % 16 == 0 && c.swa.bpp % 16 == 0 &&
+                   (c.extra_slots == 0 ||
+                    (reinterpret_cast<uintptr_t>(c.extra.base) % 16 == 0 && c.extra.bpp % 16 == 0));
+  hipStream_t stream = static_cast<hipStream_t>(c.stream);
+  const dim3 grid(static_cast<uint32_t>(c.nq * head_groups * tiles));
+  return dispatch_dtype(c.dtype, [&](auto tag) -> int {
+    using T = decltype(tag);
+    const T* qp = static_cast<const T*>(c.q);
+    if (vec)
+      dsv4_tile_kernel<T, true><<<grid, kWave, 0, stream>>>(qp, a);
+    else
+      dsv4_tile_kernel<T, false><<<grid, kWave, 0, stream>>>(qp, a);
+    CSAHCA_LAUNCH_CHECK("dsv4_tile_kernel");
+    dsv4_merge_kernel<T><<<dim3(static_cast<uint32_t>(c.nq * c.heads)), 128, 0, stream>>>(
+        a.part_ml, a.part_acc, c.sink, static_cast<T*>(c.out), a.heads, a.num_tiles);
+    CSAHCA_LAUNCH_CHECK("dsv4_merge_kernel");
+    return CSAHCA_OK;
+  });
+}
+
+int check_common(int dtype, int64_t nq, int64_t heads, int64_t bpp, int64_t page_size,
+                 int64_t num_pages, int64_t topk_slots) {
+  CSAHCA_REQUIRE(valid_dtype(dtype), "q must be float32, float64, float16 or bfloat16");
+  CSAHCA_REQUIRE(nq >= 0 && heads >= 0 && topk_slots >= 0 && num_pages >= 0 && bpp >= 0,
+                 "negative dimension");
+  CSAHCA_REQUIRE(page_size > 0, "page_size must be positive");
+  CSAHCA_REQUIRE(page_size <= INT_MAX, "page_size must fit in int32");
+  CSAHCA_REQUIRE(bpp >= page_size * (kRowBytes + kScaleBytes),
+                 "bytes_per_page is too small for DSV4 page layout");
+  return CSAHCA_OK;
+}
+
+}  // namespace
+}  // namespace csahca
+
+using namespace csahca;
+
+extern "C" size_t csahca_dsv4_decode_workspace_bytes(int64_t num_queries, int64_t heads,
+                                                     int64_t topk_slots, int64_t extra_topk_slots,
+                                                     int64_t tile_size) {
+  if (num_queries < 0 || heads < 0 || topk_slots < 0 || extra_topk_slots < 0) return 0;
+  int64_t tile, tiles;
+  dsv4_tiling(num_queries, heads, topk_slots + extra_topk_slots, tile_size, &tile, &tiles);
+  return ws_bytes(num_queries, heads, tiles);
+}
+
+extern "C" int csahca_dsv4_decode_forward_tiled(
+    const void* q, int dtype, int64_t num_queries, int64_t heads, const uint8_t* cache,
+    int64_t num_pages, int64_t bytes_per_page, int64_t page_size, const int32_t* token_indices,
+    int64_t topk_slots, const int32_t* topk_lengths, const uint8_t* extra_cache,
+    int64_t extra_num_pages, int64_t extra_bytes_per_page, int64_t extra_page_size,
+    const int32_t* extra_token_indices, int64_t extra_topk_slots,
+    const int32_t* extra_topk_lengths, const float* attn_sink, double softmax_scale,
+    int64_t tile_size, void* out, void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  int rc = check_common(dtype, num_queries, heads, bytes_per_page, page_size, num_pages, topk_slots);
+  if (rc != CSAHCA_OK) return rc;
+  CSAHCA_REQUIRE(bytes_per_page % 4 == 0,
+                 "tiled DSV4 kernel requires bytes_per_page divisible by 4 for vectorized loads");
+  CSAHCA_REQUIRE(tile_size >= 0, "tile_size must be non-negative");
+  const bool has_extra = extra_cache != nullptr && extra_num_pages * extra_bytes_per_page > 0 &&
+                         extra_token_indices != nullptr && num_queries * extra_topk_slots > 0;
+  Dsv4Call c{};
+  if (has_extra) {
+    CSAHCA_REQUIRE(extra_page_size > 0, "extra_page_size must be positive");
+    CSAHCA_REQUIRE(extra_page_size <= INT_MAX, "extra_page_size must fit in int32");
+    CSAHCA_REQUIRE(extra_bytes_per_page >= extra_page_size * (kRowBytes + kScaleBytes),
+                   "extra_bytes_per_page is too small for DSV4 page layout");
+    CSAHCA_REQUIRE(extra_bytes_per_page % 4 == 0,
+                   "tiled DSV4 kernel requires extra_bytes_per_page divisible by 4 for vectorized loads");
+    c.extra = CacheView{extra_cache, extra_num_pages, extra_bytes_per_page, static_cast<int>(extra_page_size)};
+    c.eidx = extra_token_indices;
+    c.extra_slots = extra_topk_slots;
+    c.elens = extra_topk_lengths;
+  }
+  c.q = q;
+  c.dtype = dtype;
+  c.nq = num_queries;
+  c.heads = heads;
+  c.swa = CacheView{cache, num_pages, bytes_per_page, static_cast<int>(page_size)};
+  c.idx = token_indices;
+  c.topk_slots = topk_slots;
+  c.lens = topk_lengths;
+  c.sink = attn_sink;
+  c.softmax_scale = softmax_scale;
+  c.tile_size = tile_size;
+  c.out = out;
+  c.workspace = workspace;
+  c.workspace_bytes = workspace_bytes;
+  c.stream = stream;
+  return dsv4_run(c);
+}
+
+extern "C" int csahca_dsv4_swa_decode_forward(const void* q, int dtype, int64_t num_queries,
+                                              int64_t heads, const uint8_t* cache,
+                                              int64_t num_pages, int64_t bytes_per_page,
+                                              int64_t page_size, const int32_t* token_indices,
+                                              int64_t topk_slots, const int32_t* topk_lengths,
+                                              const float* attn_sink, double softmax_scale,
+                                              void* out, void* workspace, size_t workspace_bytes,
+                                              void* stream) {
+  clear_error();
+  int rc = check_common(dtype, num_queries, heads, bytes_per_page, page_size, num_pages, topk_slots);
+  if (rc != CSAHCA_OK) return rc;
+  Dsv4Call c{};
+  c.q = q;
+  c.dtype = dtype;
+  c.nq = num_queries;
+  c.heads = heads;
+  c.swa = CacheView{cache, num_pages, bytes_per_page, static_cast<int>(page_size)};
+  c.idx = token_indices;
+  c.topk_slots = topk_slots;
+  c.lens = topk_lengths;
+  c.sink = attn_sink;
+  c.softmax_scale = softmax_scale;
+  c.tile_size = 0;
+  c.out = out;
+  c.workspace = workspace;
+  c.workspace_bytes = workspace_bytes;
+  c.stream = stream;
+  return dsv4_run(c);
+}
+
+extern "C" int csahca_dsv4_sparse_decode_forward(
+    const void* q, int dtype, int64_t num_queries, int64_t heads, const uint8_t* cache,
+    int64_t num_pages, int64_t bytes_per_page, int64_t page_size, const int32_t* token_indices,
+    int64_t topk_slots, const int32_t* topk_lengths, const uint8_t* extra_cache,
+    int64_t extra_num_pages, int64_t extra_bytes_per_page, int64_t extra_page_size,
+    const int32_t* extra_token_indices, int64_t extra_topk_slots,
+    const int32_t* extra_topk_lengths, const float* attn_sink, double softmax_scale, void* out,
+    void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  int rc = check_common(dtype, num_queries, heads, bytes_per_page, page_size, num_pages, topk_slots);
+  if (rc != CSAHCA_OK) return rc;
+  CSAHCA_REQUIRE(extra_page_size > 0, "extra_page_size must be positive");
+  CSAHCA_REQUIRE(extra_page_size <= INT_MAX, "extra_page_size must fit in int32");
+  CSAHCA_REQUIRE(extra_num_pages >= 0 && extra_topk_slots >= 0, "negative dimension");
+  CSAHCA_REQUIRE(extra_bytes_per_page >= extra_page_size * (kRowBytes + kScaleBytes),
+                 "extra_bytes_per_page is too small for DSV4 page layout");
+  Dsv4Call c{};
+  const bool has_extra = extra_cache != nullptr && extra_token_indices != nullptr &&
+                         extra_topk_slots > 0;
+  if (has_extra) {
+    c.extra = CacheView{extra_cache, extra_num_pages, extra_bytes_per_page, static_cast<int>(extra_page_size)};
+    c.eidx = extra_token_indices;
+    c.extra_slots = extra_topk_slots;
+    c.elens = extra_topk_lengths;
+  }
+  c.q = q;
+  c.dtype = dtype;
+  c.nq = num_queries;
+  c.heads = heads;
+  c.swa = CacheView{cache, num_pages, bytes_per_page, static_cast<int>(page_size)};
+  c.idx = token_indices;
+  c.topk_slots = topk_slots;
+  c.lens = topk_lengths;
+  c.sink = attn_sink;
+  c.softmax_scale = softmax_scale;
+  c.tile_size = 0;
+  c.out = out;
+  c.workspace = workspace;
+  c.workspace_bytes = workspace_bytes;
+  c.stream = stream;
+  return dsv4_run(c);
+}

@@ -1,0 +1,392 @@
+"""Torch-tensor binding of libcsahca.so -- the replacement for the reference's
+pybind module ``hybrid_attention_cuda`` (csrc/bindings.cpp:54-163).
+
+The five reference ops keep their names, argument order and error texts:
+``csa_decode_forward``, ``csa_decode_forward_tiled``, ``dsv4_swa_decode_forward``,
+``dsv4_sparse_decode_forward`` and ``dsv4_decode_forward_tiled``.  Structural
+checks (device, contiguity, rank, dtype, shape agreement) run here with the
+reference's TORCH_CHECK messages (csrc/csa_attention.cu:336-363,394-422,
+csrc/dsv4_attention.cu:593-625,671-728,775-848) and raise RuntimeError; value
+checks run in the C library.  Outputs and workspaces come from torch's caching
+allocator on the current stream; kernels run on torch's current HIP stream,
+so calls are graph-capturable.
+
+New ops next to them: ``csa_chunk_summary``, ``csa_select_topk`` and
+``csa_decode_step`` (summary scoring + top-k + sparse attention in one call).
+
+There is no CPU fallback: without the built library every op raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import torch
+
+_LIB_PATH = Path(__file__).resolve().parent / "libcsahca.so"
+_LIB = None
+
+_DTYPES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2, torch.float64: 3}
+_FLOATING = (torch.float32, torch.float16, torch.bfloat16, torch.float64)
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_sz = ctypes.c_size_t
+_dbl = ctypes.c_double
+
+_SIGNATURES = {
+    "csahca_last_error": (ctypes.c_char_p, []),
+    "csahca_abi_version": (_int, []),
+    "csahca_csa_decode_workspace_bytes": (_sz, [_i64] * 6),
+    "csahca_csa_auto_tile_size": (_i64, [_i64] * 4),
+    "csahca_csa_decode_forward": (_int, [_vp] * 5 + [_int, _int] + [_i64] * 6 + [_vp, _sz, _vp]),
+    "csahca_csa_decode_forward_tiled": (_int, [_vp] * 5 + [_int, _int] + [_i64] * 7 + [_vp, _sz, _vp]),
+    "csahca_csa_chunk_summary": (_int, [_vp, _vp, _int] + [_i64] * 8 + [_vp]),
+    "csahca_csa_select_workspace_bytes": (_sz, [_i64] * 3),
+    "csahca_csa_select_topk": (_int, [_vp, _vp, _vp, _int] + [_i64] * 5 + [_vp, _sz, _vp]),
+    "csahca_dsv4_decode_workspace_bytes": (_sz, [_i64] * 5),
+    "csahca_dsv4_decode_forward_tiled": (
+        _int, [_vp, _int, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _vp,
+               _i64, _vp, _vp, _dbl, _i64, _vp, _vp, _sz, _vp]),
+    "csahca_dsv4_swa_decode_forward": (
+        _int, [_vp, _int, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _dbl, _vp, _vp, _sz, _vp]),
+    "csahca_dsv4_sparse_decode_forward": (
+        _int, [_vp, _int, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _vp,
+               _i64, _vp, _vp, _dbl, _vp, _vp, _sz, _vp]),
+}
+
+EXPORTED = tuple(_SIGNATURES)
+
+
+def library_path() -> Path:
+    return _LIB_PATH
+
+
+def lib():
+    """Load libcsahca.so (raises if it has not been built)."""
+    global _LIB
+    if _LIB is None:
+        if not _LIB_PATH.exists():
+            raise RuntimeError(
+                f"{_LIB_PATH} is not built; run `python -m csahca_amd.build` (hipcc, gfx950)")
+        handle = ctypes.CDLL(str(_LIB_PATH))
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _LIB = handle
+    return _LIB
+
+
+def _check(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _rc(code: int) -> None:
+    if code != 0:
+        raise RuntimeError(lib().csahca_last_error().decode())
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else t.data_ptr()
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _workspace(nbytes: int, device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+def _defined(t) -> bool:
+    return t is not None
+
+
+def _present(t) -> bool:
+    """A tensor that carries values (None and empty tensors mean "absent")."""
+    return t is not None and t.numel() > 0
+
+
+# ---------------------------------------------------------------------------
+# CSA
+# ---------------------------------------------------------------------------
+
+def _csa_checks(q, k_cache, v_cache, chunk_indices, chunk_size, tiled: bool, tile_size=None):
+    if not (q.is_cuda and k_cache.is_cuda and v_cache.is_cuda and chunk_indices.is_cuda):
+        raise RuntimeError("all tensors must be CUDA tensors")
+    _check(q.is_contiguous(), "q must be contiguous")
+    _check(k_cache.is_contiguous(), "k_cache must be contiguous")
+    _check(v_cache.is_contiguous(), "v_cache must be contiguous")
+    _check(chunk_indices.is_contiguous(), "chunk_indices must be contiguous")
+    _check(q.dim() == 3, "q must be [batch, heads, head_dim]")
+    _check(k_cache.dim() == 4, "k_cache must be [batch, heads, seq, head_dim]")
+    _check(v_cache.shape == k_cache.shape, "v_cache must match k_cache shape")
+    _check(chunk_indices.dim() == 3, "chunk_indices must be [batch, heads, top_k]")
+    _check(q.dtype == k_cache.dtype, "q and k_cache dtype must match")
+    _check(q.dtype == v_cache.dtype, "q and v_cache dtype must match")
+    _check(chunk_indices.dtype in (torch.int32, torch.int64), "chunk_indices must be int32 or int64")
+    B, H, D = q.shape
+    _check(k_cache.shape[0] == B and k_cache.shape[1] == H and k_cache.shape[3] == D,
+           "KV cache shape must match q")
+    _check(chunk_indices.shape[0] == B and chunk_indices.shape[1] == H,
+           "chunk_indices batch/head dimensions must match q")
+    _check(chunk_size > 0, "chunk_size must be positive")
+    if tiled:
+        _check(tile_size > 0, "tile_size must be positive")
+        _check(D <= 1024, "head_dim > 1024 is not supported by the tiled kernel")
+    else:
+        _check(D <= 1024, "head_dim > 1024 is not supported by the v1 kernel")
+    _check(q.dtype in _FLOATING, f"unsupported dtype {q.dtype}")
+
+
+def csa_decode_forward(q, k_cache, v_cache, chunk_indices, chunk_size):
+    """Sparse decode over explicit chunk ids (reference op csa_decode_forward)."""
+    chunk_size = int(chunk_size)
+    _csa_checks(q, k_cache, v_cache, chunk_indices, chunk_size, tiled=False)
+    B, H, D = q.shape
+    S, top_k = k_cache.shape[2], chunk_indices.shape[2]
+    with torch.cuda.device(q.device):
+        out = torch.empty_like(q)
+        nbytes = lib().csahca_csa_decode_workspace_bytes(B, H, D, top_k, chunk_size, 0)
+        ws = _workspace(nbytes, q.device)
+        _rc(lib().csahca_csa_decode_forward(
+            _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(chunk_indices), _ptr(out), _DTYPES[q.dtype],
+            0 if chunk_indices.dtype == torch.int32 else 1, B, H, S, D, top_k, chunk_size,
+            _ptr(ws), ws.numel(), _stream()))
+    return out
+
+
+def csa_decode_forward_tiled(q, k_cache, v_cache, chunk_indices, chunk_size, tile_size):
+    """Split-KV sparse decode (reference op csa_decode_forward_tiled)."""
+    chunk_size, tile_size = int(chunk_size), int(tile_size)
+    _csa_checks(q, k_cache, v_cache, chunk_indices, chunk_size, tiled=True, tile_size=tile_size)
+    B, H, D = q.shape
+    S, top_k = k_cache.shape[2], chunk_indices.shape[2]
+    with torch.cuda.device(q.device):
+        out = torch.empty_like(q)
+        nbytes = lib().csahca_csa_decode_workspace_bytes(B, H, D, top_k, chunk_size, tile_size)
+        ws = _workspace(nbytes, q.device)
+        _rc(lib().csahca_csa_decode_forward_tiled(
+            _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(chunk_indices), _ptr(out), _DTYPES[q.dtype],
+            0 if chunk_indices.dtype == torch.int32 else 1, B, H, S, D, top_k, chunk_size, tile_size,
+            _ptr(ws), ws.numel(), _stream()))
+    return out
+
+
+def csa_auto_tile_size(batch: int, heads: int, top_k: int, chunk_size: int) -> int:
+    return int(lib().csahca_csa_auto_tile_size(batch, heads, top_k, chunk_size))
+
+
+def csa_chunk_summary(k_cache, chunk_size, *, out=None, chunk_begin: int = 0, num_chunks: int | None = None):
+    """fp32 chunk means of K (chunk_mean, hybrid_attention/reference.py:40-45).
+
+    Returns ``[B, H, S // chunk_size, D]`` fp32.  With ``out`` given, only chunks
+    ``[chunk_begin, chunk_begin + num_chunks)`` are (re)computed in place -- the
+    incremental update when the cache grows by a chunk.
+    """
+    chunk_size = int(chunk_size)
+    _check(k_cache.is_cuda, "k_cache must be CUDA")
+    _check(k_cache.is_contiguous(), "k_cache must be contiguous")
+    _check(k_cache.dim() == 4, "k_cache must be [batch, heads, seq, head_dim]")
+    _check(k_cache.dtype in _FLOATING, f"unsupported dtype {k_cache.dtype}")
+    _check(chunk_size > 0, "chunk_size must be positive")
+    B, H, S, D = k_cache.shape
+    C = S // chunk_size
+    if num_chunks is None:
+        num_chunks = C - chunk_begin
+    with torch.cuda.device(k_cache.device):
+        if out is None:
+            out = torch.empty((B, H, C, D), dtype=torch.float32, device=k_cache.device)
+        _check(out.is_cuda and out.is_contiguous() and out.dtype == torch.float32 and out.dim() == 4
+               and tuple(out.shape[:2]) == (B, H) and out.shape[3] == D,
+               "summary must be a contiguous fp32 [batch, heads, chunks, head_dim] CUDA tensor")
+        _rc(lib().csahca_csa_chunk_summary(_ptr(k_cache), _ptr(out), _DTYPES[k_cache.dtype], B, H, S, D,
+                                           chunk_size, out.shape[2], int(chunk_begin), int(num_chunks),
+                                           _stream()))
+    return out
+
+
+def csa_select_topk(q, summary, top_k):
+    """Top-k chunk ids by q . summary / sqrt(D) (select_topk_chunks scoring,
+    hybrid_attention/reference.py:51-56).  int32 ``[B, H, min(top_k, C)]``, best
+    first; equal scores are ordered by ascending chunk id."""
+    top_k = int(top_k)
+    _check(q.is_cuda and summary.is_cuda, "q and summary must be CUDA tensors")
+    _check(q.is_contiguous() and summary.is_contiguous(), "q and summary must be contiguous")
+    _check(q.dim() == 3, "q must be [batch, heads, head_dim]")
+    _check(summary.dim() == 4 and summary.dtype == torch.float32,
+           "summary must be fp32 [batch, heads, chunks, head_dim]")
+    B, H, D = q.shape
+    _check(tuple(summary.shape[:2]) == (B, H) and summary.shape[3] == D, "summary shape must match q")
+    _check(q.dtype in _FLOATING, f"unsupported dtype {q.dtype}")
+    _check(top_k >= 0, "top_k must be non-negative")
+    C = summary.shape[2]
+    k = min(top_k, C)
+    with torch.cuda.device(q.device):
+        out = torch.empty((B, H, k), dtype=torch.int32, device=q.device)
+        ws = _workspace(lib().csahca_csa_select_workspace_bytes(B, H, C), q.device)
+        _rc(lib().csahca_csa_select_topk(_ptr(q), _ptr(summary), _ptr(out), _DTYPES[q.dtype], B, H, C, D,
+                                         top_k, _ptr(ws), ws.numel(), _stream()))
+    return out
+
+
+def csa_decode_step(q, k_cache, v_cache, summary, chunk_size, top_k, tile_size: int = 0):
+    """One CSA decode step from cached summaries: select the top-k chunks, then
+    attend over their tokens.  Returns ``(out, chunk_indices)``."""
+    idx = csa_select_topk(q, summary, top_k)
+    B, H, _ = q.shape
+    ts = int(tile_size) if tile_size and tile_size > 0 else csa_auto_tile_size(B, H, idx.shape[-1], chunk_size)
+    return csa_decode_forward_tiled(q, k_cache, v_cache, idx, chunk_size, ts), idx
+
+
+# ---------------------------------------------------------------------------
+# DSV4
+# ---------------------------------------------------------------------------
+_DSV4_HEAD_DIM = 512
+
+
+def _dsv4_common(q, cache, token_indices, topk_lengths, attn_sink, page_size, allow_empty: bool):
+    _check(_defined(topk_lengths) is False or topk_lengths.is_cuda, "topk_lengths must be CUDA when defined")
+    _check(_defined(attn_sink) is False or attn_sink.is_cuda, "attn_sink must be CUDA when defined")
+    _check(q.is_contiguous(), "q must be contiguous")
+    _check(cache.is_contiguous(), "paged_k_cache_u8 must be contiguous")
+    _check(token_indices.is_contiguous(), "token_indices must be contiguous")
+    _check(not _defined(topk_lengths) or topk_lengths.is_contiguous(), "topk_lengths must be contiguous")
+    _check(not _defined(attn_sink) or attn_sink.is_contiguous(), "attn_sink must be contiguous")
+    _check(q.dim() == 3, "q must be [num_queries, heads, 512]")
+    _check(q.shape[2] == _DSV4_HEAD_DIM, "q head_dim must be 512 for DSV4")
+    _check(cache.dim() == 2, "paged_k_cache_u8 must be [num_pages, bytes_per_page]")
+    _check(cache.dtype == torch.uint8, "paged_k_cache_u8 must be uint8")
+    _check(token_indices.dim() == 2, "token_indices must be [num_queries, topk_slots]")
+    _check(token_indices.dtype == torch.int32, "token_indices must be int32")
+    _check(not _defined(topk_lengths) or topk_lengths.dtype == torch.int32, "topk_lengths must be int32 when defined")
+    _check(not _defined(attn_sink) or attn_sink.dtype == torch.float32, "attn_sink must be float32 when defined")
+    _check(page_size > 0, "page_size must be positive")
+    _check(q.dtype in _FLOATING, f"unsupported dtype {q.dtype}")
+    nq, heads = q.shape[0], q.shape[1]
+    _check(token_indices.shape[0] == nq, "token_indices query dimension must match q")
+    # None and empty tensors both mean "absent" on every route (the reference's
+    # untiled ops reject the empty tensors its own wrappers pass for None).
+    _check(not _present(topk_lengths) or topk_lengths.numel() == nq, "topk_lengths must have one value per query")
+    _check(not _present(attn_sink) or attn_sink.numel() == heads, "attn_sink must have one value per head")
+    bpp = cache.shape[1]
+    _check(bpp >= page_size * (576 + 8), "bytes_per_page is too small for DSV4 page layout")
+
+
+def _dsv4_extra_checks(extra_cache, extra_token_indices, extra_topk_lengths, nq):
+    _check(extra_cache.is_cuda, "extra_paged_k_cache_u8 must be CUDA")
+    _check(extra_token_indices.is_cuda, "extra_token_indices must be CUDA")
+    _check(not _defined(extra_topk_lengths) or extra_topk_lengths.is_cuda,
+           "extra_topk_lengths must be CUDA when defined")
+    _check(extra_cache.is_contiguous(), "extra_paged_k_cache_u8 must be contiguous")
+    _check(extra_token_indices.is_contiguous(), "extra_token_indices must be contiguous")
+    _check(not _defined(extra_topk_lengths) or extra_topk_lengths.is_contiguous(),
+           "extra_topk_lengths must be contiguous")
+    _check(extra_cache.dim() == 2, "extra_paged_k_cache_u8 must be [num_pages, bytes_per_page]")
+    _check(extra_cache.dtype == torch.uint8, "extra_paged_k_cache_u8 must be uint8")
+    _check(extra_token_indices.dim() == 2, "extra_token_indices must be [num_queries, extra_topk_slots]")
+    _check(extra_token_indices.dtype == torch.int32, "extra_token_indices must be int32")
+    _check(not _present(extra_topk_lengths) or extra_topk_lengths.dtype == torch.int32,
+           "extra_topk_lengths must be int32 when defined")
+    _check(extra_token_indices.shape[0] == nq, "extra_token_indices query dimension must match q")
+    _check(not _present(extra_topk_lengths) or extra_topk_lengths.numel() == nq,
+           "extra_topk_lengths must have one value per query")
+
+
+def _opt(t):
+    return t if _present(t) else None
+
+
+def dsv4_decode_forward_tiled(q, paged_k_cache_u8, token_indices, topk_lengths, extra_paged_k_cache_u8,
+                              extra_token_indices, extra_topk_lengths, attn_sink, page_size, extra_page_size,
+                              tile_size, softmax_scale):
+    """Reference op dsv4_decode_forward_tiled (tile_size 0 = automatic)."""
+    page_size, extra_page_size, tile_size = int(page_size), int(extra_page_size), int(tile_size)
+    if not (q.is_cuda and paged_k_cache_u8.is_cuda and token_indices.is_cuda):
+        raise RuntimeError("q, paged_k_cache_u8, and token_indices must be CUDA tensors")
+    _dsv4_common(q, paged_k_cache_u8, token_indices, topk_lengths, attn_sink, page_size, allow_empty=True)
+    _check(paged_k_cache_u8.shape[1] % 4 == 0,
+           "tiled DSV4 kernel requires bytes_per_page divisible by 4 for vectorized loads")
+    nq, heads = q.shape[0], q.shape[1]
+    has_extra = (_defined(extra_paged_k_cache_u8) and extra_paged_k_cache_u8.numel() > 0
+                 and _defined(extra_token_indices) and extra_token_indices.numel() > 0)
+    extra_slots = 0
+    if has_extra:
+        _dsv4_extra_checks(extra_paged_k_cache_u8, extra_token_indices, extra_topk_lengths, nq)
+        _check(extra_page_size > 0, "extra_page_size must be positive")
+        ebpp = extra_paged_k_cache_u8.shape[1]
+        _check(ebpp >= extra_page_size * (576 + 8), "extra_bytes_per_page is too small for DSV4 page layout")
+        _check(ebpp % 4 == 0,
+               "tiled DSV4 kernel requires extra_bytes_per_page divisible by 4 for vectorized loads")
+        extra_slots = extra_token_indices.shape[1]
+    with torch.cuda.device(q.device):
+        out = torch.empty_like(q)
+        if nq == 0 or heads == 0:
+            return out
+        ws = _workspace(lib().csahca_dsv4_decode_workspace_bytes(nq, heads, token_indices.shape[1], extra_slots,
+                                                                  tile_size), q.device)
+        ec = extra_paged_k_cache_u8 if has_extra else None
+        _rc(lib().csahca_dsv4_decode_forward_tiled(
+            _ptr(q), _DTYPES[q.dtype], nq, heads, _ptr(paged_k_cache_u8), paged_k_cache_u8.shape[0],
+            paged_k_cache_u8.shape[1], page_size, _ptr(token_indices), token_indices.shape[1],
+            _ptr(_opt(topk_lengths)), _ptr(ec), ec.shape[0] if has_extra else 0,
+            ec.shape[1] if has_extra else 0, extra_page_size if has_extra else 1,
+            _ptr(extra_token_indices) if has_extra else None, extra_slots,
+            _ptr(_opt(extra_topk_lengths)) if has_extra else None, _ptr(_opt(attn_sink)), float(softmax_scale),
+            tile_size, _ptr(out), _ptr(ws), ws.numel(), _stream()))
+    return out
+
+
+def dsv4_swa_decode_forward(q, paged_k_cache_u8, token_indices, topk_lengths, attn_sink, page_size,
+                            softmax_scale):
+    """Reference op dsv4_swa_decode_forward (SWA slots only)."""
+    page_size = int(page_size)
+    if not (q.is_cuda and paged_k_cache_u8.is_cuda and token_indices.is_cuda):
+        raise RuntimeError("q, paged_k_cache_u8, and token_indices must be CUDA tensors")
+    _dsv4_common(q, paged_k_cache_u8, token_indices, topk_lengths, attn_sink, page_size, allow_empty=True)
+    nq, heads = q.shape[0], q.shape[1]
+    with torch.cuda.device(q.device):
+        out = torch.empty_like(q)
+        if nq == 0 or heads == 0:
+            return out
+        ws = _workspace(lib().csahca_dsv4_decode_workspace_bytes(nq, heads, token_indices.shape[1], 0, 0), q.device)
+        _rc(lib().csahca_dsv4_swa_decode_forward(
+            _ptr(q), _DTYPES[q.dtype], nq, heads, _ptr(paged_k_cache_u8), paged_k_cache_u8.shape[0],
+            paged_k_cache_u8.shape[1], page_size, _ptr(token_indices), token_indices.shape[1],
+            _ptr(_opt(topk_lengths)), _ptr(_opt(attn_sink)), float(softmax_scale), _ptr(out), _ptr(ws),
+            ws.numel(), _stream()))
+    return out
+
+
+def dsv4_sparse_decode_forward(q, paged_k_cache_u8, token_indices, topk_lengths, extra_paged_k_cache_u8,
+                               extra_token_indices, extra_topk_lengths, attn_sink, page_size, extra_page_size,
+                               softmax_scale):
+    """Reference op dsv4_sparse_decode_forward (SWA + C4/C128 extra slots)."""
+    page_size, extra_page_size = int(page_size), int(extra_page_size)
+    if not (q.is_cuda and paged_k_cache_u8.is_cuda and token_indices.is_cuda
+            and extra_paged_k_cache_u8.is_cuda and extra_token_indices.is_cuda):
+        raise RuntimeError("q, paged_k_cache_u8, token_indices, extra_paged_k_cache_u8, and extra_token_indices "
+                           "must be CUDA tensors")
+    _dsv4_common(q, paged_k_cache_u8, token_indices, topk_lengths, attn_sink, page_size, allow_empty=True)
+    nq, heads = q.shape[0], q.shape[1]
+    _dsv4_extra_checks(extra_paged_k_cache_u8, extra_token_indices, extra_topk_lengths, nq)
+    _check(extra_page_size > 0, "extra_page_size must be positive")
+    _check(extra_paged_k_cache_u8.shape[1] >= extra_page_size * (576 + 8),
+           "extra_bytes_per_page is too small for DSV4 page layout")
+    with torch.cuda.device(q.device):
+        out = torch.empty_like(q)
+        if nq == 0 or heads == 0:
+            return out
+        ws = _workspace(lib().csahca_dsv4_decode_workspace_bytes(nq, heads, token_indices.shape[1],
+                                                                  extra_token_indices.shape[1], 0), q.device)
+        _rc(lib().csahca_dsv4_sparse_decode_forward(
+            _ptr(q), _DTYPES[q.dtype], nq, heads, _ptr(paged_k_cache_u8), paged_k_cache_u8.shape[0],
+            paged_k_cache_u8.shape[1], page_size, _ptr(token_indices), token_indices.shape[1],
+            _ptr(_opt(topk_lengths)), _ptr(extra_paged_k_cache_u8), extra_paged_k_cache_u8.shape[0],
+            extra_paged_k_cache_u8.shape[1], extra_page_size, _ptr(extra_token_indices),
+            extra_token_indices.shape[1], _ptr(_opt(extra_topk_lengths)), _ptr(_opt(attn_sink)),
+            float(softmax_scale), _ptr(out), _ptr(ws), ws.numel(), _stream()))
+    return out

@@ -143,3 +143,67 @@ def make_dsv4_case(*, compress_ratio: int, num_queries: int = 7, heads: int = 8,
         if t is not None:
             setattr(case, name, t.to(device))
     return case
+
+
+def make_dsv4_window_case(*, compress_ratio: int, num_queries: int, heads: int, context: int = 65536,
+                          page_size: int = 64, window: int = 128, extra_top_k: int = 64,
+                          extra_page_size: int | None = None, q_dtype: torch.dtype = torch.bfloat16,
+                          seed: int = 0, device: str | torch.device = "cpu") -> Dsv4Case:
+    """A serving-shaped DSV4 decode workload (BASELINE configs 4 and 5).
+
+    ``context`` latent rows are stored in pages of ``page_size`` whose physical
+    order is a seeded random permutation (the page table).  Query ``i`` attends
+    the ``window`` most recent tokens ending at logical position
+    ``context - 1 - i`` (SWA slots), plus -- for compress_ratio 4 / 128 --
+    ``extra_top_k`` distinct compressed entries drawn at random from the
+    ``context // compress_ratio`` entries its position can see, stored in their
+    own permuted pages of ``extra_page_size`` (default ``page_size //
+    compress_ratio``, at least 1).  All lengths are full.  Draw order: q, SWA
+    rows, SWA page permutation, sink, then extra rows, extra permutation and the
+    per-query extra selections.
+    """
+    if context % page_size:
+        raise ValueError("context must be a multiple of page_size")
+    g = torch.Generator(device="cpu")
+    g.manual_seed(seed)
+    q = torch.randn(num_queries, heads, HEAD_DIM, dtype=q_dtype, generator=g)
+    rows = torch.randn(context, HEAD_DIM, dtype=torch.bfloat16, generator=g)
+    pages = context // page_size
+    perm = torch.randperm(pages, generator=g)
+    sink = torch.randn(heads, dtype=torch.float32, generator=g)
+    phys = torch.empty_like(rows)
+    phys.view(pages, page_size, HEAD_DIM)[perm] = rows.view(pages, page_size, HEAD_DIM)
+    end = context - 1 - torch.arange(num_queries)
+    pos = end[:, None] - torch.arange(window - 1, -1, -1)[None, :]
+    pos = pos.clamp_min(0)
+    token_indices = (perm[pos // page_size] * page_size + pos % page_size).to(torch.int32)
+    lengths = torch.full((num_queries,), window, dtype=torch.int32)
+    case = Dsv4Case(q=q, k_tokens=phys, cache=None, token_indices=token_indices, topk_lengths=lengths,
+                    attn_sink=sink, page_size=page_size)
+    if compress_ratio:
+        eps = extra_page_size if extra_page_size is not None else max(1, page_size // compress_ratio)
+        n_extra = context // compress_ratio
+        if n_extra % eps:
+            raise ValueError("compressed entries must fill whole pages")
+        erows = torch.randn(n_extra, HEAD_DIM, dtype=torch.bfloat16, generator=g)
+        epages = n_extra // eps
+        eperm = torch.randperm(epages, generator=g)
+        ephys = torch.empty_like(erows)
+        ephys.view(epages, eps, HEAD_DIM)[eperm] = erows.view(epages, eps, HEAD_DIM)
+        sel = torch.empty((num_queries, extra_top_k), dtype=torch.int64)
+        for i in range(num_queries):
+            visible = max(extra_top_k, (int(end[i]) + 1) // compress_ratio)
+            sel[i] = torch.randperm(visible, generator=g)[:extra_top_k]
+        case.extra_tokens = ephys
+        case.extra_token_indices = (eperm[sel // eps] * eps + sel % eps).to(torch.int32)
+        case.extra_topk_lengths = torch.full((num_queries,), extra_top_k, dtype=torch.int32)
+        case.extra_page_size = eps
+    case.cache = pack_dsv4_cache(case.k_tokens.to(device), page_size=page_size)
+    if compress_ratio:
+        case.extra_cache = pack_dsv4_cache(case.extra_tokens.to(device), page_size=case.extra_page_size)
+    for name in ("q", "k_tokens", "token_indices", "topk_lengths", "attn_sink", "extra_tokens",
+                 "extra_token_indices", "extra_topk_lengths"):
+        t = getattr(case, name)
+        if t is not None:
+            setattr(case, name, t.to(device))
+    return case

@@ -1,0 +1,166 @@
+/*
+ * csahca.h -- C ABI of libcsahca.so, the MI355X (gfx950) compressed-sparse-attention
+ * decode library.
+ *
+ * This is the drop-in boundary for the CSAHCA reference's native op surface
+ * (module hybrid_attention_cuda: csrc/bindings.cpp:54-163, bound from Python in
+ * hybrid_attention/extension.py:13-197).  Every entry point takes plain device
+ * pointers, sizes and a HIP stream, returns a status code, and never allocates:
+ * scratch space comes from the caller through `workspace` (size from the
+ * matching *_workspace_bytes function; contents need no initialisation).
+ * No HIP or torch type appears in a signature: `stream` is a hipStream_t passed
+ * as void* (NULL = the null stream).
+ *
+ * Errors: a non-zero status; csahca_last_error() then returns the message of
+ * the last failing call on the calling thread.  Argument errors carry the
+ * reference's TORCH_CHECK texts and are detected on the host before any HIP
+ * call, so they can be exercised without a GPU.
+ *
+ * Layouts (all row-major, contiguous):
+ *   CSA:  q [batch, heads, head_dim]; k_cache, v_cache [batch, heads, seq_len,
+ *         head_dim]; chunk_indices [batch, heads, top_k]; out like q;
+ *         chunk summaries fp32 [batch, heads, num_chunks, head_dim].
+ *   DSV4: q [num_queries, heads, 512]; caches are byte arrays [num_pages,
+ *         bytes_per_page] in the DSV4 paged FP8 layout (448 e4m3 + 64 bf16 per
+ *         token row, per-64 UE8M0 scale bytes after the rows of a page);
+ *         token indices int32 [num_queries, slots]; lengths int32 [num_queries]
+ *         or NULL; attn_sink fp32 [heads] or NULL; out like q.
+ */
+#ifndef CSAHCA_H_
+#define CSAHCA_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Storage type of q / K / V / out (the reference dispatches over f32, f64, f16
+ * and bf16: AT_DISPATCH_FLOATING_TYPES_AND2, csa_attention.cu:368-383). */
+enum csahca_dtype { CSAHCA_F32 = 0, CSAHCA_F16 = 1, CSAHCA_BF16 = 2, CSAHCA_F64 = 3 };
+
+/* Chunk-index type (int32 or int64: csa_attention.cu:350-351). */
+enum csahca_index_dtype { CSAHCA_I32 = 0, CSAHCA_I64 = 1 };
+
+enum csahca_status {
+  CSAHCA_OK = 0,
+  CSAHCA_ERR_ARGUMENT = 1,  /* invalid argument (reference TORCH_CHECK failure) */
+  CSAHCA_ERR_WORKSPACE = 2, /* workspace NULL or smaller than *_workspace_bytes */
+  CSAHCA_ERR_HIP = 3        /* HIP runtime or launch error */
+};
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* csahca_last_error(void);
+
+/* ABI revision of this header (bumped on incompatible changes). */
+int csahca_abi_version(void);
+
+/* ------------------------------------------------------------------------- */
+/* CSA: sparse decode over explicit chunk ids                                 */
+/* ------------------------------------------------------------------------- */
+
+/* Workspace for csahca_csa_decode_forward(_tiled): fp32 split-KV partials.
+ * tile_size <= 0 selects the size the untiled op uses. */
+size_t csahca_csa_decode_workspace_bytes(int64_t batch, int64_t heads, int64_t head_dim,
+                                         int64_t top_k, int64_t chunk_size, int64_t tile_size);
+
+/* Replaces csa_decode_forward_cuda (csrc/csa_attention.cu:330-385; pybind op
+ * csa_decode_forward, bindings.cpp:54-64).  out[b,h] = softmax over the tokens
+ * of the chunks chunk_indices[b,h,:] (ids < 0 skipped, tokens >= seq_len
+ * skipped) of q.k/sqrt(head_dim), applied to V; 0 when no token is valid.
+ * head_dim <= 1024, chunk_size > 0. */
+int csahca_csa_decode_forward(const void* q, const void* k_cache, const void* v_cache,
+                              const void* chunk_indices, void* out, int dtype, int index_dtype,
+                              int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
+                              int64_t top_k, int64_t chunk_size, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
+/* Replaces csa_decode_forward_tiled_cuda (csrc/csa_attention.cu:387-452; pybind
+ * op csa_decode_forward_tiled, bindings.cpp:66-77).  Same result; tile_size (> 0)
+ * is the number of selected-token slots per split-KV work item. */
+int csahca_csa_decode_forward_tiled(const void* q, const void* k_cache, const void* v_cache,
+                                    const void* chunk_indices, void* out, int dtype,
+                                    int index_dtype, int64_t batch, int64_t heads,
+                                    int64_t seq_len, int64_t head_dim, int64_t top_k,
+                                    int64_t chunk_size, int64_t tile_size, void* workspace,
+                                    size_t workspace_bytes, void* stream);
+
+/* Split size the library picks for a CSA decode of this shape (>= 1). */
+int64_t csahca_csa_auto_tile_size(int64_t batch, int64_t heads, int64_t top_k,
+                                  int64_t chunk_size);
+
+/* Chunk summaries: replaces chunk_mean (hybrid_attention/reference.py:40-45).
+ * summary[b,h,c] = mean of rows c*chunk_size .. c*chunk_size+chunk_size-1 of
+ * k_cache[b,h], in fp32, for c in [chunk_begin, chunk_begin + num_chunks).
+ * Only complete chunks may be requested ((chunk_begin+num_chunks)*chunk_size
+ * <= seq_len); summary holds summary_chunks >= chunk_begin+num_chunks rows per
+ * head.  Recomputing one chunk is the incremental update for a growing cache. */
+int csahca_csa_chunk_summary(const void* k_cache, float* summary, int dtype, int64_t batch,
+                             int64_t heads, int64_t seq_len, int64_t head_dim,
+                             int64_t chunk_size, int64_t summary_chunks, int64_t chunk_begin,
+                             int64_t num_chunks, void* stream);
+
+/* Workspace for csahca_csa_select_topk: the fp32 chunk scores. */
+size_t csahca_csa_select_workspace_bytes(int64_t batch, int64_t heads, int64_t num_chunks);
+
+/* Chunk selection: replaces the scoring + torch.topk of select_topk_chunks
+ * (hybrid_attention/reference.py:48-56).  score[c] = (q . summary[c]) * 1/sqrt(D)
+ * in fp32; out_indices[b,h,:] (int32, min(top_k, num_chunks) per head) lists the
+ * best chunks by descending score, equal scores by ascending chunk id. */
+int csahca_csa_select_topk(const void* q, const float* summary, int32_t* out_indices, int dtype,
+                           int64_t batch, int64_t heads, int64_t num_chunks, int64_t head_dim,
+                           int64_t top_k, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------- */
+/* DSV4: MQA decode over the paged FP8 latent cache                           */
+/* ------------------------------------------------------------------------- */
+
+/* Workspace for the DSV4 entry points (fp32 split partials).  tile_size <= 0
+ * means automatic tiling. */
+size_t csahca_dsv4_decode_workspace_bytes(int64_t num_queries, int64_t heads, int64_t topk_slots,
+                                          int64_t extra_topk_slots, int64_t tile_size);
+
+/* Replaces dsv4_decode_forward_tiled_cuda (csrc/dsv4_attention.cu:762-909;
+ * pybind op dsv4_decode_forward_tiled, bindings.cpp:127-155).  For query i and
+ * head h: softmax over {sink[h] (value 0)} + the valid SWA slots (first
+ * clamp(topk_lengths[i], 0, topk_slots), ids >= 0) + the valid extra slots, of
+ * q.k * softmax_scale, applied to the dequantised rows (V = K).  extra_cache may
+ * be NULL (no extra slots).  tile_size 0 = automatic.  Locations on pages at or
+ * beyond num_pages are skipped. */
+int csahca_dsv4_decode_forward_tiled(
+    const void* q, int dtype, int64_t num_queries, int64_t heads, const uint8_t* cache,
+    int64_t num_pages, int64_t bytes_per_page, int64_t page_size, const int32_t* token_indices,
+    int64_t topk_slots, const int32_t* topk_lengths, const uint8_t* extra_cache,
+    int64_t extra_num_pages, int64_t extra_bytes_per_page, int64_t extra_page_size,
+    const int32_t* extra_token_indices, int64_t extra_topk_slots,
+    const int32_t* extra_topk_lengths, const float* attn_sink, double softmax_scale,
+    int64_t tile_size, void* out, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Replaces dsv4_swa_decode_forward_cuda (csrc/dsv4_attention.cu:585-657; pybind
+ * op dsv4_swa_decode_forward, bindings.cpp:79-92): SWA slots only. */
+int csahca_dsv4_swa_decode_forward(const void* q, int dtype, int64_t num_queries, int64_t heads,
+                                   const uint8_t* cache, int64_t num_pages,
+                                   int64_t bytes_per_page, int64_t page_size,
+                                   const int32_t* token_indices, int64_t topk_slots,
+                                   const int32_t* topk_lengths, const float* attn_sink,
+                                   double softmax_scale, void* out, void* workspace,
+                                   size_t workspace_bytes, void* stream);
+
+/* Replaces dsv4_sparse_decode_forward_cuda (csrc/dsv4_attention.cu:659-760;
+ * pybind op dsv4_sparse_decode_forward, bindings.cpp:94-125): SWA + extra
+ * (C4/C128) slots, extra cache required. */
+int csahca_dsv4_sparse_decode_forward(
+    const void* q, int dtype, int64_t num_queries, int64_t heads, const uint8_t* cache,
+    int64_t num_pages, int64_t bytes_per_page, int64_t page_size, const int32_t* token_indices,
+    int64_t topk_slots, const int32_t* topk_lengths, const uint8_t* extra_cache,
+    int64_t extra_num_pages, int64_t extra_bytes_per_page, int64_t extra_page_size,
+    const int32_t* extra_token_indices, int64_t extra_topk_slots,
+    const int32_t* extra_topk_lengths, const float* attn_sink, double softmax_scale, void* out,
+    void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CSAHCA_H_ */

@@ -1,0 +1,133 @@
+"""CPU-only checks of the C ABI and the torch binding: the library loads, exports
+every symbol include/csahca.h declares, and rejects bad arguments on the host
+with the reference's messages -- before any HIP call, so no GPU is needed."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from csahca_amd import extension, native
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def header_symbols():
+    text = (ROOT / "include" / "csahca.h").read_text()
+    return sorted(set(re.findall(r"\b(csahca_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not native.library_path().exists():
+        pytest.fail("libcsahca.so is not built (run python -m csahca_amd.build)")
+    return native.lib()
+
+
+def test_exports_every_header_symbol(lib):
+    syms = header_symbols()
+    assert len(syms) >= 13
+    raw = ctypes.CDLL(str(native.library_path()))
+    for s in syms:
+        assert hasattr(raw, s), s
+    assert set(syms) == set(native.EXPORTED)
+    assert lib.csahca_abi_version() == 1
+
+
+def test_workspace_sizes(lib):
+    # B1 H8 D128 k8 chunk64 tile8: 64 tiles per head -> 8*64*(2 + 128) floats (+ alignment)
+    n = lib.csahca_csa_decode_workspace_bytes(1, 8, 128, 8, 64, 8)
+    assert n >= 8 * 64 * 130 * 4
+    assert lib.csahca_csa_select_workspace_bytes(1, 8, 512) == 8 * 512 * 4
+    assert lib.csahca_dsv4_decode_workspace_bytes(1, 8, 128, 64, 0) > 0
+    assert lib.csahca_csa_auto_tile_size(1, 8, 8, 64) >= 16
+
+
+def _csa_call(lib, **over):
+    args = dict(q=1, k=1, v=1, idx=1, out=1, dtype=2, index_dtype=0, B=1, H=1, S=64, D=128, top_k=1, chunk=64,
+                tile=8, ws=None, wsb=0)
+    args.update(over)
+    return lib.csahca_csa_decode_forward_tiled(args["q"], args["k"], args["v"], args["idx"], args["out"],
+                                               args["dtype"], args["index_dtype"], args["B"], args["H"], args["S"],
+                                               args["D"], args["top_k"], args["chunk"], args["tile"], args["ws"],
+                                               args["wsb"], None)
+
+
+def test_csa_argument_errors_before_any_launch(lib):
+    assert _csa_call(lib, chunk=0) == 1
+    assert lib.csahca_last_error().decode() == "chunk_size must be positive"
+    assert _csa_call(lib, tile=0) == 1
+    assert lib.csahca_last_error().decode() == "tile_size must be positive"
+    assert _csa_call(lib, D=2048) == 1
+    assert "head_dim > 1024" in lib.csahca_last_error().decode()
+    assert _csa_call(lib, dtype=9) == 1
+    assert _csa_call(lib, index_dtype=5) == 1
+    assert lib.csahca_last_error().decode() == "chunk_indices must be int32 or int64"
+    # missing workspace is reported, not dereferenced
+    assert _csa_call(lib) == 2
+    # empty problems succeed without touching memory
+    assert _csa_call(lib, B=0) == 0
+
+
+def test_dsv4_argument_errors(lib):
+    f = lib.csahca_dsv4_decode_forward_tiled
+    common = dict(q=1, dtype=2, nq=1, heads=8, cache=1, pages=1, bpp=37440, ps=64, idx=1, slots=4, lens=None,
+                  ecache=None, epages=0, ebpp=0, eps=1, eidx=None, eslots=0, elens=None, sink=None, scale=0.04,
+                  tile=0, out=1, ws=None, wsb=0)
+
+    def call(**o):
+        a = dict(common)
+        a.update(o)
+        return f(a["q"], a["dtype"], a["nq"], a["heads"], a["cache"], a["pages"], a["bpp"], a["ps"], a["idx"],
+                 a["slots"], a["lens"], a["ecache"], a["epages"], a["ebpp"], a["eps"], a["eidx"], a["eslots"],
+                 a["elens"], a["sink"], a["scale"], a["tile"], a["out"], a["ws"], a["wsb"], None)
+
+    assert call(ps=0) == 1 and lib.csahca_last_error().decode() == "page_size must be positive"
+    assert call(bpp=1000) == 1
+    assert lib.csahca_last_error().decode() == "bytes_per_page is too small for DSV4 page layout"
+    assert call(bpp=37442) == 1
+    assert "divisible by 4" in lib.csahca_last_error().decode()
+    assert call(ecache=1, epages=4, ebpp=9792, eps=0, eidx=1, eslots=8) == 1
+    assert lib.csahca_last_error().decode() == "extra_page_size must be positive"
+    assert call(ecache=1, epages=4, ebpp=100, eps=16, eidx=1, eslots=8) == 1
+    assert lib.csahca_last_error().decode() == "extra_bytes_per_page is too small for DSV4 page layout"
+    assert call() == 2  # valid arguments, no workspace
+    assert call(nq=0) == 0
+    g = lib.csahca_dsv4_sparse_decode_forward
+    rc = g(1, 2, 1, 8, 1, 1, 37440, 64, 1, 4, None, 1, 1, 9792, 0, 1, 8, None, None, 0.04, 1, None, 0, None)
+    assert rc == 1 and lib.csahca_last_error().decode() == "extra_page_size must be positive"
+
+
+def test_binding_rejects_cpu_tensors_with_reference_messages(lib):
+    q = torch.zeros(1, 2, 64, dtype=torch.bfloat16)
+    k = torch.zeros(1, 2, 128, 64, dtype=torch.bfloat16)
+    idx = torch.zeros(1, 2, 2, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="all tensors must be CUDA tensors"):
+        native.csa_decode_forward(q, k, k, idx, 64)
+    with pytest.raises(RuntimeError, match="all tensors must be CUDA tensors"):
+        extension.csa_decode_forward_tiled(q, k, k, idx, 64)
+    cache = torch.zeros(1, 37440, dtype=torch.uint8)
+    tok = torch.zeros(1, 4, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="q, paged_k_cache_u8, and token_indices must be CUDA tensors"):
+        extension.dsv4_swa_decode_forward(torch.zeros(1, 8, 512), cache, tok, None, None, 64, 0.04)
+    with pytest.raises(RuntimeError, match="extra_token_indices must be CUDA tensors"):
+        native.dsv4_sparse_decode_forward(torch.zeros(1, 8, 512), cache, tok, None, cache, tok, None, None, 64, 1,
+                                          0.04)
+
+
+def test_extension_env_flags(monkeypatch):
+    monkeypatch.setenv("CSAHCA_DSV4_TILE_SIZE", "17")
+    assert extension._dsv4_tile_size() == 17
+    monkeypatch.setenv("CSAHCA_DSV4_TILE_SIZE", "x")
+    assert extension._dsv4_tile_size() == 0
+    monkeypatch.setenv("CSAHCA_DSV4_TILED", "off")
+    assert extension._dsv4_tiled_enabled(native) is False
+    monkeypatch.setenv("CSAHCA_DSV4_TILED", "1")
+    assert extension._dsv4_tiled_enabled(native) is True
+
+
+def test_product_package_does_not_import_oracle():
+    for p in (ROOT / "csahca_amd").rglob("*.py"):
+        text = p.read_text()
+        assert "import oracle" not in text and "from oracle" not in text, p

@@ -1,0 +1,274 @@
+"""GPU parity of the CSA kernels against the CPU oracle (and golden vectors).
+
+Tolerances: outputs |got - ref| <= 2e-2 + 1e-2 |ref| for
+16-bit storage (1e-4 + 1e-4 |ref| for fp32/fp64 storage); selected chunk ids
+bit-exact under the declared tie-break (score desc, chunk id asc), where a
+mismatch is accepted only between chunks whose oracle scores agree to 1e-5
+(fp32 summation-order noise).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from csahca_amd import extension, native
+from csahca_amd.synthetic import clustered_chunks, make_synthetic_case, plant_chunks, scattered_chunks
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.fail("no HIP device visible")
+    native.lib()
+
+
+def tol_for(dtype):
+    return (2e-2, 1e-2) if dtype in (torch.bfloat16, torch.float16) else (1e-4, 1e-4)
+
+
+def assert_close(got: torch.Tensor, ref: np.ndarray, atol: float, rtol: float, what: str = ""):
+    g = got.detach().float().cpu().numpy().astype(np.float64)
+    assert g.shape == ref.shape, (g.shape, ref.shape)
+    diff = np.abs(g - ref)
+    bad = diff > atol + rtol * np.abs(ref)
+    assert not bad.any(), f"{what} max_abs={diff.max():.3e} bad={int(bad.sum())}/{bad.size}"
+
+
+def assert_indices(got: torch.Tensor, want: np.ndarray, scores: np.ndarray, eps: float = 1e-5):
+    g = got.cpu().numpy()
+    assert g.shape == want.shape
+    if np.array_equal(g, want):
+        return
+    B, H, k = want.shape
+    for b in range(B):
+        for h in range(H):
+            if np.array_equal(g[b, h], want[b, h]):
+                continue
+            assert len(set(g[b, h].tolist())) == k
+            s = scores[b, h]
+            for j in range(k):
+                a, w = s[g[b, h, j]], s[want[b, h, j]]
+                assert abs(a - w) <= eps * max(1.0, abs(w)), (b, h, j, g[b, h], want[b, h])
+
+
+def run_tiled(case, idx, tile):
+    return extension.csa_decode_forward_tiled(case.q.to(DEV), case.k_cache.to(DEV), case.v_cache.to(DEV),
+                                              idx.to(DEV), case.chunk_size, tile)
+
+
+# ---------------------------------------------------------------------------
+
+def test_headline_decode_step():
+    """B1 H8 S32768 D128 chunk64 k8 bf16: summaries, selection, attention."""
+    case = make_synthetic_case(batch=1, heads=8, seq_len=32768, head_dim=128, chunk_size=64, top_k=8, seed=0)
+    q, k, v = case.q.to(DEV), case.k_cache.to(DEV), case.v_cache.to(DEV)
+    summ = extension.csa_chunk_summary(k, 64)
+    summ_ref = oracle.chunk_mean(case.k_cache, 64)
+    np.testing.assert_allclose(summ.cpu().numpy(), summ_ref, rtol=0, atol=2e-6)
+    idx = extension.csa_select_topk(q, summ, 8)
+    want, scores = oracle.select_topk(case.q, summ_ref, 8)
+    assert_indices(idx, want, scores)
+    ref32 = oracle.csa_attend(case.q, case.k_cache, case.v_cache, want, 64, prob_dtype=oracle.F32)
+    ref_torch_csa = oracle.csa_reference(case.q, case.k_cache, case.v_cache, chunk_size=64, top_k=8,
+                                         selected_chunks=want, dtype=torch.bfloat16)
+    for tile in (8, 16, 64, native.csa_auto_tile_size(1, 8, 8, 64)):
+        out = extension.csa_decode_forward_tiled(q, k, v, idx, 64, tile)
+        assert_close(out, ref32, 2e-2, 1e-2, f"tile={tile}")
+        assert_close(out, ref_torch_csa, 2e-2, 1e-2, f"vs torch-csa tile={tile}")
+    out, idx2 = native.csa_decode_step(q, k, v, summ, 64, 8)
+    assert torch.equal(idx2, idx)
+    assert_close(out, ref32, 2e-2, 1e-2, "fused step")
+    out1 = extension.csa_decode_forward(q, k, v, idx.long(), 64)
+    assert_close(out1, ref32, 2e-2, 1e-2, "v1 op")
+
+
+def test_golden_small_fixture(golden_dir):
+    g = np.load(golden_dir / "csa_small.npz")
+    to_t = lambda bits: torch.from_numpy(bits.view(np.int16).copy()).view(torch.bfloat16).to(DEV)
+    q, k, v = to_t(g["q"]), to_t(g["k"]), to_t(g["v"])
+    summ = extension.csa_chunk_summary(k, 64)
+    np.testing.assert_allclose(summ.cpu().numpy(), g["chunk_mean"], rtol=0, atol=2e-6)
+    idx = extension.csa_select_topk(q, summ, 4)
+    assert np.array_equal(idx.cpu().numpy(), g["selected"])
+    out = extension.csa_decode_forward_tiled(q, k, v, idx, 64)
+    want = oracle.bf16_bits_to_f32(g["csa_out"]).astype(np.float64)
+    assert_close(out, want, 2e-2, 1e-2, "golden csa_out")
+
+
+SWEEP = [
+    # B, H, S, D, chunk, k, dtype
+    (1, 8, 8192, 128, 64, 8, torch.bfloat16),
+    (1, 8, 8192, 128, 64, 32, torch.bfloat16),
+    (3, 2, 4096, 128, 64, 5, torch.bfloat16),
+    (2, 3, 2048, 64, 64, 4, torch.bfloat16),
+    (2, 2, 2048, 256, 32, 6, torch.bfloat16),
+    (1, 2, 1024, 512, 64, 4, torch.bfloat16),
+    (2, 2, 2048, 128, 64, 8, torch.float16),
+    (2, 2, 2048, 128, 64, 8, torch.float32),
+    (1, 2, 1024, 64, 64, 4, torch.float64),
+    (1, 3, 1000, 96, 50, 4, torch.bfloat16),   # generic path: D not a vector width, chunk not a power of 2
+    (1, 2, 512, 1024, 64, 2, torch.bfloat16),  # generic path, widest head
+    (1, 2, 512, 32, 16, 7, torch.float32),
+]
+
+
+@pytest.mark.parametrize("B,H,S,D,chunk,k,dtype", SWEEP)
+@pytest.mark.parametrize("index_dtype", [torch.int32, torch.int64])
+def test_sweep_parity(B, H, S, D, chunk, k, dtype, index_dtype):
+    g = torch.Generator().manual_seed(B * 1000 + S + D + k)
+    q = torch.randn(B, H, D, generator=g).to(dtype)
+    kc = torch.randn(B, H, S, D, generator=g).to(dtype)
+    vc = torch.randn(B, H, S, D, generator=g).to(dtype)
+    C = S // chunk
+    idx = torch.stack([torch.randperm(C, generator=g)[:k] for _ in range(B * H)]).view(B, H, k).to(index_dtype)
+    ref = oracle.csa_attend(q, kc, vc, idx, chunk, prob_dtype=oracle.F32)
+    atol, rtol = tol_for(dtype)
+    qd, kd, vd, idd = q.to(DEV), kc.to(DEV), vc.to(DEV), idx.to(DEV)
+    for tile in (1, 7, 8, 64, k * chunk):
+        out = extension.csa_decode_forward_tiled(qd, kd, vd, idd, chunk, tile)
+        assert out.dtype == dtype and out.shape == q.shape
+        assert_close(out, ref, atol, rtol, f"tile={tile}")
+    assert_close(extension.csa_decode_forward(qd, kd, vd, idd, chunk), ref, atol, rtol, "v1")
+    # selection parity on the same inputs
+    summ = extension.csa_chunk_summary(kd, chunk)
+    summ_ref = oracle.chunk_mean(kc, chunk)
+    np.testing.assert_allclose(summ.cpu().numpy(), summ_ref, rtol=1e-6, atol=2e-6)
+    want, scores = oracle.select_topk(q, summ_ref, k)
+    assert_indices(extension.csa_select_topk(qd, summ, k), want, scores)
+
+
+def test_edge_indices():
+    B, H, S, D, chunk = 1, 4, 1000, 128, 64  # last chunk (id 15) is partial: tokens 960..999
+    g = torch.Generator().manual_seed(11)
+    q = torch.randn(B, H, D, generator=g).bfloat16()
+    kc = torch.randn(B, H, S, D, generator=g).bfloat16()
+    vc = torch.randn(B, H, S, D, generator=g).bfloat16()
+    idx = torch.tensor([[[3, -1, 15, 9],        # negative id skipped, partial chunk
+                         [-1, -1, -1, -1],      # nothing valid -> zeros
+                         [40, 15, -5, 15],      # id past the cache skipped, duplicate counted twice
+                         [0, 1, 2, 3]]], dtype=torch.int32)
+    ref = oracle.csa_attend(q, kc, vc, idx, chunk)
+    for tile in (1, 8, 33, 256):
+        out = extension.csa_decode_forward_tiled(q.to(DEV), kc.to(DEV), vc.to(DEV), idx.to(DEV), chunk, tile)
+        assert_close(out, ref, 2e-2, 1e-2, f"tile={tile}")
+        assert torch.all(out[0, 1] == 0)
+    # top_k = 0 -> zeros
+    out = extension.csa_decode_forward_tiled(q.to(DEV), kc.to(DEV), vc.to(DEV),
+                                             torch.empty(B, H, 0, dtype=torch.int32, device=DEV), chunk, 8)
+    assert torch.all(out == 0)
+
+
+@pytest.mark.parametrize("kind", ["scattered", "clustered"])
+@pytest.mark.parametrize("S,k", [(32768, 8), (131072, 32)])
+def test_planted_selection_bit_exact(kind, S, k):
+    B, H, D, chunk = 1, 8, 128, 64
+    C = S // chunk
+    case = make_synthetic_case(batch=B, heads=H, seq_len=S, head_dim=D, chunk_size=chunk, top_k=k, seed=2)
+    ids = scattered_chunks(B, H, C, k) if kind == "scattered" else clustered_chunks(B, H, C, k)
+    kp = plant_chunks(case.q, case.k_cache, ids, chunk, alpha=1.0).to(DEV)
+    summ = extension.csa_chunk_summary(kp, chunk)
+    idx = extension.csa_select_topk(case.q.to(DEV), summ, k)
+    assert torch.equal(idx.cpu(), ids)
+
+
+def test_tie_break_lowest_index_first():
+    q = torch.ones(2, 3, 64, dtype=torch.bfloat16, device=DEV)
+    k = torch.ones(2, 3, 64 * 40, 64, dtype=torch.bfloat16, device=DEV)
+    summ = extension.csa_chunk_summary(k, 64)
+    idx = extension.csa_select_topk(q, summ, 7)
+    assert torch.equal(idx.cpu(), torch.arange(7, dtype=torch.int32).expand(2, 3, 7))
+    # ties below distinct winners: chunk 30 best, then equal rest in index order
+    k[:, :, 30 * 64:31 * 64] = 2.0
+    idx = extension.csa_select_topk(q, extension.csa_chunk_summary(k, 64), 4)
+    assert torch.equal(idx.cpu(), torch.tensor([30, 0, 1, 2], dtype=torch.int32).expand(2, 3, 4))
+
+
+def test_select_top_k_larger_than_chunks_and_wide():
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(2, 2, 128, generator=g).bfloat16()
+    summ = torch.randn(2, 2, 3000, 128, generator=g) * 0.1
+    want, scores = oracle.select_topk(q, summ, 300)
+    got = extension.csa_select_topk(q.to(DEV), summ.to(DEV), 300)
+    assert_indices(got, want, scores)
+    want, scores = oracle.select_topk(q, summ[:, :, :5], 9)
+    got = extension.csa_select_topk(q.to(DEV), summ[:, :, :5].contiguous().to(DEV), 9)
+    assert got.shape == (2, 2, 5)
+    assert_indices(got, want, scores)
+
+
+def test_summary_incremental_update():
+    case = make_synthetic_case(batch=1, heads=2, seq_len=4096, head_dim=128, chunk_size=64, top_k=4, seed=9)
+    k = case.k_cache.to(DEV)
+    full = extension.csa_chunk_summary(k, 64)
+    part = torch.zeros_like(full)
+    native.csa_chunk_summary(k, 64, out=part, chunk_begin=10, num_chunks=5)
+    assert torch.equal(part[:, :, 10:15], full[:, :, 10:15])
+    assert torch.all(part[:, :, :10] == 0) and torch.all(part[:, :, 15:] == 0)
+
+
+def test_deterministic_and_tile_invariant():
+    case = make_synthetic_case(batch=2, heads=8, seq_len=16384, head_dim=128, chunk_size=64, top_k=16, seed=4)
+    q, k, v = case.q.to(DEV), case.k_cache.to(DEV), case.v_cache.to(DEV)
+    summ = extension.csa_chunk_summary(k, 64)
+    idx = extension.csa_select_topk(q, summ, 16)
+    a = extension.csa_decode_forward_tiled(q, k, v, idx, 64, 16)
+    b = extension.csa_decode_forward_tiled(q, k, v, idx, 64, 16)
+    assert torch.equal(a, b)
+    assert torch.equal(idx, extension.csa_select_topk(q, summ, 16))
+    outs = [extension.csa_decode_forward_tiled(q, k, v, idx, 64, t).float() for t in (1, 8, 64, 1024)]
+    for o in outs[1:]:
+        assert torch.allclose(o, outs[0], atol=1e-2, rtol=1e-2)
+
+
+def test_large_offsets_beyond_2_to_32_elements():
+    """B32 H8 S131072 D128: K and V each hold 2^32 elements, so the last heads sit
+    past every 32-bit offset.  Heads (0,0) and (31,7) are checked on the CPU."""
+    B, H, S, D, chunk, k = 32, 8, 131072, 128, 64, 8
+    g = torch.Generator(device=DEV).manual_seed(0)
+    kc = torch.empty(B, H, S, D, dtype=torch.bfloat16, device=DEV).normal_(generator=g)
+    vc = torch.empty(B, H, S, D, dtype=torch.bfloat16, device=DEV).normal_(generator=g)
+    q = torch.randn(B, H, D, dtype=torch.bfloat16, device=DEV, generator=g)
+    C = S // chunk
+    idx = torch.arange(C - k, C, dtype=torch.int32, device=DEV).flip(0).expand(B, H, k).contiguous()
+    out = extension.csa_decode_forward_tiled(q, kc, vc, idx, chunk, 64)
+    summ = extension.csa_chunk_summary(kc, chunk)
+    sel = extension.csa_select_topk(q, summ, k)
+    for b, h in ((0, 0), (31, 7)):
+        ks, vs = kc[b:b + 1, h:h + 1].cpu(), vc[b:b + 1, h:h + 1].cpu()
+        qs = q[b:b + 1, h:h + 1].cpu()
+        ref = oracle.csa_attend(qs, ks, vs, idx[b:b + 1, h:h + 1].cpu(), chunk)
+        assert_close(out[b:b + 1, h:h + 1], ref, 2e-2, 1e-2, f"bh=({b},{h})")
+        sref = oracle.chunk_mean(ks, chunk)
+        np.testing.assert_allclose(summ[b:b + 1, h:h + 1].cpu().numpy(), sref, rtol=0, atol=2e-6)
+        want, scores = oracle.select_topk(qs, sref, k)
+        assert_indices(sel[b:b + 1, h:h + 1], want, scores)
+    del kc, vc
+    torch.cuda.empty_cache()
+
+
+def test_cuda_graph_replays_match_eager():
+    case = make_synthetic_case(batch=1, heads=8, seq_len=32768, head_dim=128, chunk_size=64, top_k=8, seed=0)
+    q, k, v = case.q.to(DEV), case.k_cache.to(DEV), case.v_cache.to(DEV)
+    summ = extension.csa_chunk_summary(k, 64)
+    eager_out, eager_idx = native.csa_decode_step(q, k, v, summ, 64, 8)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        native.csa_decode_step(q, k, v, summ, 64, 8)  # warm up allocations on the side stream
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        gout, gidx = native.csa_decode_step(q, k, v, summ, 64, 8)
+    for _ in range(3):
+        gout.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(gidx, eager_idx)
+        assert torch.equal(gout, eager_out)
+        native.csa_decode_step(q, k, v, summ, 64, 8)  # eager work between replays
+        torch.cuda.synchronize()

@@ -1,0 +1,178 @@
+"""GPU parity of the DSV4 paged-FP8 decode against the CPU oracle and the
+reference's golden vectors.  Tolerance for the FP8-cache modes (BASELINE north
+star): |got - ref| <= 5e-2 + 5e-2 |ref| for 16-bit queries; fp32 queries are
+held to 1e-4 + 1e-4 |ref|."""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from csahca_amd import dsv4_layout, extension, native
+from csahca_amd.synthetic import make_dsv4_case, make_dsv4_window_case
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+SCALE = 1.0 / math.sqrt(512)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.fail("no HIP device visible")
+    native.lib()
+
+
+def assert_close(got, ref, atol=5e-2, rtol=5e-2, what=""):
+    g = got.detach().float().cpu().numpy().astype(np.float64)
+    assert g.shape == ref.shape
+    diff = np.abs(g - ref)
+    bad = diff > atol + rtol * np.abs(ref)
+    assert not bad.any(), f"{what} max_abs={diff.max():.3e} bad={int(bad.sum())}/{bad.size}"
+
+
+def oracle_out(c, sink=True, scale=SCALE, lengths=True):
+    kw = {}
+    if c.extra_cache is not None:
+        kw = dict(extra_cache=c.extra_cache.cpu(), extra_token_indices=c.extra_token_indices.cpu(),
+                  extra_topk_lengths=c.extra_topk_lengths.cpu() if lengths else None,
+                  extra_page_size=c.extra_page_size)
+    return oracle.dsv4_reference_attention(c.q.cpu(), c.cache.cpu(), c.token_indices.cpu(),
+                                           c.topk_lengths.cpu() if lengths else None,
+                                           c.attn_sink.cpu() if sink else None, page_size=c.page_size,
+                                           softmax_scale=scale, **kw)
+
+
+def gpu_out(c, sink=True, scale=SCALE, lengths=True):
+    s = c.attn_sink.to(DEV) if sink else None
+    if c.extra_cache is not None:
+        return extension.dsv4_sparse_decode_forward(
+            c.q.to(DEV), c.cache.to(DEV), c.token_indices.to(DEV), c.topk_lengths.to(DEV) if lengths else None,
+            c.extra_cache.to(DEV), c.extra_token_indices.to(DEV),
+            c.extra_topk_lengths.to(DEV) if lengths else None, s, c.page_size, c.extra_page_size, scale)
+    return extension.dsv4_swa_decode_forward(c.q.to(DEV), c.cache.to(DEV), c.token_indices.to(DEV),
+                                             c.topk_lengths.to(DEV) if lengths else None, s, c.page_size, scale)
+
+
+@pytest.mark.parametrize("ratio", [0, 4, 128])
+def test_golden_fixtures(golden_dir, ratio):
+    g = np.load(golden_dir / f"dsv4_c{ratio}.npz")
+    bf = lambda bits: torch.from_numpy(bits.view(np.int16).copy()).view(torch.bfloat16).to(DEV)
+    q = bf(g["q"])
+    cache = torch.from_numpy(g["cache"]).to(DEV)
+    idx = torch.from_numpy(g["token_indices"]).to(DEV)
+    lens = torch.from_numpy(g["topk_lengths"]).to(DEV)
+    sink = torch.from_numpy(g["attn_sink"]).to(DEV)
+    ps = int(g["page_size"])
+    for key, s in (("out", sink), ("out_nosink", None)):
+        if ratio:
+            out = extension.dsv4_sparse_decode_forward(
+                q, cache, idx, lens, torch.from_numpy(g["extra_cache"]).to(DEV),
+                torch.from_numpy(g["extra_token_indices"]).to(DEV),
+                torch.from_numpy(g["extra_topk_lengths"]).to(DEV), s, ps, int(g["extra_page_size"]),
+                float(g["softmax_scale"]))
+        else:
+            out = extension.dsv4_swa_decode_forward(q, cache, idx, lens, s, ps, float(g["softmax_scale"]))
+        want = oracle.bf16_bits_to_f32(g[key]).astype(np.float64)
+        assert_close(out, want, what=key)
+
+
+@pytest.mark.parametrize("ratio", [0, 4, 128])
+@pytest.mark.parametrize("nq,heads", [(1, 8), (1, 64), (32, 8), (32, 64)])
+def test_baseline_window_configs(ratio, nq, heads):
+    c = make_dsv4_window_case(compress_ratio=ratio, num_queries=nq, heads=heads, seed=ratio + nq + heads,
+                              device=DEV)
+    ref = oracle_out(c)
+    assert_close(gpu_out(c), ref, what="tiled")
+    for scale in (1.0 / math.sqrt(576),):
+        assert_close(gpu_out(c, scale=scale), oracle_out(c, scale=scale), what="scale 1/sqrt(576)")
+
+
+@pytest.mark.parametrize("ratio", [0, 4, 128])
+def test_reference_harness_shapes_page_256(ratio):
+    c = make_dsv4_case(compress_ratio=ratio, num_queries=7, heads=8, num_tokens=1024, top_k=128, page_size=256,
+                       extra_tokens=1024, extra_top_k=0, seed=1, device=DEV)
+    ref = oracle_out(c)
+    assert_close(gpu_out(c), ref)
+    assert_close(gpu_out(c, sink=False), oracle_out(c, sink=False), what="no sink")
+    assert_close(gpu_out(c, lengths=False), oracle_out(c, lengths=False), what="no lengths")
+
+
+@pytest.mark.parametrize("route", ["tiled-auto", "tiled-1", "tiled-8", "tiled-1000", "untiled"])
+def test_routes_agree(route, monkeypatch):
+    if route == "untiled":
+        monkeypatch.setenv("CSAHCA_DSV4_TILED", "0")
+    else:
+        monkeypatch.setenv("CSAHCA_DSV4_TILE_SIZE", "0" if route == "tiled-auto" else route.split("-")[1])
+    for ratio in (0, 4):
+        c = make_dsv4_case(compress_ratio=ratio, num_queries=5, heads=16, num_tokens=512, top_k=64, page_size=64,
+                           extra_tokens=512, extra_top_k=48, seed=3, device=DEV)
+        assert_close(gpu_out(c), oracle_out(c), what=route)
+
+
+@pytest.mark.parametrize("q_dtype", [torch.float32, torch.float16, torch.float64])
+def test_query_dtypes(q_dtype):
+    c = make_dsv4_case(compress_ratio=4, num_queries=3, heads=8, num_tokens=256, top_k=32, page_size=64,
+                       extra_tokens=256, extra_top_k=32, q_dtype=q_dtype, seed=4, device=DEV)
+    out = gpu_out(c)
+    assert out.dtype == q_dtype
+    tol = (5e-2, 5e-2) if q_dtype == torch.float16 else (1e-4, 1e-4)
+    assert_close(out, oracle_out(c), *tol)
+
+
+def test_edges():
+    c = make_dsv4_case(compress_ratio=4, num_queries=4, heads=8, num_tokens=256, top_k=16, page_size=64,
+                       extra_tokens=256, extra_top_k=16, seed=6, device=DEV)
+    c.topk_lengths = torch.tensor([0, 16, 100, -3], dtype=torch.int32, device=DEV)
+    c.extra_topk_lengths = torch.tensor([0, 5, 16, 0], dtype=torch.int32, device=DEV)
+    c.token_indices[1, :4] = -1
+    c.token_indices[2, 3] = 10_000_000  # page past the cache: skipped
+    assert_close(gpu_out(c), oracle_out(c))
+    # query 0 and 3 have nothing valid: with a sink the output is exactly 0
+    out = gpu_out(c)
+    assert torch.all(out[0] == 0) and torch.all(out[3] == 0)
+    out = gpu_out(c, sink=False)
+    assert torch.all(out[0] == 0)
+    # every slot -1
+    c.token_indices.fill_(-1)
+    c.extra_token_indices.fill_(-1)
+    assert torch.all(gpu_out(c) == 0)
+
+
+def test_unaligned_bytes_per_page_scalar_path():
+    c = make_dsv4_case(compress_ratio=0, num_queries=3, heads=8, num_tokens=256, top_k=32, page_size=64, seed=7)
+    bpp = c.cache.shape[1]
+    wide = torch.zeros((c.cache.shape[0], bpp + 4), dtype=torch.uint8)
+    wide[:, :bpp] = c.cache  # rows and scales keep their offsets; 4 trailing pad bytes per page
+    c.cache = wide
+    assert_close(gpu_out(c), oracle_out(c))
+
+
+def test_e4m3_and_scale_decode_exhaustive():
+    """Single valid slot, no sink, fp32 query: out = the dequantised row exactly.
+    Rows cover all 256 e4m3 codes (NaN codes excluded) under many scale bytes."""
+    codes = np.array([b for b in range(256) if (b & 0x7F) != 0x7F], dtype=np.uint8)
+    ps = 4
+    bpp = dsv4_layout.bytes_per_page(ps)
+    # exponent bytes keep every dequantised value a normal fp32 number
+    scale_bytes = [93, 100, 110, 120, 127, 130, 140, 200]
+    n = len(scale_bytes)
+    cache = np.zeros((math.ceil(n / ps), bpp), dtype=np.uint8)
+    rope = torch.randn(n, 64, generator=torch.Generator().manual_seed(0)).bfloat16()
+    rope_bytes = rope.view(torch.int16).numpy().view(np.uint8).reshape(n, 128)
+    for t, sb in enumerate(scale_bytes):
+        page, r = divmod(t, ps)
+        row = np.resize(np.roll(codes, 37 * t), 448)
+        cache[page, r * 576:r * 576 + 448] = row
+        cache[page, r * 576 + 448:r * 576 + 576] = rope_bytes[t]
+        cache[page, ps * 576 + r * 8:ps * 576 + r * 8 + 7] = [sb + 3 * j for j in range(7)]
+    locs = np.arange(n, dtype=np.int32)
+    want = oracle.dequant_dsv4_cache(cache, locs, page_size=ps).astype(np.float64)
+    q = torch.zeros(n, 1, 512, dtype=torch.float32, device=DEV)
+    idx = torch.from_numpy(locs.reshape(n, 1)).to(DEV)
+    out = extension.dsv4_swa_decode_forward(q, torch.from_numpy(cache).to(DEV), idx, None, None, ps, SCALE)
+    got = out[:, 0].cpu().numpy().astype(np.float64)
+    # the oracle dequant rounds nope values to bf16 (exact for e4m3 * 2^k)
+    assert np.array_equal(got, want)
