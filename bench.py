@@ -1,0 +1,392 @@
+#!/usr/bin/env python
+"""bench.py -- CSA decode ms/token at 32K context on one MI355X, with the HBM
+roofline of the dominant kernel, the CPU oracle baseline, and DSV4 ms/query.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep] [--no-dsv4]
+
+Workload (BASELINE config 2 at its headline point): one decode step = select the
+top-8 of 512 chunks from cached fp32 chunk summaries (score + top-k kernels),
+then split-KV sparse attention over the 512 selected tokens of each head plus
+the partial merge.  B=1, H=8, D=128, S=32768, chunk 64, bf16 N(0,1) inputs from
+the CPU generator (seed 0).  Inputs are resident in HBM before timing.
+
+Caches lie: a step touches ~4 MiB, which L2 (4 MiB per XCD) or the 256 MiB
+Infinity Cache would hold, so the timed loop rotates through --copies distinct
+copies of (K, V, summaries) -- by default 128, i.e. 512 MiB of touched bytes per
+rotation and 16 GiB resident.  The K timed steps are HIP-graph replays (one graph
+node per kernel) bracketed by synchronisations; eager timing is reported too.
+
+The roofline entry uses per-dispatch device durations measured live with HIP
+events (hipExtLaunchKernel start/stop, via csahca_profile_*) over K eager steps.
+
+Prints ONE JSON line on stdout; progress goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_HBM_GBPS = 8000.0
+METRIC = "CSA decode ms/token @32K ctx (1 GPU) + achieved HBM GB/s vs peak; DSV4 ms/query"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2048)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--copies", type=int, default=128)
+    ap.add_argument("--tile", type=int, default=0, help="CSA split size for --route two-pass (0 = library choice)")
+    ap.add_argument("--route", choices=["fused", "two-pass"], default="fused",
+                    help="fused: one launch per step; two-pass: score, top-k, attend and merge kernels")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-dsv4", action="store_true")
+    ap.add_argument("--sweep", action="store_true", help="also run the BASELINE config-2 sweep (stderr + json)")
+    ap.add_argument("--sweep-out", type=Path, default=None)
+    return ap.parse_args()
+
+
+# ---------------------------------------------------------------------------
+# helpers
+# ---------------------------------------------------------------------------
+
+def graph_of(fn_list):
+    """Capture the callables in order into one HIP graph (after a side-stream warm-up)."""
+    import torch
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for fn in fn_list[:2]:
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for fn in fn_list:
+            fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph_steps(graph, rem_graph, per_graph, steps):
+    """Replay so that exactly `steps` steps run; returns elapsed ms (device events)."""
+    import torch
+
+    full, rem = divmod(steps, per_graph)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(full):
+        graph.replay()
+    if rem:
+        rem_graph[rem].replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end)
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+# ---------------------------------------------------------------------------
+# CSA headline
+# ---------------------------------------------------------------------------
+
+def csa_bench(args, B=1, H=8, S=32768, D=128, chunk=64, top_k=8, copies=None, seed=0, planted=None,
+              profile=True, eager=True):
+    import torch
+
+    from csahca_amd import native
+    from csahca_amd.synthetic import make_synthetic_case, plant_chunks, scattered_chunks
+
+    dev = torch.device("cuda", 0)
+    if B * S <= 8 * 32768:
+        case = make_synthetic_case(batch=B, heads=H, seq_len=S, head_dim=D, chunk_size=chunk, top_k=top_k,
+                                   seed=seed)
+        kc = case.k_cache
+        if planted == "scattered":
+            kc = plant_chunks(case.q, kc, scattered_chunks(B, H, S // chunk, top_k), chunk, alpha=1.0)
+        q = case.q.to(dev)
+        k0, v0 = kc.to(dev), case.v_cache.to(dev)
+        del case, kc
+    else:  # large sweep points: draw on the device (timing only, no CPU check)
+        g = torch.Generator(device=dev).manual_seed(seed)
+        q = torch.randn(B, H, D, dtype=torch.bfloat16, device=dev, generator=g)
+        k0 = torch.empty(B, H, S, D, dtype=torch.bfloat16, device=dev).normal_(generator=g)
+        v0 = torch.empty(B, H, S, D, dtype=torch.bfloat16, device=dev).normal_(generator=g)
+    summ0 = native.csa_chunk_summary(k0, chunk)
+    C = S // chunk
+    sel_bytes = B * H * top_k * chunk * D * 2 * 2
+    summ_bytes = B * H * C * D * 4
+    small = B * H * D * 2 * 2 + B * H * top_k * 4  # q + out + indices
+    step_bytes = sel_bytes + summ_bytes + small
+    if copies is None:
+        budget = 48 * 2 ** 30
+        per_copy = 2 * k0.numel() * k0.element_size() + summ0.numel() * 4
+        want = max(1, math.ceil(1.0 * 2 ** 30 / max(step_bytes, 1)))
+        copies = max(1, min(args.copies, want, budget // max(per_copy, 1)))
+    ks, vs, ss = [k0], [v0], [summ0]
+    for _ in range(copies - 1):
+        ks.append(k0.clone())
+        vs.append(v0.clone())
+        ss.append(summ0.clone())
+    tile = (args.tile or native.csa_auto_tile_size(B, H, min(top_k, C), chunk)) if args.route == "two-pass" else 0
+
+    def step(i):
+        j = i % copies
+        return native.csa_decode_step(q, ks[j], vs[j], ss[j], chunk, top_k, tile)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    per_graph = copies
+    graph = graph_of([lambda i=i: step(i) for i in range(per_graph)])
+    rem = args.steps % per_graph
+    rem_graph = {rem: graph_of([lambda i=i: step(i) for i in range(rem)])} if rem else {}
+    ms_graph = time_graph_steps(graph, rem_graph, per_graph, args.steps)
+    res = dict(B=B, H=H, S=S, D=D, chunk=chunk, top_k=top_k, tile=tile, copies=copies,
+               ms_per_step_graph=ms_graph / args.steps, step_bytes=step_bytes, sel_bytes=sel_bytes,
+               summ_bytes=summ_bytes)
+    if eager:
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            step(i)
+        torch.cuda.synchronize()
+        res["ms_per_step_eager"] = (time.perf_counter() - t0) * 1e3 / args.steps
+    if profile:
+        with native.profile_launches() as prof:
+            for i in range(args.steps):
+                step(i)
+        res["kernels"] = prof.results
+    del graph, rem_graph, ks, vs, ss, k0, v0, summ0
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return res
+
+
+def kernel_bytes(name, r):
+    """Algorithmic HBM bytes per launch of each CSA kernel for workload r."""
+    B, H, D, C, k, chunk = r["B"], r["H"], r["D"], r["S"] // r["chunk"], r["top_k"], r["chunk"]
+    if name.startswith("csa_attend"):
+        return r["sel_bytes"] + B * H * D * 2 + B * H * k * 4          # selected K,V + q + chunk ids
+    if name.startswith("csa_score"):
+        return r["summ_bytes"] + B * H * D * 2                            # summaries + q
+    if name == "csa_topk_kernel":
+        return B * H * C * 4 + B * H * k * 4                              # scores in, ids out
+    if name == "csa_merge_kernel":
+        return B * H * D * 2                                              # output row
+    if name == "csa_step_kernel":
+        # summaries + selected K,V + q + out + chunk ids (the whole decode step)
+        return r["summ_bytes"] + r["sel_bytes"] + B * H * D * 2 * 2 + B * H * k * 4
+    return 0
+
+
+def cpu_baseline(seconds: float):
+    """Time the oracle's decode step (selection from cached summaries + torch-csa
+    attention, bf16-rounded probabilities) on the host on a bounded sample."""
+    import oracle
+    from csahca_amd.synthetic import make_synthetic_case
+
+    case = make_synthetic_case(batch=1, heads=8, seq_len=32768, head_dim=128, chunk_size=64, top_k=8, seed=0)
+    summ = oracle.chunk_mean(case.k_cache, 64)
+    nthreads = max(1, min(oracle.ncores(), 8))  # the attention parallelises over the 8 heads
+    t = oracle.DecodeStepTimer(case.q, case.k_cache, case.v_cache, summ, 64, 8)
+    t.step(nthreads)
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        t.step(nthreads)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds and n >= 3:
+            break
+    ms = el * 1e3 / n
+    return {"value": round(ms, 5), "unit": "ms/token", "cores": nthreads, "kind": "port",
+            "sample": f"{n} decode steps (B1 H8 S32768 D128 chunk64 k8; top-8 selection from cached fp32 "
+                      f"summaries + attention over 512 tokens/head) of the C oracle, {el:.1f} s wall, "
+                      f"{nthreads} OpenMP threads on '{cpu_model()}' ({oracle.ncores()} cores visible)"}
+
+
+# ---------------------------------------------------------------------------
+# DSV4
+# ---------------------------------------------------------------------------
+
+def dsv4_bench(steps=200, copies=64):
+    import torch
+
+    from csahca_amd import native
+    from csahca_amd.synthetic import make_dsv4_window_case
+
+    dev = torch.device("cuda", 0)
+    scale = 1.0 / math.sqrt(512)
+    out = {}
+    for ratio in (0, 4, 128):
+        c = make_dsv4_window_case(compress_ratio=ratio, num_queries=32, heads=64, seed=ratio, device=dev)
+        caches = [c.cache] + [c.cache.clone() for _ in range(copies - 1)]
+        ecaches = ([c.extra_cache] + [c.extra_cache.clone() for _ in range(copies - 1)]) if ratio else None
+        for nq in (1, 32):
+            for H in (8, 64):
+                q = c.q[:nq, :H].contiguous()
+                idx = c.token_indices[:nq].contiguous()
+                lens = c.topk_lengths[:nq].contiguous()
+                sink = c.attn_sink[:H].contiguous()
+                if ratio:
+                    eidx = c.extra_token_indices[:nq].contiguous()
+                    elens = c.extra_topk_lengths[:nq].contiguous()
+
+                def call(j):
+                    if ratio:
+                        return native.dsv4_decode_forward_tiled(q, caches[j], idx, lens, ecaches[j], eidx, elens,
+                                                                sink, c.page_size, c.extra_page_size, 0, scale)
+                    return native.dsv4_decode_forward_tiled(q, caches[j], idx, lens, None, None, None, sink,
+                                                            c.page_size, 1, 0, scale)
+
+                for j in range(3):
+                    call(j)
+                g = graph_of([lambda j=j: call(j) for j in range(copies)])
+                reps = max(1, steps // copies)
+                ms = time_graph_steps(g, {}, copies, reps * copies) / (reps * copies)
+                with native.profile_launches() as prof:
+                    for j in range(copies):
+                        call(j)
+                slots = idx.shape[1] + (eidx.shape[1] if ratio else 0)
+                bytes_q = nq * slots * 584 + nq * H * 1024 * 2 + nq * slots * 4 + H * 4
+                tile_us = prof.results.get("dsv4_tile_kernel", {}).get("avg_us", float("nan"))
+                key = f"c{ratio}_nq{nq}_h{H}"
+                out[key] = {"ms_per_call": round(ms, 5), "ms_per_query": round(ms / nq, 5),
+                            "query_heads_per_s": round(nq * H / (ms / 1e3), 1),
+                            "tile_kernel_us": round(tile_us, 3),
+                            "merge_kernel_us": round(prof.results.get("dsv4_merge_kernel", {}).get("avg_us", 0), 3),
+                            "algorithmic_bytes": bytes_q,
+                            "achieved_gbps_call": round(bytes_q / (ms / 1e3) / 1e9, 1)}
+                log(f"dsv4 {key}: {out[key]}")
+                del g
+        del caches, ecaches, c
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    return out
+
+
+def sweep(args):
+    rows = []
+    for B in (1, 8, 32):
+        for S in (8192, 32768, 131072):
+            for k in (8, 32):
+                for variant in ("iid", "scattered"):
+                    if variant == "scattered" and B * S > 8 * 32768:
+                        continue  # planting is a CPU loop; keep it to the small points
+                    r = csa_bench(args, B=B, S=S, top_k=k, copies=None, planted=None if variant == "iid" else
+                                     "scattered", eager=False)
+                    kern = {n: v["avg_us"] for n, v in r["kernels"].items()}
+                    row = dict(B=B, S=S, top_k=k, variant=variant, tile=r["tile"], copies=r["copies"],
+                               ms_per_step=round(r["ms_per_step_graph"], 5),
+                               step_gbps=round(r["step_bytes"] / (r["ms_per_step_graph"] / 1e3) / 1e9, 1),
+                               kernels_us={n: round(v, 3) for n, v in kern.items()})
+                    att = [n for n in kern if n.startswith("csa_attend")]
+                    if att:
+                        row["attend_gbps"] = round(kernel_bytes(att[0], r) / (kern[att[0]] * 1e-6) / 1e9, 1)
+                    log("sweep", json.dumps(row))
+                    rows.append(row)
+    return rows
+
+
+def main():
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}); "
+              "the decode path has no cross-GPU exchange to time here", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        sys.exit(1)
+    from csahca_amd import native
+
+    native.lib()
+    log(f"device: {torch.cuda.get_device_name(0)}")
+    r = csa_bench(args, copies=args.copies)
+    ms = r["ms_per_step_graph"]
+    kern = r["kernels"]
+    log("csa kernels:", json.dumps(kern))
+    # dominant kernel = largest total device time
+    dom = max(kern, key=lambda n: kern[n]["total_ms"])
+    dom_bytes = kernel_bytes(dom, r)
+    dom_us = kern[dom]["avg_us"]
+    achieved = dom_bytes / (dom_us * 1e-6) / 1e9
+    traffic = None
+    tfile = ROOT / "profiles" / "traffic.json"
+    if tfile.exists():
+        try:
+            traffic = json.loads(tfile.read_text()).get(dom, {}).get("hbm_bytes_per_launch")
+        except (ValueError, AttributeError):
+            traffic = None
+    line = {
+        "metric": METRIC,
+        "value": round(ms, 6),
+        "unit": "ms/token",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "csa_decode_step B1 H8 D128 S32768 chunk64 top_k8 (select from cached fp32 "
+                               "summaries + split-KV attend + merge)",
+                   "batch": 1, "heads": 8, "head_dim": 128, "seq_len": 32768, "chunk_size": 64, "top_k": 8,
+                   "route": args.route, "tile": r["tile"] or None, "cache_copies_rotated": r["copies"],
+                   "timing": "hip graph replay",
+                   "parallelism": "single GPU"},
+        "tokens_per_s": round(1e3 / ms, 1),
+        "ms_per_step_eager": round(r["ms_per_step_eager"], 6),
+        "step_bytes": r["step_bytes"],
+        "step_hbm_gbps": round(r["step_bytes"] / (ms / 1e3) / 1e9, 1),
+        "kernels_avg_us": {n: round(v["avg_us"], 3) for n, v in kern.items()},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": traffic,
+                     "bytes_per_launch": dom_bytes, "avg_launch_us": round(dom_us, 3)},
+    }
+    if not args.no_dsv4:
+        line["dsv4"] = dsv4_bench()
+    if args.sweep:
+        rows = sweep(args)
+        out = args.sweep_out or (ROOT / "gpurun_out" / "sweep.json")
+        out.parent.mkdir(parents=True, exist_ok=True)
+        out.write_text(json.dumps(rows, indent=1) + "\n")
+    if not args.no_cpu_baseline:
+        log("cpu baseline ...")
+        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -5,6 +5,7 @@
 // by log2(e)) so every exponential is one v_exp_f32.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -146,6 +147,31 @@ int dispatch_dtype(int dtype, F&& f) {
   do {                                                              \
     if (!(cond)) return ::csahca::fail(CSAHCA_ERR_ARGUMENT, (msg)); \
   } while (0)
+
+// Launch-time profiling (csahca_profile_begin/end): while active on the
+// calling thread, launches go through hipExtLaunchKernelGGL with a start/stop
+// event pair, which timestamps the dispatch itself.
+bool profiling_active();
+bool profile_take_events(hipEvent_t* start, hipEvent_t* stop);
+void profile_record(const char* name, hipEvent_t start, hipEvent_t stop);
+
+template <typename... KArgs, typename... Args>
+int launch(const char* name, void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t shmem,
+           hipStream_t stream, Args... args) {
+  if (profiling_active()) {
+    hipEvent_t a = nullptr, b = nullptr;
+    if (!profile_take_events(&a, &b)) return fail(CSAHCA_ERR_HIP, "profiling: hipEventCreate failed");
+    hipExtLaunchKernelGGL(kernel, grid, block, static_cast<uint32_t>(shmem), stream, a, b, 0u,
+                          static_cast<KArgs>(args)...);
+    profile_record(name, a, b);
+  } else {
+    hipLaunchKernelGGL(kernel, grid, block, static_cast<uint32_t>(shmem), stream,
+                       static_cast<KArgs>(args)...);
+  }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail_hip(e, name);
+  return CSAHCA_OK;
+}
 
 #define CSAHCA_LAUNCH_CHECK(where)                                 \
   do {                                                             \

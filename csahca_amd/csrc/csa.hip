@@ -2,53 +2,29 @@
 //
 // Decode step (one query token per (batch, head)):
 //   1. csa_summary_*   : fp32 mean of every chunk of K (the chunk summaries).
-//   2. csa_score_*     : score[c] = (q . summary[c]) / sqrt(D), fp32.
-//   3. csa_topk_kernel : per (b,h) one wavefront selects the top-k chunks by
-//                        radix select over order-preserving uint32 keys, then
-//                        ranks the k winners (score desc, chunk id asc).
+//   2. csa_score_*     : score[c] = (q . summary[c]) / sqrt(D) in fp32, stored as
+//                        an order-preserving uint32 key.
+//   3. csa_topk_kernel : per (b,h) one wavefront loads the keys into LDS once and
+//                        selects the top-k (radix select + rank; score desc,
+//                        chunk id asc).
 //   4. csa_attend_*    : split-KV sparse attention.  Work item = one wavefront
 //                        over `tile` consecutive selected-token slots of one
 //                        (b,h); K/V rows are fetched with 16-byte lane loads so
-//                        a wavefront-wide load moves whole 256-byte rows
-//                        (D=128, bf16); online softmax in registers; writes an
-//                        fp32 partial (m, l, acc[D]).
-//   5. csa_merge_kernel: log-sum-exp merge of the partials of each (b,h).
-// All offsets are 64-bit.
-#include "common.hpp"
+//                        one wavefront-wide load moves whole rows; online
+//                        softmax in registers; fp32 partial (m, l, acc[D]).
+//   5. csa_merge_kernel: log-sum-exp merge of the partials of each (b,h), with
+//                        all partial loads independent of each other.
+// csa_step.hip fuses 2-5 into one launch.  All offsets are 64-bit.
+#include "csa_device.hpp"
 
+#include <algorithm>
 #include <climits>
 
 namespace csahca {
 namespace {
 
 // ---------------------------------------------------------------------------
-// Selected-slot -> token mapping shared by the attend kernels.
-// Slot s of (b,h) is token idx[s / chunk] * chunk + s % chunk; the slot is
-// skipped when the chunk id is negative or the token is past seq_len
-// (csrc/csa_attention.cu:176-185).
-// ---------------------------------------------------------------------------
-template <typename IdxT>
-__device__ __forceinline__ bool slot_token(const IdxT* __restrict__ ib, int s, int chunk,
-                                           int chunk_shift, int64_t seq_len, int64_t& tok) {
-  int cs, off;
-  if (chunk_shift >= 0) {
-    cs = s >> chunk_shift;
-    off = s & (chunk - 1);
-  } else {
-    cs = s / chunk;
-    off = s - cs * chunk;
-  }
-  const int64_t c = static_cast<int64_t>(ib[cs]);
-  tok = c * chunk + off;
-  return c >= 0 && tok < seq_len;
-}
-
-// ---------------------------------------------------------------------------
-// Split-KV sparse attention, vectorised path.
-// D = VEC * LPR with LPR (lanes per row) a power of two <= 64; a wavefront-wide
-// 16-byte load covers RPL = 64 / LPR rows.  Each lane owns VEC columns of q,
-// K, V and acc; a row's dot product is a butterfly over its LPR lanes.
-// U row loads per lane per iteration keep 2*U*16 bytes in flight per lane.
+// Split-KV sparse attention (vectorised path).
 // ---------------------------------------------------------------------------
 template <typename T, typename IdxT, int D, int U>
 __global__ __launch_bounds__(64) void csa_attend_vec_kernel(
@@ -56,11 +32,8 @@ __global__ __launch_bounds__(64) void csa_attend_vec_kernel(
     const IdxT* __restrict__ idx, float* __restrict__ part_ml, float* __restrict__ part_acc,
     int64_t seq_len, int top_k, int chunk, int chunk_shift, int tile, int num_tiles,
     float qscale) {
-  constexpr int VEC = Vec16<T>::N;
-  constexpr int LPR = D / VEC;
-  constexpr int RPL = kWave / LPR;
-  static_assert(LPR >= 1 && LPR <= kWave && (LPR & (LPR - 1)) == 0, "bad row split");
-
+  using L = AttendLayout<T, D>;
+  constexpr int VEC = L::VEC, LPR = L::LPR, RPL = L::RPL;
   const int lane = threadIdx.x;
   const int grp = lane / LPR;
   const int col = lane % LPR;
@@ -72,94 +45,36 @@ __global__ __launch_bounds__(64) void csa_attend_vec_kernel(
   load16<T>(q + bh * D + col * VEC, qf);
 #pragma unroll
   for (int e = 0; e < VEC; ++e) qf[e] *= qscale;
-
   const T* __restrict__ kb = k + bh * seq_len * D + col * VEC;
   const T* __restrict__ vb = v + bh * seq_len * D + col * VEC;
   const IdxT* __restrict__ ib = idx + bh * top_k;
   const int total = top_k * chunk;
   const int s0 = t * tile;
   const int s1 = min(s0 + tile, total);
-
-  float m = -INFINITY, l = 0.f;
-  float acc[VEC];
-#pragma unroll
-  for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
-
-  for (int base = s0; base < s1; base += RPL * U) {
-    float kr[U][VEC], vr[U][VEC];
-    bool ok[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int s = base + grp + RPL * u;
-      int64_t tok = 0;
-      ok[u] = s < s1 && slot_token(ib, s, chunk, chunk_shift, seq_len, tok);
-      if (ok[u]) {
-        load16<T>(kb + tok * D, kr[u]);
-        load16<T>(vb + tok * D, vr[u]);
-      } else {
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) kr[u][e] = vr[u][e] = 0.f;
-      }
-    }
-    float sc[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      float d = 0.f;
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) d = fmaf(qf[e], kr[u][e], d);
-      sc[u] = d;
-    }
-#pragma unroll
-    for (int off = LPR / 2; off >= 1; off >>= 1) {
-#pragma unroll
-      for (int u = 0; u < U; ++u) sc[u] += __shfl_xor(sc[u], off, kWave);
-    }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      sc[u] = ok[u] ? sc[u] : -INFINITY;
-      mx = fmaxf(mx, sc[u]);
-    }
-#pragma unroll
-    for (int off = LPR; off < kWave; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
-    const float m_new = fmaxf(m, mx);
-    if (m_new == -INFINITY) continue;  // wave-uniform: nothing valid yet
-    const float alpha = fast_exp2(m - m_new);
-    l *= alpha;
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) acc[e] *= alpha;
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const float p = fast_exp2(sc[u] - m_new);
-      l += p;
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) acc[e] = fmaf(p, vr[u][e], acc[e]);
-    }
-    m = m_new;
-  }
-
-  // Fold the RPL row groups (each holds its own rows' l and acc).
-#pragma unroll
-  for (int off = LPR; off < kWave; off <<= 1) {
-    l += __shfl_xor(l, off, kWave);
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) acc[e] += __shfl_xor(acc[e], off, kWave);
-  }
+  auto get_id = [&](int cs) { return ib[cs]; };
+  auto tok_of = [&](int s, int64_t& tok) {
+    return slot_token_of(get_id, s, chunk, chunk_shift, seq_len, tok);
+  };
+  WaveSoftmax<T, D> st;
+  st.init();
+  for (int base = s0; base < s1; base += RPL * U) attend_block<T, D, U>(st, qf, kb, vb, base, s1, grp, tok_of);
+  fold_row_groups(st);
   const int64_t p = bh * num_tiles + t;
   if (grp == 0) {
     float* dst = part_acc + p * D + col * VEC;
     if constexpr (VEC % 4 == 0) {
 #pragma unroll
       for (int e = 0; e < VEC; e += 4)
-        *reinterpret_cast<float4*>(dst + e) = make_float4(acc[e], acc[e + 1], acc[e + 2], acc[e + 3]);
+        *reinterpret_cast<float4*>(dst + e) =
+            make_float4(st.acc[e], st.acc[e + 1], st.acc[e + 2], st.acc[e + 3]);
     } else {
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) dst[e] = acc[e];
+      for (int e = 0; e < VEC; ++e) dst[e] = st.acc[e];
     }
   }
   if (lane == 0) {
-    part_ml[2 * p] = m;
-    part_ml[2 * p + 1] = l;
+    part_ml[2 * p] = st.m;
+    part_ml[2 * p + 1] = st.l;
   }
 }
 
@@ -185,13 +100,14 @@ __global__ __launch_bounds__(64) void csa_attend_generic_kernel(
   const T* __restrict__ kb = k + bh * seq_len * D;
   const T* __restrict__ vb = v + bh * seq_len * D;
   const IdxT* __restrict__ ib = idx + bh * top_k;
+  auto get_id = [&](int cs) { return ib[cs]; };
   const int total = top_k * chunk;
   const int s0 = t * tile;
   const int s1 = min(s0 + tile, total);
   float m = -INFINITY, l = 0.f;
   for (int s = s0; s < s1; ++s) {
     int64_t tok;
-    if (!slot_token(ib, s, chunk, chunk_shift, seq_len, tok)) continue;
+    if (!slot_token_of(get_id, s, chunk, chunk_shift, seq_len, tok)) continue;
     const T* kr = kb + tok * D;
     const T* vr = vb + tok * D;
     float dot = 0.f;
@@ -225,42 +141,75 @@ __global__ __launch_bounds__(64) void csa_attend_generic_kernel(
   }
 }
 
+// Block-wide reductions for 256-thread blocks.
+__device__ __forceinline__ float block_max256(float v, float* red) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  v = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  return v;
+}
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+  v = wave_sum(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  v = (red[0] + red[1]) + (red[2] + red[3]);
+  __syncthreads();
+  return v;
+}
+
 // Log-sum-exp merge of the split partials of one (b,h) (the merge pass of
 // csrc/csa_attention.cu:224-274): M = max m_t, L = sum_{l_t>0} l_t 2^(m_t-M),
 // out = sum_{l_t>0} 2^(m_t-M) acc_t / L, or 0 when L is not positive.
+// 256 threads; the tile loops carry no data-dependent branches, so their loads
+// issue back to back.  Column d is summed by G = max(1, 256 / D) thread groups.
 template <typename T>
 __global__ __launch_bounds__(256) void csa_merge_kernel(const float* __restrict__ part_ml,
                                                         const float* __restrict__ part_acc,
                                                         T* __restrict__ out, int D, int num_tiles) {
+  __shared__ float red[4];
+  __shared__ float colsum[256];
   const int64_t bh = blockIdx.x;
   const float* ml = part_ml + 2 * bh * num_tiles;
-  __shared__ float s_max, s_inv;
-  if (threadIdx.x < kWave) {
-    float mx = -INFINITY;
-    for (int t = threadIdx.x; t < num_tiles; t += kWave) mx = fmaxf(mx, ml[2 * t]);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
-    float L = 0.f;
-    for (int t = threadIdx.x; t < num_tiles; t += kWave) {
+  float mx = -INFINITY;
+  for (int t = threadIdx.x; t < num_tiles; t += 256) mx = fmaxf(mx, ml[2 * t]);
+  mx = block_max256(mx, red);
+  float L = 0.f;
+  if (mx != -INFINITY) {
+    for (int t = threadIdx.x; t < num_tiles; t += 256) {
       const float lt = ml[2 * t + 1];
-      if (lt > 0.f) L += lt * fast_exp2(ml[2 * t] - mx);
-    }
-    L = wave_sum(L);
-    if (threadIdx.x == 0) {
-      s_max = mx;
-      s_inv = L > 0.f ? 1.f / L : 0.f;
+      L += lt > 0.f ? lt * fast_exp2(ml[2 * t] - mx) : 0.f;
     }
   }
-  __syncthreads();
-  const float mx = s_max, inv = s_inv;
+  L = block_sum256(L, red);
+  const float inv = (mx != -INFINITY && L > 0.f) ? 1.f / L : 0.f;
   const float* pa = part_acc + bh * num_tiles * static_cast<int64_t>(D);
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+  const int G = D >= 256 ? 1 : 256 / D;
+  const int g = threadIdx.x / (D >= 256 ? 256 : D);
+  for (int d0 = 0; d0 < D; d0 += (D >= 256 ? 256 : D)) {
+    const int d = d0 + threadIdx.x % (D >= 256 ? 256 : D);
     float a = 0.f;
-    for (int t = 0; t < num_tiles; ++t) {
-      const float lt = ml[2 * t + 1];
-      if (lt > 0.f) a = fmaf(fast_exp2(ml[2 * t] - mx), pa[static_cast<int64_t>(t) * D + d], a);
+    if (g < G && d < D && inv > 0.f) {
+#pragma unroll 8
+      for (int t = g; t < num_tiles; t += G) {
+        const float lt = ml[2 * t + 1];
+        const float w = lt > 0.f ? fast_exp2(ml[2 * t] - mx) : 0.f;
+        a = fmaf(w, pa[static_cast<int64_t>(t) * D + d], a);
+      }
     }
-    out[bh * D + d] = from_f32<T>(a * inv);
+    if (G > 1) {
+      colsum[threadIdx.x] = a;
+      __syncthreads();
+      if (g == 0 && d < D) {
+        for (int j = 1; j < G; ++j) a += colsum[threadIdx.x + j * D];
+        out[bh * D + d] = from_f32<T>(a * inv);
+      }
+      __syncthreads();
+    } else if (d < D) {
+      out[bh * D + d] = from_f32<T>(a * inv);
+    }
   }
 }
 
@@ -273,9 +222,8 @@ __global__ __launch_bounds__(64) void csa_summary_vec_kernel(const T* __restrict
                                                              int64_t seq_len, int chunk,
                                                              int64_t summary_chunks,
                                                              int64_t chunk_begin, int64_t nreq) {
-  constexpr int VEC = Vec16<T>::N;
-  constexpr int LPR = D / VEC;
-  constexpr int RPL = kWave / LPR;
+  using L = AttendLayout<T, D>;
+  constexpr int VEC = L::VEC, LPR = L::LPR, RPL = L::RPL;
   const int lane = threadIdx.x;
   const int grp = lane / LPR;
   const int col = lane % LPR;
@@ -329,15 +277,15 @@ __global__ __launch_bounds__(64) void csa_summary_generic_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Chunk scores: score[c] = (q . summary[c]) * scale, fp32 (reference.py:54-55).
-// Summary rows are fp32: a lane loads 4 columns; R chunks per wavefront.
+// Chunk scores -> order keys of score[c] = (q . summary[c]) * scale
+// (reference.py:54-55).  Summary rows are fp32: a lane loads 4 columns; R rows
+// per wavefront.
 // ---------------------------------------------------------------------------
 template <typename T, int D, int R>
 __global__ __launch_bounds__(64) void csa_score_vec_kernel(const T* __restrict__ q,
                                                            const float* __restrict__ summary,
-                                                           float* __restrict__ scores,
-                                                           int64_t C, int64_t blocks_per_head,
-                                                           float scale) {
+                                                           uint32_t* __restrict__ keys, int64_t C,
+                                                           int64_t blocks_per_head, float scale) {
   constexpr int LPR = D / 4;
   constexpr int RPL = kWave / LPR;
   static_assert(R % RPL == 0, "R must be a multiple of rows per load");
@@ -350,27 +298,13 @@ __global__ __launch_bounds__(64) void csa_score_vec_kernel(const T* __restrict__
   float qf[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) qf[e] = to_f32(q[bh * D + col * 4 + e]);
-  const float* __restrict__ sb = summary + bh * C * D + col * 4;
   float sc[U];
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int64_t c = c0 + grp + RPL * u;
-    float a[4] = {0.f, 0.f, 0.f, 0.f};
-    if (c < C) load16<float>(sb + c * D, a);
-    float d = 0.f;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) d = fmaf(qf[e], a[e], d);
-    sc[u] = d;
-  }
-#pragma unroll
-  for (int off = LPR / 2; off >= 1; off >>= 1)
-#pragma unroll
-    for (int u = 0; u < U; ++u) sc[u] += __shfl_xor(sc[u], off, kWave);
+  score_block<D, U>(qf, summary + bh * C * D + col * 4, c0, C, grp, sc);
   if (col == 0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t c = c0 + grp + RPL * u;
-      if (c < C) scores[bh * C + c] = sc[u] * scale;
+      if (c < C) keys[bh * C + c] = order_key(sc[u] * scale);
     }
   }
 }
@@ -378,7 +312,7 @@ __global__ __launch_bounds__(64) void csa_score_vec_kernel(const T* __restrict__
 template <typename T>
 __global__ __launch_bounds__(64) void csa_score_generic_kernel(const T* __restrict__ q,
                                                                const float* __restrict__ summary,
-                                                               float* __restrict__ scores, int64_t C,
+                                                               uint32_t* __restrict__ keys, int64_t C,
                                                                int D, float scale) {
   const int64_t bh = blockIdx.x / C;
   const int64_t c = blockIdx.x % C;
@@ -386,115 +320,33 @@ __global__ __launch_bounds__(64) void csa_score_generic_kernel(const T* __restri
   for (int j = threadIdx.x; j < D; j += kWave)
     d = fmaf(to_f32(q[bh * D + j]), summary[(bh * C + c) * D + j], d);
   d = wave_sum(d);
-  if (threadIdx.x == 0) scores[bh * C + c] = d * scale;
+  if (threadIdx.x == 0) keys[bh * C + c] = order_key(d * scale);
 }
 
-// ---------------------------------------------------------------------------
-// Top-k chunk selection (torch.topk in reference.py:56, with the declared
-// tie-break: higher score first, equal scores by lower chunk id).
-// One wavefront per (b,h):
-//   * radix select (4 passes of 8 bits, LDS histograms) finds the k-th largest
-//     order key T and how many keys equal to T are needed;
-//   * keys > T are gathered (any order), then the needed keys == T in ascending
-//     chunk order (ballot + prefix popcount);
-//   * each winner's output position is its rank among the k winners.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t order_key(float x) {
-  const uint32_t u = __float_as_uint(x);
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-__global__ __launch_bounds__(64) void csa_topk_kernel(const float* __restrict__ scores,
+// Top-k per (b,h): keys -> LDS in one batch of loads (when they fit), then the
+// wavefront top-k of csa_device.hpp (register path of M keys per lane, or the
+// radix select).
+template <int M, bool kInLds>
+__global__ __launch_bounds__(64) void csa_topk_kernel(const uint32_t* __restrict__ keys,
                                                       int32_t* __restrict__ out, int64_t C, int k) {
-  extern __shared__ uint32_t lds[];
-  uint32_t* hist = lds;                                      // 256
-  uint32_t* skey = lds + 256;                                // k
-  int32_t* sidx = reinterpret_cast<int32_t*>(skey + k);      // k
-  __shared__ uint32_t s_count;
-  const int lane = threadIdx.x;
+  extern __shared__ uint64_t lds64[];
+  uint32_t* ckey = reinterpret_cast<uint32_t*>(lds64);
+  int32_t* cpos = reinterpret_cast<int32_t*>(ckey + kWave);
+  uint32_t* hist = reinterpret_cast<uint32_t*>(cpos + kWave);
+  uint32_t* skey = hist + 256;
+  int32_t* sidx = reinterpret_cast<int32_t*>(skey + k);
+  uint32_t* counter = reinterpret_cast<uint32_t*>(sidx + k);
+  uint32_t* kl = counter + 1;
   const int64_t bh = blockIdx.x;
-  const float* __restrict__ sc = scores + bh * C;
-
-  uint32_t prefix = 0, pmask = 0;
-  uint32_t need = static_cast<uint32_t>(k);  // rank of the k-th key among the candidates
-  for (int pass = 0; pass < 4; ++pass) {
-    const int shift = 24 - 8 * pass;
-    for (int b = lane; b < 256; b += kWave) hist[b] = 0;
-    __syncthreads();
-    for (int64_t i = lane; i < C; i += kWave) {
-      const uint32_t key = order_key(sc[i]);
-      if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
-    }
-    __syncthreads();
-    const uint32_t h0 = hist[4 * lane], h1 = hist[4 * lane + 1], h2 = hist[4 * lane + 2],
-                   h3 = hist[4 * lane + 3];
-    const uint32_t mine = h0 + h1 + h2 + h3;
-    uint32_t incl = mine;  // sum over lanes >= this lane (higher digits)
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-      const uint32_t t = __shfl_down(incl, off, kWave);
-      if (lane + off < kWave) incl += t;
-    }
-    uint32_t cum = incl - mine;  // keys whose digit is above this lane's bins
-    int found = -1;
-    uint32_t rest = 0;
-    const uint32_t hb[4] = {h3, h2, h1, h0};
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      if (found < 0 && cum < need && cum + hb[b] >= need) {
-        found = 4 * lane + 3 - b;
-        rest = need - cum;
-      }
-      cum += hb[b];
-    }
-    const unsigned long long bal = __ballot(found >= 0);
-    // Exactly one lane finds the digit (the candidates always number >= need);
-    // fall back to lane 0 / digit 0 rather than read an undefined lane.
-    const int src = bal ? __ffsll(static_cast<long long>(bal)) - 1 : 0;
-    const int digit = bal ? __shfl(found, src, kWave) : 0;
-    need = bal ? static_cast<uint32_t>(__shfl(static_cast<int>(rest), src, kWave)) : need;
-    need = need < 1u ? 1u : (need > static_cast<uint32_t>(k) ? static_cast<uint32_t>(k) : need);
-    prefix |= static_cast<uint32_t>(digit) << shift;
-    pmask |= 0xffu << shift;
-    __syncthreads();
-  }
-  const uint32_t T = prefix;
-  const int n_above = k - static_cast<int>(need);
-  if (lane == 0) s_count = 0;
-  __syncthreads();
-  for (int64_t i = lane; i < C; i += kWave) {
-    const uint32_t key = order_key(sc[i]);
-    if (key > T) {
-      const uint32_t pos = atomicAdd(&s_count, 1u);
-      if (pos < static_cast<uint32_t>(k)) {
-        skey[pos] = key;
-        sidx[pos] = static_cast<int32_t>(i);
-      }
-    }
-  }
-  uint32_t taken = 0;
-  for (int64_t base = 0; base < C && taken < need; base += kWave) {
-    const int64_t i = base + lane;
-    const bool eq = i < C && order_key(sc[i]) == T;
-    const unsigned long long bal = __ballot(eq);
-    const uint32_t before = static_cast<uint32_t>(__popcll(bal & ((1ull << lane) - 1ull)));
-    if (eq && taken + before < need) {
-      skey[n_above + taken + before] = T;
-      sidx[n_above + taken + before] = static_cast<int32_t>(i);
-    }
-    taken += static_cast<uint32_t>(__popcll(bal));
-  }
-  __syncthreads();
-  for (int j = lane; j < k; j += kWave) {
-    const uint32_t kj = skey[j];
-    const int32_t ij = sidx[j];
-    int r = 0;
-    for (int i = 0; i < k; ++i) {
-      const uint32_t ki = skey[i];
-      const int32_t ii = sidx[i];
-      r += (ki > kj) || (ki == kj && ii < ij);
-    }
-    out[bh * k + r] = ij;
+  const uint32_t* kg = keys + bh * C;
+  int32_t* o = out + bh * k;
+  auto emit = [&](int r, int32_t i) { o[r] = i; };
+  if constexpr (kInLds) {
+    for (int i = threadIdx.x; i < C; i += kWave) kl[i] = kg[i];
+    wave_lds_sync();
+    wave_topk<M>(kl, static_cast<int>(C), k, ckey, cpos, hist, skey, sidx, counter, emit);
+  } else {
+    wave_topk<M>(kg, static_cast<int>(C), k, ckey, cpos, hist, skey, sidx, counter, emit);
   }
 }
 
@@ -502,6 +354,7 @@ __global__ __launch_bounds__(64) void csa_topk_kernel(const float* __restrict__ 
 // Host side
 // ---------------------------------------------------------------------------
 constexpr int kMaxTopkSelect = 4096;  // LDS bound of csa_topk_kernel
+constexpr size_t kLdsBudget = 64 * 1024;
 
 int chunk_shift_of(int64_t chunk) {
   if (chunk > 0 && (chunk & (chunk - 1)) == 0) {
@@ -534,10 +387,10 @@ int launch_attend(const void* q, const void* k, const void* v, const void* idx, 
                         reinterpret_cast<uintptr_t>(v)) % 16 == 0;
 #define CSAHCA_ATTEND_VEC(DD)                                                                  \
   if (aligned && D == DD && (DD / VEC) <= kWave) {                                           \
-    csa_attend_vec_kernel<T, IdxT, (DD / VEC <= kWave ? DD : VEC), 4><<<grid, kWave, 0, stream>>>( \
-        qp, kp, vp, ip, part_ml, part_acc, S, top_k, chunk, cshift, tile, num_tiles, qscale);  \
-    CSAHCA_LAUNCH_CHECK("csa_attend_vec_kernel");                                            \
-    return CSAHCA_OK;                                                                        \
+    return launch("csa_attend_vec_kernel",                                                   \
+                  csa_attend_vec_kernel<T, IdxT, (DD / VEC <= kWave ? DD : VEC), 4>, grid,   \
+                  dim3(kWave), 0, stream, qp, kp, vp, ip, part_ml, part_acc, S, top_k, chunk, \
+                  cshift, tile, num_tiles, qscale);                                          \
   }
   CSAHCA_ATTEND_VEC(64)
   CSAHCA_ATTEND_VEC(128)
@@ -547,11 +400,9 @@ int launch_attend(const void* q, const void* k, const void* v, const void* idx, 
   const int64_t J = ceil_div(D, kWave);
 #define CSAHCA_ATTEND_GEN(JJ)                                                                  \
   if (J <= JJ) {                                                                               \
-    csa_attend_generic_kernel<T, IdxT, JJ><<<grid, kWave, 0, stream>>>(                        \
-        qp, kp, vp, ip, part_ml, part_acc, S, static_cast<int>(D), top_k, chunk, cshift, tile, \
-        num_tiles, qscale);                                                                    \
-    CSAHCA_LAUNCH_CHECK("csa_attend_generic_kernel");                                        \
-    return CSAHCA_OK;                                                                          \
+    return launch("csa_attend_generic_kernel", csa_attend_generic_kernel<T, IdxT, JJ>, grid,   \
+                  dim3(kWave), 0, stream, qp, kp, vp, ip, part_ml, part_acc, S,                \
+                  static_cast<int>(D), top_k, chunk, cshift, tile, num_tiles, qscale);         \
   }
   CSAHCA_ATTEND_GEN(1)
   CSAHCA_ATTEND_GEN(2)
@@ -564,7 +415,7 @@ int launch_attend(const void* q, const void* k, const void* v, const void* idx, 
 
 int csa_decode_impl(const void* q, const void* k, const void* v, const void* idx, void* out,
                     int dtype, int index_dtype, int64_t B, int64_t H, int64_t S, int64_t D,
-                    int64_t top_k, int64_t chunk, int64_t tile, const char* kernel_name,
+                    int64_t top_k, int64_t chunk, int64_t tile, const char* d_msg,
                     void* workspace, size_t workspace_bytes, void* stream_ptr) {
   clear_error();
   CSAHCA_REQUIRE(valid_dtype(dtype), "q, k_cache and v_cache must be float32, float64, float16 or bfloat16");
@@ -573,12 +424,12 @@ int csa_decode_impl(const void* q, const void* k, const void* v, const void* idx
   CSAHCA_REQUIRE(B >= 0 && H >= 0 && S >= 0 && D >= 0 && top_k >= 0, "negative dimension");
   CSAHCA_REQUIRE(chunk > 0, "chunk_size must be positive");
   CSAHCA_REQUIRE(tile > 0, "tile_size must be positive");
-  CSAHCA_REQUIRE(D <= 1024, kernel_name);
-  CSAHCA_REQUIRE(top_k * chunk <= INT_MAX, "top_k * chunk_size must fit in int32");
+  CSAHCA_REQUIRE(D <= 1024, d_msg);
   CSAHCA_REQUIRE(chunk <= INT_MAX && top_k <= INT_MAX, "chunk_size and top_k must fit in int32");
+  CSAHCA_REQUIRE(top_k * chunk <= INT_MAX, "top_k * chunk_size must fit in int32");
   const int64_t bh = B * H;
   if (bh == 0 || D == 0) return CSAHCA_OK;
-  CSAHCA_REQUIRE(q && k && v && out && (idx || top_k == 0), "null tensor pointer");
+  CSAHCA_REQUIRE(q && out && (S == 0 || (k && v)) && (idx || top_k == 0), "null tensor pointer");
   const int64_t total = top_k * chunk;
   const int64_t tiles = std::max<int64_t>(1, ceil_div(total, tile));
   CSAHCA_REQUIRE(bh * tiles <= INT32_MAX, "too many split-KV work items");
@@ -590,27 +441,67 @@ int csa_decode_impl(const void* q, const void* k, const void* v, const void* idx
   float* part_acc = reinterpret_cast<float*>(static_cast<char*>(workspace) + ((ml + 255) & ~size_t{255}));
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
   const int tl = static_cast<int>(std::min<int64_t>(tile, std::max<int64_t>(total, 1)));
-  // A null chunk list (top_k == 0) never dereferences idx: every slot range is empty.
+  // Stand-ins for pointers that are never dereferenced (no selected slots / no tokens).
   const void* idx_ok = idx ? idx : q;
+  const void* k_ok = k ? k : q;
+  const void* v_ok = v ? v : q;
   return dispatch_dtype(dtype, [&](auto tag) -> int {
     using T = decltype(tag);
     int rc = index_dtype == CSAHCA_I32
-                 ? launch_attend<T, int32_t>(q, k, v, idx_ok, part_ml, part_acc, bh, S, D,
+                 ? launch_attend<T, int32_t>(q, k_ok, v_ok, idx_ok, part_ml, part_acc, bh, S, D,
                                              static_cast<int>(top_k), static_cast<int>(chunk), tl,
                                              static_cast<int>(tiles), stream)
-                 : launch_attend<T, int64_t>(q, k, v, idx_ok, part_ml, part_acc, bh, S, D,
+                 : launch_attend<T, int64_t>(q, k_ok, v_ok, idx_ok, part_ml, part_acc, bh, S, D,
                                              static_cast<int>(top_k), static_cast<int>(chunk), tl,
                                              static_cast<int>(tiles), stream);
     if (rc != CSAHCA_OK) return rc;
-    const int threads = static_cast<int>(std::min<int64_t>(256, ceil_div(D, kWave) * kWave));
-    csa_merge_kernel<T><<<dim3(static_cast<uint32_t>(bh)), threads, 0, stream>>>(
-        part_ml, part_acc, static_cast<T*>(out), static_cast<int>(D), static_cast<int>(tiles));
-    CSAHCA_LAUNCH_CHECK("csa_merge_kernel");
-    return CSAHCA_OK;
+    return launch("csa_merge_kernel", csa_merge_kernel<T>, dim3(static_cast<uint32_t>(bh)), dim3(256), 0,
+                  stream, static_cast<const float*>(part_ml), static_cast<const float*>(part_acc),
+                  static_cast<T*>(out), static_cast<int>(D), static_cast<int>(tiles));
   });
 }
 
 }  // namespace
+
+// Shared with csa_step.hip: scores + top-k into out_indices using `keys` scratch.
+int csa_select_launch(const void* q, const float* summary, int32_t* out_indices, int dtype,
+                      int64_t bh, int64_t C, int64_t D, int64_t k, uint32_t* keys,
+                      hipStream_t stream) {
+  const float scale = 1.0f / sqrtf(static_cast<float>(D));
+  const bool aligned = reinterpret_cast<uintptr_t>(summary) % 16 == 0;
+  int rc = dispatch_dtype(dtype, [&](auto tag) -> int {
+    using T = decltype(tag);
+    const T* qp = static_cast<const T*>(q);
+#define CSAHCA_SCORE_VEC(DD, RR)                                                           \
+  if (aligned && D == DD) {                                                                \
+    const int64_t bph = ceil_div(C, RR);                                                   \
+    return launch("csa_score_vec_kernel", csa_score_vec_kernel<T, DD, RR>,                 \
+                  dim3(static_cast<uint32_t>(bh * bph)), dim3(kWave), 0, stream, qp,       \
+                  summary, keys, C, bph, scale);                                           \
+  }
+    CSAHCA_SCORE_VEC(64, 16)
+    CSAHCA_SCORE_VEC(128, 16)
+    CSAHCA_SCORE_VEC(256, 8)
+#undef CSAHCA_SCORE_VEC
+    return launch("csa_score_generic_kernel", csa_score_generic_kernel<T>,
+                  dim3(static_cast<uint32_t>(bh * C)), dim3(kWave), 0, stream, qp, summary, keys, C,
+                  static_cast<int>(D), scale);
+  });
+  if (rc != CSAHCA_OK) return rc;
+  const size_t base = kCandBytes + (256 + 2 * static_cast<size_t>(k) + 1) * sizeof(uint32_t);
+  const bool in_lds = base + static_cast<size_t>(C) * sizeof(uint32_t) <= kLdsBudget;
+  const size_t lds = base + (in_lds ? static_cast<size_t>(C) * sizeof(uint32_t) : 0);
+  const dim3 grid(static_cast<uint32_t>(bh));
+  const uint32_t* kp = keys;
+  const int ki = static_cast<int>(k);
+  switch (topk_regs_for(C, k) * 2 + (in_lds ? 1 : 0)) {
+    case 17: return launch("csa_topk_kernel", csa_topk_kernel<8, true>, grid, dim3(kWave), lds, stream, kp, out_indices, C, ki);
+    case 65: return launch("csa_topk_kernel", csa_topk_kernel<32, true>, grid, dim3(kWave), lds, stream, kp, out_indices, C, ki);
+    case 1: return launch("csa_topk_kernel", csa_topk_kernel<0, true>, grid, dim3(kWave), lds, stream, kp, out_indices, C, ki);
+    default: return launch("csa_topk_kernel", csa_topk_kernel<0, false>, grid, dim3(kWave), lds, stream, kp, out_indices, C, ki);
+  }
+}
+
 }  // namespace csahca
 
 using namespace csahca;
@@ -691,29 +582,26 @@ extern "C" int csahca_csa_chunk_summary(const void* k_cache, float* summary, int
     constexpr int VEC = Vec16<T>::N;
 #define CSAHCA_SUM_VEC(DD)                                                                   \
   if (aligned && head_dim == DD && DD / VEC <= kWave) {                                      \
-    csa_summary_vec_kernel<T, (DD / VEC <= kWave ? DD : VEC)><<<grid, kWave, 0, stream>>>(   \
-        kp, summary, seq_len, static_cast<int>(chunk_size), summary_chunks, chunk_begin,     \
-        num_chunks);                                                                         \
-    CSAHCA_LAUNCH_CHECK("csa_summary_vec_kernel");                                         \
-    return CSAHCA_OK;                                                                        \
+    return launch("csa_summary_vec_kernel",                                                  \
+                  csa_summary_vec_kernel<T, (DD / VEC <= kWave ? DD : VEC)>, grid,           \
+                  dim3(kWave), 0, stream, kp, summary, seq_len,                              \
+                  static_cast<int>(chunk_size), summary_chunks, chunk_begin, num_chunks);    \
   }
     CSAHCA_SUM_VEC(64)
     CSAHCA_SUM_VEC(128)
     CSAHCA_SUM_VEC(256)
     CSAHCA_SUM_VEC(512)
 #undef CSAHCA_SUM_VEC
-    csa_summary_generic_kernel<T><<<grid, kWave, 0, stream>>>(
-        kp, summary, seq_len, static_cast<int>(head_dim), static_cast<int>(chunk_size),
-        summary_chunks, chunk_begin, num_chunks);
-    CSAHCA_LAUNCH_CHECK("csa_summary_generic_kernel");
-    return CSAHCA_OK;
+    return launch("csa_summary_generic_kernel", csa_summary_generic_kernel<T>, grid, dim3(kWave),
+                  0, stream, kp, summary, seq_len, static_cast<int>(head_dim),
+                  static_cast<int>(chunk_size), summary_chunks, chunk_begin, num_chunks);
   });
 }
 
 extern "C" size_t csahca_csa_select_workspace_bytes(int64_t batch, int64_t heads,
                                                     int64_t num_chunks) {
   if (batch < 0 || heads < 0 || num_chunks < 0) return 0;
-  return static_cast<size_t>(batch * heads * num_chunks) * sizeof(float);
+  return static_cast<size_t>(batch * heads * num_chunks) * sizeof(uint32_t);
 }
 
 extern "C" int csahca_csa_select_topk(const void* q, const float* summary, int32_t* out_indices,
@@ -728,6 +616,7 @@ extern "C" int csahca_csa_select_topk(const void* q, const float* summary, int32
   CSAHCA_REQUIRE(head_dim <= 1024, "head_dim > 1024 is not supported");
   const int64_t k = std::min(top_k, num_chunks);
   CSAHCA_REQUIRE(k <= kMaxTopkSelect, "top_k > 4096 is not supported by the selection kernel");
+  CSAHCA_REQUIRE(num_chunks <= INT_MAX, "num_chunks must fit in int32");
   const int64_t bh = batch * heads;
   if (bh == 0 || k == 0) return CSAHCA_OK;
   CSAHCA_REQUIRE(q && summary && out_indices, "null tensor pointer");
@@ -735,34 +624,6 @@ extern "C" int csahca_csa_select_topk(const void* q, const float* summary, int32
   const size_t need = csahca_csa_select_workspace_bytes(batch, heads, num_chunks);
   if (workspace == nullptr || workspace_bytes < need)
     return fail(CSAHCA_ERR_WORKSPACE, "workspace too small for csa select");
-  float* scores = static_cast<float*>(workspace);
-  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
-  const float scale = 1.0f / sqrtf(static_cast<float>(head_dim));
-  const bool aligned = reinterpret_cast<uintptr_t>(summary) % 16 == 0;
-  int rc = dispatch_dtype(dtype, [&](auto tag) -> int {
-    using T = decltype(tag);
-    const T* qp = static_cast<const T*>(q);
-#define CSAHCA_SCORE_VEC(DD, RR)                                                           \
-  if (aligned && head_dim == DD) {                                                         \
-    const int64_t bph = ceil_div(num_chunks, RR);                                          \
-    csa_score_vec_kernel<T, DD, RR><<<dim3(static_cast<uint32_t>(bh * bph)), kWave, 0,     \
-                                      stream>>>(qp, summary, scores, num_chunks, bph, scale); \
-    CSAHCA_LAUNCH_CHECK("csa_score_vec_kernel");                                         \
-    return CSAHCA_OK;                                                                      \
-  }
-    CSAHCA_SCORE_VEC(64, 16)
-    CSAHCA_SCORE_VEC(128, 16)
-    CSAHCA_SCORE_VEC(256, 8)
-#undef CSAHCA_SCORE_VEC
-    csa_score_generic_kernel<T><<<dim3(static_cast<uint32_t>(bh * num_chunks)), kWave, 0, stream>>>(
-        qp, summary, scores, num_chunks, static_cast<int>(head_dim), scale);
-    CSAHCA_LAUNCH_CHECK("csa_score_generic_kernel");
-    return CSAHCA_OK;
-  });
-  if (rc != CSAHCA_OK) return rc;
-  const size_t lds = (256 + 2 * static_cast<size_t>(k)) * sizeof(uint32_t);
-  csa_topk_kernel<<<dim3(static_cast<uint32_t>(bh)), kWave, lds, stream>>>(
-      scores, out_indices, num_chunks, static_cast<int>(k));
-  CSAHCA_LAUNCH_CHECK("csa_topk_kernel");
-  return CSAHCA_OK;
+  return csa_select_launch(q, summary, out_indices, dtype, bh, num_chunks, head_dim, k,
+                           static_cast<uint32_t*>(workspace), static_cast<hipStream_t>(stream_ptr));
 }

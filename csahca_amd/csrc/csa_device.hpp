@@ -1,0 +1,348 @@
+// csa_device.hpp -- wavefront-level building blocks of the CSA decode kernels.
+#pragma once
+
+#include "common.hpp"
+
+namespace csahca {
+
+// Order-preserving map fp32 -> uint32 (larger float -> larger key; +NaN above +inf).
+__device__ __forceinline__ uint32_t order_key(float x) {
+  const uint32_t u = __float_as_uint(x);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// Wavefront-local ordering point for LDS traffic between lanes of one wavefront.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+}
+
+// Slot s -> token of chunk ids[s / chunk] (chunk_shift >= 0 when chunk is a
+// power of two).  False when the chunk id is negative or the token is past
+// seq_len (csrc/csa_attention.cu:176-185).
+template <typename GetId>
+__device__ __forceinline__ bool slot_token_of(GetId get_id, int s, int chunk, int chunk_shift,
+                                              int64_t seq_len, int64_t& tok) {
+  int cs, off;
+  if (chunk_shift >= 0) {
+    cs = s >> chunk_shift;
+    off = s & (chunk - 1);
+  } else {
+    cs = s / chunk;
+    off = s - cs * chunk;
+  }
+  const int64_t c = static_cast<int64_t>(get_id(cs));
+  tok = c * chunk + off;
+  return c >= 0 && tok < seq_len;
+}
+
+// ---------------------------------------------------------------------------
+// Top-k over uint32 keys held in LDS, executed by ONE wavefront.
+// Declared order: larger key first, equal keys by lower position first.
+//   radix select (4 x 8-bit digits, LDS histogram) -> k-th key T and how many
+//   keys equal to T are needed; gather keys > T, then the needed T keys in
+//   ascending position (ballot + prefix popcount); rank the k winners.
+// Scratch: hist[256], skey[k], sidx[k], counter[1].  Output: out[rank] = position.
+// ---------------------------------------------------------------------------
+template <typename Out>
+__device__ void wave_topk_lds(const uint32_t* keys, int C, int k, uint32_t* hist, uint32_t* skey,
+                              int32_t* sidx, uint32_t* counter, Out out) {
+  const int lane = threadIdx.x & (kWave - 1);
+  uint32_t prefix = 0, pmask = 0;
+  uint32_t need = static_cast<uint32_t>(k);
+  for (int pass = 0; pass < 4; ++pass) {
+    const int shift = 24 - 8 * pass;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) hist[lane + kWave * b] = 0;
+    wave_lds_sync();
+    for (int i = lane; i < C; i += kWave) {
+      const uint32_t key = keys[i];
+      if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+    }
+    wave_lds_sync();
+    const uint32_t h0 = hist[4 * lane], h1 = hist[4 * lane + 1], h2 = hist[4 * lane + 2],
+                   h3 = hist[4 * lane + 3];
+    const uint32_t mine = h0 + h1 + h2 + h3;
+    uint32_t incl = mine;  // keys whose digit lies in bins owned by lanes >= this lane
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const uint32_t t = __shfl_down(incl, off, kWave);
+      if (lane + off < kWave) incl += t;
+    }
+    uint32_t cum = incl - mine;
+    int found = -1;
+    uint32_t rest = 0;
+    const uint32_t hb[4] = {h3, h2, h1, h0};
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      if (found < 0 && cum < need && cum + hb[b] >= need) {
+        found = 4 * lane + 3 - b;
+        rest = need - cum;
+      }
+      cum += hb[b];
+    }
+    const unsigned long long bal = __ballot(found >= 0);
+    const int src = bal ? __ffsll(static_cast<long long>(bal)) - 1 : 0;
+    const int digit = bal ? __shfl(found, src, kWave) : 0;
+    if (bal) need = static_cast<uint32_t>(__shfl(static_cast<int>(rest), src, kWave));
+    need = need < 1u ? 1u : (need > static_cast<uint32_t>(k) ? static_cast<uint32_t>(k) : need);
+    prefix |= static_cast<uint32_t>(digit) << shift;
+    pmask |= 0xffu << shift;
+    wave_lds_sync();
+  }
+  const uint32_t T = prefix;
+  const uint32_t n_above = static_cast<uint32_t>(k) - need;
+  if (lane == 0) *counter = 0;
+  wave_lds_sync();
+  for (int i = lane; i < C; i += kWave) {
+    const uint32_t key = keys[i];
+    if (key > T) {
+      const uint32_t pos = atomicAdd(counter, 1u);
+      if (pos < n_above) {
+        skey[pos] = key;
+        sidx[pos] = i;
+      }
+    }
+  }
+  uint32_t taken = 0;
+  for (int base = 0; base < C && taken < need; base += kWave) {
+    const int i = base + lane;
+    const bool eq = i < C && keys[i] == T;
+    const unsigned long long bal = __ballot(eq);
+    const uint32_t before = static_cast<uint32_t>(__popcll(bal & ((1ull << lane) - 1ull)));
+    if (eq && taken + before < need) {
+      skey[n_above + taken + before] = T;
+      sidx[n_above + taken + before] = i;
+    }
+    taken += static_cast<uint32_t>(__popcll(bal));
+  }
+  wave_lds_sync();
+  for (int j = lane; j < k; j += kWave) {
+    const uint32_t kj = skey[j];
+    const int32_t ij = sidx[j];
+    int r = 0;
+    for (int i = 0; i < k; ++i) {
+      const uint32_t ki = skey[i];
+      const int32_t ii = sidx[i];
+      r += (ki > kj) || (ki == kj && ii < ij);
+    }
+    out(r, ij);
+  }
+  wave_lds_sync();
+}
+
+// LDS bytes the fast top-k needs for its survivors (64 keys + 64 positions).
+constexpr int kCandBytes = 64 * 8;
+
+// ---------------------------------------------------------------------------
+// Top-k for k <= 64 built on ballots and readlane, executed by ONE wavefront.
+//   1. each lane takes the largest key of its positions (lane + 64 j);
+//   2. t = the k-th largest of those lane maxima, by a 32-step bit bisection on
+//      ballot counts (t = largest value with >= k lane maxima >= t); at least k
+//      keys are >= t, and every key of the answer is >= t;
+//   3. keys >= t are compacted into LDS in ascending position (ballot + prefix
+//      popcount);
+//   4. with n <= 64 survivors, lane j ranks survivor j against the others by
+//      readlane: rank = #{key_i > key_j or (key_i == key_j and pos_i < pos_j)}.
+// Returns false (nothing emitted) when more than 64 keys survive; the caller
+// then runs wave_topk_lds.
+// ---------------------------------------------------------------------------
+// M = keys held per lane (C <= 64 * M); all of them are loaded in one batch and
+// every later pass works from registers.
+template <int M, typename Out>
+__device__ bool wave_topk_regs(const uint32_t* keys, int C, int k, uint32_t* ckey, int32_t* cpos,
+                               Out out) {
+  const int lane = threadIdx.x & (kWave - 1);
+  uint32_t v[M];
+#pragma unroll
+  for (int j = 0; j < M; ++j) {
+    const int i = lane + kWave * j;
+    v[j] = i < C ? keys[i] : 0u;
+  }
+  uint32_t mx = 0;
+#pragma unroll
+  for (int j = 0; j < M; ++j) mx = v[j] > mx ? v[j] : mx;
+  const bool valid = lane < C;
+  uint32_t t = 0;
+#pragma unroll 8
+  for (int b = 31; b >= 0; --b) {
+    const uint32_t cand = t | (1u << b);
+    const int cnt = __popcll(__ballot(valid && mx >= cand));
+    t = cnt >= k ? cand : t;
+  }
+  int n = 0;
+#pragma unroll
+  for (int j = 0; j < M; ++j) {
+    const int i = lane + kWave * j;
+    const bool take = i < C && v[j] >= t;
+    const unsigned long long bal = __ballot(take);
+    const int pos = n + __popcll(bal & ((1ull << lane) - 1ull));
+    if (take && pos < kWave) {
+      ckey[pos] = v[j];
+      cpos[pos] = i;
+    }
+    n += __popcll(bal);
+  }
+  if (n > kWave) return false;
+  wave_lds_sync();
+  const uint32_t kj = lane < n ? ckey[lane] : 0u;
+  const int32_t pj = lane < n ? cpos[lane] : 0x7fffffff;
+  int r = 0;
+  for (int i = 0; i < n; ++i) {
+    const uint32_t ki = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(kj), i));
+    const int32_t pi = __builtin_amdgcn_readlane(pj, i);
+    r += (ki > kj) || (ki == kj && pi < pj);
+  }
+  if (lane < n && r < k) out(r, pj);
+  wave_lds_sync();
+  return true;
+}
+
+// Register-path size for a selection: keys per lane M (C <= 64 * M), or 0 for
+// the LDS radix path only.  Kernels take M as a template parameter so each
+// instantiation carries exactly one register path.
+inline int topk_regs_for(int64_t C, int64_t k) {
+  if (k > kWave) return 0;
+  if (C <= 512) return 8;
+  if (C <= 2048) return 32;
+  return 0;
+}
+
+// Top-k with the declared order: the register path when M > 0 (falling back
+// when too many keys tie around its threshold), else the LDS radix select.
+template <int M, typename Out>
+__device__ __forceinline__ void wave_topk(const uint32_t* keys, int C, int k, uint32_t* ckey,
+                                          int32_t* cpos, uint32_t* hist, uint32_t* skey,
+                                          int32_t* sidx, uint32_t* counter, Out out) {
+  if constexpr (M > 0) {
+    if (k <= kWave && wave_topk_regs<M>(keys, C, k, ckey, cpos, out)) return;
+  }
+  wave_topk_lds(keys, C, k, hist, skey, sidx, counter, out);
+}
+
+// ---------------------------------------------------------------------------
+// Online-softmax state of one wavefront over rows of a [*, D] K/V pair, with
+// the row split of csa_attend: each lane owns VEC = 16/sizeof(T) columns, a
+// wavefront-wide 16-byte load covers RPL = 64 / (D / VEC) rows.  Scores are in
+// the base-2 domain (q pre-scaled by log2(e)/sqrt(D)).
+// ---------------------------------------------------------------------------
+template <typename T, int D>
+struct AttendLayout {
+  static constexpr int VEC = Vec16<T>::N;
+  static constexpr int LPR = D / VEC;
+  static constexpr int RPL = kWave / LPR;
+  static_assert(LPR >= 1 && LPR <= kWave && (LPR & (LPR - 1)) == 0, "bad row split");
+};
+
+template <typename T, int D>
+struct WaveSoftmax {
+  static constexpr int VEC = AttendLayout<T, D>::VEC;
+  float m, l;
+  float acc[VEC];
+  __device__ __forceinline__ void init() {
+    m = -INFINITY;
+    l = 0.f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+  }
+};
+
+// Process rows base + grp + RPL*u (u < U) of the slot range [.., s1): tok_of(s,
+// tok) maps a slot to a token (false = skip).  kb/vb point at this lane's
+// columns of row 0 of the (b,h) cache.
+template <typename T, int D, int U, typename TokOf>
+__device__ __forceinline__ void attend_block(WaveSoftmax<T, D>& st, const float* qf,
+                                             const T* __restrict__ kb, const T* __restrict__ vb,
+                                             int base, int s1, int grp, TokOf tok_of) {
+  using L = AttendLayout<T, D>;
+  constexpr int VEC = L::VEC, LPR = L::LPR, RPL = L::RPL;
+  float kr[U][VEC], vr[U][VEC];
+  bool ok[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int s = base + grp + RPL * u;
+    int64_t tok = 0;
+    ok[u] = s < s1 && tok_of(s, tok);
+    if (ok[u]) {
+      load16<T>(kb + tok * D, kr[u]);
+      load16<T>(vb + tok * D, vr[u]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) kr[u][e] = vr[u][e] = 0.f;
+    }
+  }
+  float sc[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    float d = 0.f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) d = fmaf(qf[e], kr[u][e], d);
+    sc[u] = d;
+  }
+#pragma unroll
+  for (int off = LPR / 2; off >= 1; off >>= 1) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) sc[u] += __shfl_xor(sc[u], off, kWave);
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    sc[u] = ok[u] ? sc[u] : -INFINITY;
+    mx = fmaxf(mx, sc[u]);
+  }
+#pragma unroll
+  for (int off = LPR; off < kWave; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
+  const float m_new = fmaxf(st.m, mx);
+  if (m_new == -INFINITY) return;  // wavefront-uniform: nothing valid yet
+  const float alpha = fast_exp2(st.m - m_new);
+  st.l *= alpha;
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) st.acc[e] *= alpha;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const float p = fast_exp2(sc[u] - m_new);
+    st.l += p;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) st.acc[e] = fmaf(p, vr[u][e], st.acc[e]);
+  }
+  st.m = m_new;
+}
+
+// Fold the RPL row groups of a wavefront's state (afterwards every lane of
+// group 0 holds the full l and its VEC columns of acc).
+template <typename T, int D>
+__device__ __forceinline__ void fold_row_groups(WaveSoftmax<T, D>& st) {
+  using L = AttendLayout<T, D>;
+#pragma unroll
+  for (int off = L::LPR; off < kWave; off <<= 1) {
+    st.l += __shfl_xor(st.l, off, kWave);
+#pragma unroll
+    for (int e = 0; e < L::VEC; ++e) st.acc[e] += __shfl_xor(st.acc[e], off, kWave);
+  }
+}
+
+// Scores of R consecutive fp32 summary rows starting at c0 (rows >= C skipped):
+// lanes own 4 columns; returns the score of row c0 + grp + RPL*u in sc[u] on the
+// lanes with col == 0.
+template <int D, int U>
+__device__ __forceinline__ void score_block(const float* qf4, const float* __restrict__ sb,
+                                            int64_t c0, int64_t C, int grp, float* sc) {
+  constexpr int LPR = D / 4;
+  constexpr int RPL = kWave / LPR;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t c = c0 + grp + RPL * u;
+    float a[4] = {0.f, 0.f, 0.f, 0.f};
+    if (c < C) load16<float>(sb + c * D, a);
+    float d = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) d = fmaf(qf4[e], a[e], d);
+    sc[u] = d;
+  }
+#pragma unroll
+  for (int off = LPR / 2; off >= 1; off >>= 1)
+#pragma unroll
+    for (int u = 0; u < U; ++u) sc[u] += __shfl_xor(sc[u], off, kWave);
+}
+
+}  // namespace csahca

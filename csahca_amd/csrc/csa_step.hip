@@ -1,0 +1,465 @@
+// csa_step.hip -- one-launch CSA decode step for gfx950:
+//   chunk scores from cached fp32 summaries -> top-k chunk selection ->
+//   split-KV sparse attention over the selected tokens -> partial merge.
+//
+// Each (b,h) head is served by P workgroups of 4 wavefronts:
+//   A. workgroup p scores chunks [C*p/P, C*(p+1)/P) and publishes their order
+//      keys (fp32 score -> monotone uint32);
+//   B. every workgroup gathers the head's C keys into LDS and wavefront 0 runs
+//      the top-k (same keys, deterministic algorithm: identical everywhere);
+//   C. workgroup p attends the selected-token slots [T*p/P, T*(p+1)/P) (T = k *
+//      chunk) -- chunk ids from LDS, K/V rows by 16-byte lane loads -- and folds
+//      its 4 wavefronts' online-softmax states in LDS;
+//   D. the workgroup whose arrival is the P-th merges the P partials
+//      (log-sum-exp) into the output.
+// With P == 1 a workgroup owns its head and nothing crosses workgroups.
+//
+// Cross-workgroup exchange without cache maintenance: on gfx950 an agent-scope
+// fence writes back / invalidates the whole L2 of an XCD, which at hundreds of
+// workgroups costs tens of microseconds.  Instead every exchanged 32-bit value
+// travels in a 64-bit word (tag << 32 | value) written and read with
+// device-scope atomic stores/loads, which are coherent across XCDs on their
+// own.  The tag is this launch's number for the head (epoch[h] + 1, read at
+// entry; the merging workgroup publishes it as the new epoch when done), so a
+// reader accepts a word only once it belongs to the current launch and needs no
+// separate ordering; every wait is bounded (on time-out a sticky status bit is
+// set and the kernel still completes).  The arrival counter is never reset:
+// after the launch with tag t it holds t * P.
+// The workspace must be zero before the first launch.
+#include "csa_device.hpp"
+
+#include <algorithm>
+#include <climits>
+#include <cstdlib>
+#include <type_traits>
+
+namespace csahca {
+
+int csa_select_launch(const void* q, const float* summary, int32_t* out_indices, int dtype,
+                      int64_t bh, int64_t C, int64_t D, int64_t k, uint32_t* keys,
+                      hipStream_t stream);
+
+namespace {
+
+constexpr int kStepWaves = 4;
+constexpr int kStepThreads = kStepWaves * kWave;
+constexpr int kStepMaxP = 64;
+constexpr int kStepMaxK = 1024;
+constexpr size_t kStepLds = 64 * 1024;
+constexpr uint32_t kSpinLimit = 1u << 20;
+
+struct StepParams {
+  const void* q;
+  const float* summary;
+  const void* kcache;
+  const void* vcache;
+  void* out;
+  int32_t* idx_out;
+  uint32_t* status;
+  uint32_t* epoch;     // [BH]
+  uint32_t* arrive;    // [BH]
+  uint64_t* keys;      // [BH][C] tagged keys
+  uint64_t* part;      // [BH][P][D + 2] tagged partials (m, l, acc[D])
+  int64_t S;
+  int64_t C;
+  int chunk;
+  int chunk_shift;
+  int topk;
+  int P;
+  float score_scale;
+  float qscale;
+};
+
+__device__ __forceinline__ void put_tagged(uint64_t* p, uint32_t tag, uint32_t v) {
+  __hip_atomic_store(p, (static_cast<uint64_t>(tag) << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint64_t get_raw(const uint64_t* p) {
+  return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Wait (bounded) until *p carries `tag`; returns its value bits.
+__device__ __forceinline__ uint32_t wait_tagged(const uint64_t* p, uint64_t w, uint32_t tag, uint32_t* status) {
+  uint32_t it = 0;
+  while (static_cast<uint32_t>(w >> 32) != tag) {
+    __builtin_amdgcn_s_sleep(1);
+    w = get_raw(p);
+    if (++it > kSpinLimit) {
+      __hip_atomic_fetch_or(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;
+    }
+  }
+  return static_cast<uint32_t>(w);
+}
+
+template <typename T, int D, int TOPK_M>
+__global__ __launch_bounds__(kStepThreads) void csa_step_kernel(StepParams a) {
+  using L = AttendLayout<T, D>;
+  constexpr int VEC = L::VEC, LPR = L::LPR, RPL = L::RPL;
+  constexpr int SLPR = D / 4, SRPL = kWave / SLPR;  // fp32 summary rows
+  constexpr int U = 4;
+  constexpr int B8 = 8;                              // tagged key loads issued per batch
+  constexpr int kGather = 24;                        // tagged partial loads per thread per batch
+
+  // LDS: ckey[64] | cpos[64] | hist[256] | skey[k] | sidx[k] | sel[k] | count | comb |
+  //      keys[max(C, P*(D+2))] (the head's keys, later the gathered partials)
+  extern __shared__ uint64_t smem64[];
+  uint32_t* ckey = reinterpret_cast<uint32_t*>(smem64);
+  int32_t* cpos = reinterpret_cast<int32_t*>(ckey + kWave);
+  uint32_t* hist = reinterpret_cast<uint32_t*>(cpos + kWave);
+  uint32_t* skey = hist + 256;
+  int32_t* sidx = reinterpret_cast<int32_t*>(skey + a.topk);
+  int32_t* sel = sidx + a.topk;
+  uint32_t* lcount = reinterpret_cast<uint32_t*>(sel + a.topk);
+  float* comb = reinterpret_cast<float*>(lcount + 1);
+  uint32_t* keys_l = reinterpret_cast<uint32_t*>(comb + kStepWaves * (D + 2));
+  __shared__ int s_last;
+
+  const int tid = threadIdx.x;
+  const int wave = tid / kWave;
+  const int lane = tid % kWave;
+  const int P = a.P;
+  const int64_t h = blockIdx.x / P;
+  const int p = static_cast<int>(blockIdx.x % P);
+  const int64_t C = a.C;
+  const T* __restrict__ q = static_cast<const T*>(a.q) + h * D;
+
+  // This launch's tag for the head.  Every thread issues the (same-address)
+  // load; it is first consumed when phase A publishes keys, so its latency
+  // overlaps the summary loads.
+  const uint32_t tag =
+      P > 1 ? __hip_atomic_load(&a.epoch[h], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u : 0u;
+
+  // ---- A: order keys of this workgroup's chunk range ----------------------
+  {
+    const int grp = lane / SLPR, col = lane % SLPR;
+    float qf4[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) qf4[e] = to_f32(q[col * 4 + e]);
+    const float* __restrict__ sb = a.summary + h * C * D + col * 4;
+    uint64_t* kg = a.keys + h * C;
+    const int64_t c0 = C * p / P, c1 = C * (p + 1) / P;
+    for (int64_t blk = c0; blk < c1; blk += kStepWaves * SRPL * U) {
+      const int64_t base = blk + wave * SRPL * U;
+      float sc[U];
+      score_block<D, U>(qf4, sb, base, c1, grp, sc);
+      if (col == 0) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int64_t c = base + grp + SRPL * u;
+          if (c < c1) {
+            const uint32_t key = order_key(sc[u] * a.score_scale);
+            if (P > 1)
+              put_tagged(kg + c, tag, key);
+            else
+              keys_l[c] = key;
+          }
+        }
+      }
+    }
+  }
+
+  // ---- B: gather the head's keys, top-k -----------------------------------
+  if (P > 1) {
+    const uint64_t* kg = a.keys + h * C;
+    for (int64_t i0 = tid; i0 < C; i0 += kStepThreads * B8) {
+      uint64_t w[B8];
+#pragma unroll
+      for (int j = 0; j < B8; ++j) {
+        const int64_t i = i0 + j * kStepThreads;
+        w[j] = i < C ? get_raw(kg + i) : 0;
+      }
+#pragma unroll
+      for (int j = 0; j < B8; ++j) {
+        const int64_t i = i0 + j * kStepThreads;
+        if (i < C) keys_l[i] = wait_tagged(kg + i, w[j], tag, a.status);
+      }
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    int32_t* io = a.idx_out + h * a.topk;
+    const bool write_ids = (p == 0);
+    auto emit = [&](int r, int32_t i) {
+      sel[r] = i;
+      if (write_ids) io[r] = i;
+    };
+    wave_topk<TOPK_M>(keys_l, static_cast<int>(C), a.topk, ckey, cpos, hist, skey, sidx, lcount, emit);
+  }
+  __syncthreads();
+
+  // ---- C: attention over this workgroup's slots ---------------------------
+  const int nslots = a.topk * a.chunk;
+  const int s0 = static_cast<int>(static_cast<int64_t>(nslots) * p / P);
+  const int s1 = static_cast<int>(static_cast<int64_t>(nslots) * (p + 1) / P);
+  const int grp = lane / LPR, col = lane % LPR;
+  float qf[VEC];
+  load16<T>(q + col * VEC, qf);
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) qf[e] *= a.qscale;
+  const T* __restrict__ kb = static_cast<const T*>(a.kcache) + h * a.S * D + col * VEC;
+  const T* __restrict__ vb = static_cast<const T*>(a.vcache) + h * a.S * D + col * VEC;
+  auto get_id = [&](int cs) { return sel[cs]; };
+  auto tok_of = [&](int s, int64_t& tok) {
+    return slot_token_of(get_id, s, a.chunk, a.chunk_shift, a.S, tok);
+  };
+  WaveSoftmax<T, D> st;
+  st.init();
+  for (int blk = s0; blk < s1; blk += kStepWaves * RPL * U)
+    attend_block<T, D, U>(st, qf, kb, vb, blk + wave * RPL * U, s1, grp, tok_of);
+  fold_row_groups(st);
+  float* cw = comb + wave * (D + 2);
+  if (lane == 0) {
+    cw[0] = st.m;
+    cw[1] = st.l;
+  }
+  if (grp == 0) {
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) cw[2 + col * VEC + e] = st.acc[e];
+  }
+  __syncthreads();
+  float M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < kStepWaves; ++w)
+    if (comb[w * (D + 2) + 1] > 0.f) M = fmaxf(M, comb[w * (D + 2)]);
+  float Lsum = 0.f, A = 0.f;
+  const int d = tid;
+  if (M != -INFINITY) {
+#pragma unroll
+    for (int w = 0; w < kStepWaves; ++w) {
+      const float lw = comb[w * (D + 2) + 1];
+      if (lw > 0.f) {
+        const float wt = fast_exp2(comb[w * (D + 2)] - M);
+        Lsum = fmaf(wt, lw, Lsum);
+        if (d < D) A = fmaf(wt, comb[w * (D + 2) + 2 + d], A);
+      }
+    }
+  }
+  T* __restrict__ out = static_cast<T*>(a.out) + h * D;
+  if (P == 1) {
+    if (d < D) out[d] = from_f32<T>(Lsum > 0.f ? A / Lsum : 0.f);
+    return;
+  }
+
+  // ---- D: publish the partial; the P-th arrival merges --------------------
+  uint64_t* pp = a.part + (h * P + p) * static_cast<int64_t>(D + 2);
+  if (d < D) put_tagged(pp + 2 + d, tag, __float_as_uint(A));
+  if (tid == 0) {
+    put_tagged(pp, tag, __float_as_uint(M));
+    put_tagged(pp + 1, tag, __float_as_uint(Lsum));
+    const uint32_t old = __hip_atomic_fetch_add(&a.arrive[h], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = (old + 1u == tag * static_cast<uint32_t>(P));
+  }
+  __syncthreads();
+  if (!s_last) return;
+  // Gather all P partials ((m, l, acc[D]) each) into LDS in one batch of loads
+  // spread over the 256 threads, then merge from LDS.
+  const uint64_t* ph = a.part + h * P * static_cast<int64_t>(D + 2);
+  float* pb = reinterpret_cast<float*>(keys_l);
+  const int nw = P * (D + 2);
+  for (int i0 = tid; i0 < nw; i0 += kStepThreads * kGather) {
+    uint64_t w[kGather];
+#pragma unroll
+    for (int j = 0; j < kGather; ++j) {
+      const int i = i0 + j * kStepThreads;
+      w[j] = i < nw ? get_raw(ph + i) : 0;
+    }
+#pragma unroll
+    for (int j = 0; j < kGather; ++j) {
+      const int i = i0 + j * kStepThreads;
+      if (i < nw) pb[i] = __uint_as_float(wait_tagged(ph + i, w[j], tag, a.status));
+    }
+  }
+  __syncthreads();
+  // Wavefront 0: one partial per lane -> weights 2^(m_j - M) (0 for empty
+  // partials) and the total L; then every column is a branch-free dot product.
+  float* wts = comb;  // P weights, then L at [kStepMaxP]
+  if (wave == 0) {
+    const float mj = lane < P ? pb[lane * (D + 2)] : -INFINITY;
+    const float lj = lane < P ? pb[lane * (D + 2) + 1] : 0.f;
+    float mx = lj > 0.f ? mj : -INFINITY;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
+    const float w = (lj > 0.f && mx != -INFINITY) ? fast_exp2(mj - mx) : 0.f;
+    if (lane < P) wts[lane] = w;
+    const float Lt = wave_sum(w * lj);
+    if (lane == 0) wts[kStepMaxP] = Lt;
+  }
+  __syncthreads();
+  if (d < D) {
+    float AA = 0.f;
+#pragma unroll 8
+    for (int j = 0; j < P; ++j) AA = fmaf(wts[j], pb[j * (D + 2) + 2 + d], AA);
+    const float LL = wts[kStepMaxP];
+    out[d] = from_f32<T>(LL > 0.f ? AA / LL : 0.f);
+  }
+  __syncthreads();
+  if (tid == 0) __hip_atomic_store(&a.epoch[h], tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+int device_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+size_t align256(size_t n) { return (n + 255) & ~size_t{255}; }
+
+struct StepLayout {
+  size_t epoch, arrive, keys, part, total;
+};
+
+StepLayout step_layout(int64_t bh, int64_t C, int64_t D, int64_t k, int64_t chunk) {
+  StepLayout L;
+  L.epoch = 256;
+  L.arrive = L.epoch + align256(static_cast<size_t>(bh) * 4);
+  L.keys = L.arrive + align256(static_cast<size_t>(bh) * 4);
+  L.part = L.keys + align256(static_cast<size_t>(bh * C) * 8);
+  const size_t fused = static_cast<size_t>(bh * kStepMaxP * (D + 2)) * 8;
+  const int64_t tile = csahca_csa_auto_tile_size(1, bh, k, chunk);
+  const int64_t tiles = std::max<int64_t>(1, ceil_div(k * chunk, tile));
+  const size_t split = align256(static_cast<size_t>(bh * tiles * 2) * 4) + static_cast<size_t>(bh * tiles * D) * 4;
+  L.total = L.part + std::max(fused, split);
+  return L;
+}
+
+int64_t env_wgs_per_head() {
+  static int64_t v = -1;
+  if (v < 0) {
+    const char* s = std::getenv("CSAHCA_STEP_WGS_PER_HEAD");
+    v = s ? std::max<int64_t>(0, std::atoll(s)) : 0;
+  }
+  return v;
+}
+
+}  // namespace
+}  // namespace csahca
+
+using namespace csahca;
+
+extern "C" size_t csahca_csa_step_workspace_bytes(int64_t batch, int64_t heads, int64_t num_chunks,
+                                                  int64_t head_dim, int64_t top_k,
+                                                  int64_t chunk_size) {
+  if (batch < 0 || heads < 0 || num_chunks < 0 || head_dim < 0 || top_k < 0 || chunk_size <= 0) return 0;
+  const int64_t k = std::min(top_k, num_chunks);
+  return step_layout(batch * heads, num_chunks, head_dim, k, chunk_size).total;
+}
+
+extern "C" int csahca_csa_decode_step(const void* q, const void* k_cache, const void* v_cache,
+                                      const float* summary, void* out, int32_t* out_indices,
+                                      int dtype, int64_t batch, int64_t heads, int64_t seq_len,
+                                      int64_t head_dim, int64_t num_chunks, int64_t chunk_size,
+                                      int64_t top_k, void* workspace, size_t workspace_bytes,
+                                      void* stream_ptr) {
+  clear_error();
+  CSAHCA_REQUIRE(valid_dtype(dtype), "q, k_cache and v_cache must be float32, float64, float16 or bfloat16");
+  CSAHCA_REQUIRE(batch >= 0 && heads >= 0 && seq_len >= 0 && head_dim >= 0 && num_chunks >= 0,
+                 "negative dimension");
+  CSAHCA_REQUIRE(chunk_size > 0 && chunk_size <= INT_MAX, "chunk_size must be positive");
+  CSAHCA_REQUIRE(top_k >= 0, "top_k must be non-negative");
+  CSAHCA_REQUIRE(head_dim <= 1024, "head_dim > 1024 is not supported");
+  CSAHCA_REQUIRE(num_chunks <= INT_MAX && num_chunks * chunk_size <= seq_len,
+                 "summaries cover more chunks than the cache holds");
+  const int64_t k = std::min(top_k, num_chunks);
+  CSAHCA_REQUIRE(k <= 4096, "top_k > 4096 is not supported by the selection kernel");
+  CSAHCA_REQUIRE(k * chunk_size <= INT_MAX, "top_k * chunk_size must fit in int32");
+  const int64_t bh = batch * heads;
+  if (bh == 0 || head_dim == 0) return CSAHCA_OK;
+  CSAHCA_REQUIRE(q && out && summary && (k == 0 || (k_cache && v_cache && out_indices)),
+                 "null tensor pointer");
+  const StepLayout lay = step_layout(bh, num_chunks, head_dim, k, chunk_size);
+  if (workspace == nullptr || workspace_bytes < lay.total)
+    return fail(CSAHCA_ERR_WORKSPACE, "workspace too small for csa decode step");
+  char* ws = static_cast<char*>(workspace);
+  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+
+  const int ncu = device_cu_count();
+  const bool aligned = ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k_cache) |
+                         reinterpret_cast<uintptr_t>(v_cache) | reinterpret_cast<uintptr_t>(summary)) %
+                        16) == 0;
+  const bool fused_dtype = dtype == CSAHCA_BF16 || dtype == CSAHCA_F16 || dtype == CSAHCA_F32;
+  const bool fused_dim = head_dim == 64 || head_dim == 128 || head_dim == 256;
+  const size_t lds_base = kCandBytes + (256 + 3 * static_cast<size_t>(k) + 1) * 4 +
+                          static_cast<size_t>(kStepWaves * (head_dim + 2)) * 4;
+  int64_t P = env_wgs_per_head();
+  if (P == 0 && ncu > 0) P = (2 * static_cast<int64_t>(ncu)) / std::max<int64_t>(bh, 1);
+  P = std::min<int64_t>({P, kStepMaxP, ceil_div(num_chunks, 8), ceil_div(k * chunk_size, 16)});
+  P = std::max<int64_t>(1, P);
+  // keys region: the head's C keys, later (P > 1) the P gathered partials
+  const size_t lds = lds_base + static_cast<size_t>(std::max<int64_t>(num_chunks, P > 1 ? P * (head_dim + 2) : 0)) * 4;
+  if (k > 0 && k <= kStepMaxK && fused_dtype && fused_dim && aligned && ncu > 0 && lds <= kStepLds) {
+    CSAHCA_REQUIRE(bh * P <= INT32_MAX, "too many heads in one call");
+    StepParams pr;
+    pr.q = q;
+    pr.summary = summary;
+    pr.kcache = k_cache;
+    pr.vcache = v_cache;
+    pr.out = out;
+    pr.idx_out = out_indices;
+    pr.status = reinterpret_cast<uint32_t*>(ws);
+    pr.epoch = reinterpret_cast<uint32_t*>(ws + lay.epoch);
+    pr.arrive = reinterpret_cast<uint32_t*>(ws + lay.arrive);
+    pr.keys = reinterpret_cast<uint64_t*>(ws + lay.keys);
+    pr.part = reinterpret_cast<uint64_t*>(ws + lay.part);
+    pr.S = seq_len;
+    pr.C = num_chunks;
+    pr.chunk = static_cast<int>(chunk_size);
+    int shift = -1;
+    if ((chunk_size & (chunk_size - 1)) == 0) {
+      shift = 0;
+      while ((int64_t{1} << shift) < chunk_size) ++shift;
+    }
+    pr.chunk_shift = shift;
+    pr.topk = static_cast<int>(k);
+    pr.P = static_cast<int>(P);
+    pr.score_scale = 1.0f / sqrtf(static_cast<float>(head_dim));
+    pr.qscale = kLog2e / sqrtf(static_cast<float>(head_dim));
+    const dim3 grid(static_cast<uint32_t>(bh * P));
+    return dispatch_dtype(dtype, [&](auto tag) -> int {
+      using T = decltype(tag);
+      if constexpr (std::is_same_v<T, double>) {
+        return fail(CSAHCA_ERR_ARGUMENT, "unreachable");
+      } else {
+        const int m = topk_regs_for(num_chunks, k);
+#define CSAHCA_STEP_LAUNCH(DD, MM) \
+  return launch("csa_step_kernel", csa_step_kernel<T, DD, MM>, grid, dim3(kStepThreads), lds, stream, pr)
+#define CSAHCA_STEP_BY_M(DD)                          \
+  if (m == 8) CSAHCA_STEP_LAUNCH(DD, 8);             \
+  if (m == 32) CSAHCA_STEP_LAUNCH(DD, 32);           \
+  CSAHCA_STEP_LAUNCH(DD, 0);
+        if (head_dim == 64) { CSAHCA_STEP_BY_M(64) }
+        if (head_dim == 128) { CSAHCA_STEP_BY_M(128) }
+        CSAHCA_STEP_BY_M(256)
+#undef CSAHCA_STEP_BY_M
+#undef CSAHCA_STEP_LAUNCH
+      }
+    });
+  }
+  // General path: score + top-k kernels, then the split-KV decode.
+  uint32_t* keys = reinterpret_cast<uint32_t*>(ws + lay.keys);
+  if (k > 0) {
+    int rc = csa_select_launch(q, summary, out_indices, dtype, bh, num_chunks, head_dim, k, keys, stream);
+    if (rc != CSAHCA_OK) return rc;
+  }
+  const int64_t tile = csahca_csa_auto_tile_size(batch, heads, k, chunk_size);
+  return csahca_csa_decode_forward_tiled(q, k_cache, v_cache, out_indices, out, dtype, CSAHCA_I32, batch,
+                                         heads, seq_len, head_dim, k, chunk_size, tile, ws + lay.part,
+                                         lay.total - lay.part, stream);
+}
+
+extern "C" int csahca_csa_step_status(const void* workspace, uint32_t* status_out, void* stream_ptr) {
+  clear_error();
+  CSAHCA_REQUIRE(workspace && status_out, "null pointer");
+  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  hipError_t e = hipMemcpyAsync(status_out, workspace, sizeof(uint32_t), hipMemcpyDeviceToHost, stream);
+  if (e != hipSuccess) return fail_hip(e, "csahca_csa_step_status");
+  e = hipStreamSynchronize(stream);
+  if (e != hipSuccess) return fail_hip(e, "csahca_csa_step_status");
+  return CSAHCA_OK;
+}

@@ -353,15 +353,15 @@ int dsv4_run(const Dsv4Call& c) {
   return dispatch_dtype(c.dtype, [&](auto tag) -> int {
     using T = decltype(tag);
     const T* qp = static_cast<const T*>(c.q);
-    if (vec)
-      dsv4_tile_kernel<T, true><<<grid, kWave, 0, stream>>>(qp, a);
-    else
-      dsv4_tile_kernel<T, false><<<grid, kWave, 0, stream>>>(qp, a);
-    CSAHCA_LAUNCH_CHECK("dsv4_tile_kernel");
-    dsv4_merge_kernel<T><<<dim3(static_cast<uint32_t>(c.nq * c.heads)), 128, 0, stream>>>(
-        a.part_ml, a.part_acc, c.sink, static_cast<T*>(c.out), a.heads, a.num_tiles);
-    CSAHCA_LAUNCH_CHECK("dsv4_merge_kernel");
-    return CSAHCA_OK;
+    const int rc = vec ? launch("dsv4_tile_kernel", dsv4_tile_kernel<T, true>, grid, dim3(kWave), 0,
+                                stream, qp, a)
+                       : launch("dsv4_tile_kernel", dsv4_tile_kernel<T, false>, grid, dim3(kWave), 0,
+                                stream, qp, a);
+    if (rc != CSAHCA_OK) return rc;
+    return launch("dsv4_merge_kernel", dsv4_merge_kernel<T>,
+                  dim3(static_cast<uint32_t>(c.nq * c.heads)), dim3(128), 0, stream,
+                  static_cast<const float*>(a.part_ml), static_cast<const float*>(a.part_acc), c.sink,
+                  static_cast<T*>(c.out), a.heads, a.num_tiles);
   });
 }
 

@@ -1,15 +1,36 @@
-// status.cpp -- error state of the C ABI (thread-local last-error message).
+// status.cpp -- error state of the C ABI (thread-local last-error message) and the
+// launch profiler (per-dispatch device durations from hipExtLaunchKernel events).
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
+#include <cstring>
 #include <string>
+#include <vector>
 
 #include "common.hpp"
 
 namespace csahca {
 namespace {
 thread_local std::string g_last_error;
-}
+
+struct ProfRecord {
+  const char* name;
+  hipEvent_t start;
+  hipEvent_t stop;
+};
+struct ProfResult {
+  const char* name;
+  int64_t launches;
+  double total_ms;
+  double min_ms;
+  double max_ms;
+};
+thread_local bool g_prof_on = false;
+thread_local std::vector<hipEvent_t> g_pool;
+thread_local size_t g_pool_used = 0;
+thread_local std::vector<ProfRecord> g_records;
+thread_local std::vector<ProfResult> g_results;
+}  // namespace
 
 int fail(int code, const char* msg) {
   g_last_error = msg ? msg : "";
@@ -26,8 +47,74 @@ int fail_hip(hipError_t err, const char* where) {
 
 void clear_error() { g_last_error.clear(); }
 
+bool profiling_active() { return g_prof_on; }
+
+bool profile_take_events(hipEvent_t* start, hipEvent_t* stop) {
+  while (g_pool.size() < g_pool_used + 2) {
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return false;
+    g_pool.push_back(e);
+  }
+  *start = g_pool[g_pool_used++];
+  *stop = g_pool[g_pool_used++];
+  return true;
+}
+
+void profile_record(const char* name, hipEvent_t start, hipEvent_t stop) {
+  g_records.push_back(ProfRecord{name, start, stop});
+}
+
 }  // namespace csahca
 
-extern "C" const char* csahca_last_error(void) { return csahca::g_last_error.c_str(); }
+using namespace csahca;
+
+extern "C" const char* csahca_last_error(void) { return g_last_error.c_str(); }
 
 extern "C" int csahca_abi_version(void) { return 1; }
+
+extern "C" int csahca_profile_begin(void) {
+  g_records.clear();
+  g_results.clear();
+  g_pool_used = 0;
+  g_prof_on = true;
+  return CSAHCA_OK;
+}
+
+extern "C" int csahca_profile_end(void) {
+  g_prof_on = false;
+  g_results.clear();
+  for (const ProfRecord& r : g_records) {
+    const hipError_t e = hipEventSynchronize(r.stop);
+    if (e != hipSuccess) return -fail_hip(e, "csahca_profile_end");
+    float ms = 0.f;
+    const hipError_t e2 = hipEventElapsedTime(&ms, r.start, r.stop);
+    if (e2 != hipSuccess) return -fail_hip(e2, "csahca_profile_end");
+    ProfResult* slot = nullptr;
+    for (ProfResult& p : g_results)
+      if (std::strcmp(p.name, r.name) == 0) slot = &p;
+    if (slot == nullptr) {
+      g_results.push_back(ProfResult{r.name, 0, 0.0, 1e30, 0.0});
+      slot = &g_results.back();
+    }
+    slot->launches += 1;
+    slot->total_ms += ms;
+    if (ms < slot->min_ms) slot->min_ms = ms;
+    if (ms > slot->max_ms) slot->max_ms = ms;
+  }
+  g_records.clear();
+  g_pool_used = 0;
+  return static_cast<int>(g_results.size());
+}
+
+extern "C" int csahca_profile_result(int i, const char** name, int64_t* launches, double* total_ms,
+                                     double* min_ms, double* max_ms) {
+  if (i < 0 || static_cast<size_t>(i) >= g_results.size())
+    return fail(CSAHCA_ERR_ARGUMENT, "profile result index out of range");
+  const ProfResult& p = g_results[static_cast<size_t>(i)];
+  if (name) *name = p.name;
+  if (launches) *launches = p.launches;
+  if (total_ms) *total_ms = p.total_ms;
+  if (min_ms) *min_ms = p.min_ms;
+  if (max_ms) *max_ms = p.max_ms;
+  return CSAHCA_OK;
+}

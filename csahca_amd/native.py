@@ -54,6 +54,13 @@ _SIGNATURES = {
     "csahca_dsv4_sparse_decode_forward": (
         _int, [_vp, _int, _i64, _i64, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i64, _vp,
                _i64, _vp, _vp, _dbl, _vp, _vp, _sz, _vp]),
+    "csahca_csa_step_workspace_bytes": (_sz, [_i64] * 6),
+    "csahca_csa_decode_step": (_int, [_vp] * 6 + [_int] + [_i64] * 7 + [_vp, _sz, _vp]),
+    "csahca_csa_step_status": (_int, [_vp, ctypes.POINTER(ctypes.c_uint32), _vp]),
+    "csahca_profile_begin": (_int, []),
+    "csahca_profile_end": (_int, []),
+    "csahca_profile_result": (_int, [_int, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_i64),
+                                     ctypes.POINTER(_dbl), ctypes.POINTER(_dbl), ctypes.POINTER(_dbl)]),
 }
 
 EXPORTED = tuple(_SIGNATURES)
@@ -233,13 +240,67 @@ def csa_select_topk(q, summary, top_k):
     return out
 
 
+_STEP_WS: dict = {}
+
+
+def _step_workspace(nbytes: int, device, signature: tuple) -> torch.Tensor:
+    """Step workspace kept per (device, stream).  The fused step keeps per-head
+    launch epochs and arrival counters in it, laid out by the problem shape, so
+    it is zero-filled (a fill kernel) whenever it is created or the shape changes."""
+    key = (device.index, _stream())
+    ent = _STEP_WS.get(key)
+    if ent is None or ent[0].numel() < nbytes:
+        ent = [torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device), signature]
+        _STEP_WS[key] = ent
+    elif ent[1] != signature:
+        ent[0].zero_()
+        ent[1] = signature
+    return ent[0]
+
+
 def csa_decode_step(q, k_cache, v_cache, summary, chunk_size, top_k, tile_size: int = 0):
-    """One CSA decode step from cached summaries: select the top-k chunks, then
-    attend over their tokens.  Returns ``(out, chunk_indices)``."""
-    idx = csa_select_topk(q, summary, top_k)
-    B, H, _ = q.shape
-    ts = int(tile_size) if tile_size and tile_size > 0 else csa_auto_tile_size(B, H, idx.shape[-1], chunk_size)
-    return csa_decode_forward_tiled(q, k_cache, v_cache, idx, chunk_size, ts), idx
+    """One CSA decode step from cached summaries in one launch: select the top-k
+    chunks (as csa_select_topk), then attend over their tokens (as
+    csa_decode_forward).  Returns ``(out, chunk_indices)``.
+
+    ``tile_size`` > 0 runs the two-pass route instead (selection kernels, then
+    the split-KV op with that split size)."""
+    chunk_size, top_k = int(chunk_size), int(top_k)
+    if tile_size and tile_size > 0:
+        idx = csa_select_topk(q, summary, top_k)
+        return csa_decode_forward_tiled(q, k_cache, v_cache, idx, chunk_size, int(tile_size)), idx
+    _csa_checks(q, k_cache, v_cache, torch.empty((q.shape[0], q.shape[1], 0), dtype=torch.int32, device=q.device),
+                chunk_size, tiled=False)
+    _check(summary.is_cuda and summary.is_contiguous() and summary.dtype == torch.float32 and summary.dim() == 4,
+           "summary must be a contiguous fp32 [batch, heads, chunks, head_dim] CUDA tensor")
+    B, H, D = q.shape
+    S = k_cache.shape[2]
+    _check(tuple(summary.shape[:2]) == (B, H) and summary.shape[3] == D, "summary shape must match q")
+    C = summary.shape[2]
+    _check(top_k >= 0, "top_k must be non-negative")
+    k = min(top_k, C)
+    with torch.cuda.device(q.device):
+        out = torch.empty_like(q)
+        idx = torch.empty((B, H, k), dtype=torch.int32, device=q.device)
+        ws = _step_workspace(lib().csahca_csa_step_workspace_bytes(B, H, C, D, top_k, chunk_size), q.device,
+                             (B * H, C, D, k, chunk_size))
+        _rc(lib().csahca_csa_decode_step(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(summary), _ptr(out), _ptr(idx),
+                                         _DTYPES[q.dtype], B, H, S, D, C, chunk_size, top_k, _ptr(ws), ws.numel(),
+                                         _stream()))
+    return out, idx
+
+
+def csa_step_status(device=None) -> dict:
+    """Sticky status words of this process's step workspaces (0 = healthy)."""
+    out = {}
+    for key, (ws, _sig) in _STEP_WS.items():
+        if device is not None and key[0] != torch.device(device).index:
+            continue
+        val = ctypes.c_uint32(0)
+        with torch.cuda.device(ws.device):
+            _rc(lib().csahca_csa_step_status(_ptr(ws), ctypes.byref(val), _stream()))
+        out[key] = val.value
+    return out
 
 
 # ---------------------------------------------------------------------------
@@ -390,3 +451,32 @@ def dsv4_sparse_decode_forward(q, paged_k_cache_u8, token_indices, topk_lengths,
             extra_token_indices.shape[1], _ptr(_opt(extra_topk_lengths)), _ptr(_opt(attn_sink)),
             float(softmax_scale), _ptr(out), _ptr(ws), ws.numel(), _stream()))
     return out
+
+
+# ---------------------------------------------------------------------------
+# Launch profiler
+# ---------------------------------------------------------------------------
+class profile_launches:
+    """Context manager: per-kernel device durations of the library's launches on
+    this thread (hipExtLaunchKernel start/stop events).  After the block,
+    ``.results`` maps kernel name -> dict(launches, total_ms, min_ms, max_ms,
+    avg_us)."""
+
+    def __enter__(self):
+        _rc(lib().csahca_profile_begin())
+        self.results = {}
+        return self
+
+    def __exit__(self, *exc):
+        n = lib().csahca_profile_end()
+        if n < 0:
+            raise RuntimeError(lib().csahca_last_error().decode())
+        for i in range(n):
+            name = ctypes.c_char_p()
+            cnt = _i64()
+            tot, mn, mx = _dbl(), _dbl(), _dbl()
+            _rc(lib().csahca_profile_result(i, ctypes.byref(name), ctypes.byref(cnt), ctypes.byref(tot),
+                                            ctypes.byref(mn), ctypes.byref(mx)))
+            self.results[name.value.decode()] = dict(launches=cnt.value, total_ms=tot.value, min_ms=mn.value,
+                                                     max_ms=mx.value, avg_us=1e3 * tot.value / max(cnt.value, 1))
+        return False

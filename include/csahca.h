@@ -112,6 +112,30 @@ int csahca_csa_select_topk(const void* q, const float* summary, int32_t* out_ind
                            int64_t batch, int64_t heads, int64_t num_chunks, int64_t head_dim,
                            int64_t top_k, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Workspace for csahca_csa_decode_step. */
+size_t csahca_csa_step_workspace_bytes(int64_t batch, int64_t heads, int64_t num_chunks,
+                                       int64_t head_dim, int64_t top_k, int64_t chunk_size);
+
+/* One CSA decode step in a single launch (new op; it fuses select_topk_chunks,
+ * hybrid_attention/reference.py:48-56 with the summaries cached, and the
+ * csa_decode_forward_tiled op, csrc/csa_attention.cu:387-452): selects
+ * min(top_k, num_chunks) chunks from summary [batch, heads, num_chunks,
+ * head_dim] exactly as csahca_csa_select_topk (ids to out_indices), then writes
+ * the sparse attention over their tokens to out, as csahca_csa_decode_forward.
+ * num_chunks * chunk_size <= seq_len.  The workspace must be zero-filled before
+ * its first use; every completed call leaves it reusable.  One workspace must
+ * not be shared by calls that can run concurrently (e.g. on two streams). */
+int csahca_csa_decode_step(const void* q, const void* k_cache, const void* v_cache,
+                           const float* summary, void* out, int32_t* out_indices, int dtype,
+                           int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
+                           int64_t num_chunks, int64_t chunk_size, int64_t top_k,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
+/* Reads the step workspace's sticky status word (0 = healthy; bit 0 = a
+ * workgroup hand-off timed out, so a result may be wrong) into host memory;
+ * synchronises the stream. */
+int csahca_csa_step_status(const void* workspace, uint32_t* status_out, void* stream);
+
 /* ------------------------------------------------------------------------- */
 /* DSV4: MQA decode over the paged FP8 latent cache                           */
 /* ------------------------------------------------------------------------- */
@@ -158,6 +182,20 @@ int csahca_dsv4_sparse_decode_forward(
     const int32_t* extra_token_indices, int64_t extra_topk_slots,
     const int32_t* extra_topk_lengths, const float* attn_sink, double softmax_scale, void* out,
     void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------- */
+/* Launch profiler (measurement aid; no counterpart in the reference)         */
+/* ------------------------------------------------------------------------- */
+
+/* Between begin and end, every kernel this thread launches through the library
+ * carries a start/stop HIP event pair (hipExtLaunchKernel), which timestamps the
+ * dispatch itself -- the same interval a kernel trace reports.  end waits for
+ * those kernels and folds the durations per kernel name; it returns the number
+ * of distinct kernels (or a negative status).  Not for use under graph capture. */
+int csahca_profile_begin(void);
+int csahca_profile_end(void);
+int csahca_profile_result(int index, const char** kernel_name, int64_t* launches,
+                          double* total_ms, double* min_ms, double* max_ms);
 
 #ifdef __cplusplus
 }

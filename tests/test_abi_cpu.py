@@ -27,7 +27,7 @@ def lib():
 
 def test_exports_every_header_symbol(lib):
     syms = header_symbols()
-    assert len(syms) >= 13
+    assert len(syms) >= 19
     raw = ctypes.CDLL(str(native.library_path()))
     for s in syms:
         assert hasattr(raw, s), s

@@ -272,3 +272,55 @@ def test_cuda_graph_replays_match_eager():
         assert torch.equal(gout, eager_out)
         native.csa_decode_step(q, k, v, summ, 64, 8)  # eager work between replays
         torch.cuda.synchronize()
+
+
+FUSED = [
+    # B, H, S, D, chunk, k, dtype      (P = workgroups per head follows from B*H)
+    (1, 8, 32768, 128, 64, 8, torch.bfloat16),     # headline: P = 32
+    (1, 8, 32768, 128, 64, 32, torch.bfloat16),
+    (2, 8, 8192, 128, 64, 8, torch.bfloat16),
+    (8, 8, 8192, 128, 64, 16, torch.bfloat16),     # P = 8
+    (32, 8, 4096, 128, 64, 8, torch.bfloat16),     # P = 2
+    (64, 8, 2048, 128, 64, 4, torch.bfloat16),     # P = 1: one workgroup per head
+    (1, 4, 8192, 64, 64, 8, torch.float16),
+    (1, 2, 8192, 256, 32, 12, torch.float32),
+    (1, 1, 1048576, 64, 64, 8, torch.bfloat16),    # 16384 chunks: keys stay in global memory
+    (1, 2, 4096, 96, 64, 4, torch.bfloat16),       # head_dim 96: two-pass fallback inside the op
+    (1, 2, 4096, 128, 64, 4, torch.float64),       # fp64: two-pass fallback
+    (1, 2, 32768, 128, 16, 2000, torch.bfloat16),  # k > 1024: two-pass fallback
+    (1, 2, 2048, 128, 64, 50, torch.bfloat16),     # k > C clamps to C
+]
+
+
+@pytest.mark.parametrize("B,H,S,D,chunk,k,dtype", FUSED)
+def test_fused_step_matches_oracle_and_two_pass(B, H, S, D, chunk, k, dtype):
+    g = torch.Generator().manual_seed(B * 7 + H * 3 + k + D)
+    q = torch.randn(B, H, D, generator=g).to(dtype)
+    kc = torch.randn(B, H, S, D, generator=g).to(dtype)
+    vc = torch.randn(B, H, S, D, generator=g).to(dtype)
+    qd, kd, vd = q.to(DEV), kc.to(DEV), vc.to(DEV)
+    summ = extension.csa_chunk_summary(kd, chunk)
+    out, idx = native.csa_decode_step(qd, kd, vd, summ, chunk, k)
+    idx2 = extension.csa_select_topk(qd, summ, k)
+    assert torch.equal(idx, idx2)
+    want, scores = oracle.select_topk(q, summ.cpu(), k)
+    assert_indices(idx, want, scores)
+    atol, rtol = tol_for(dtype)
+    if B * H * S * D <= 64 * 8 * 2048 * 128:
+        ref = oracle.csa_attend(q, kc, vc, idx.cpu(), chunk, prob_dtype=oracle.F32)
+        assert_close(out, ref, atol, rtol, "fused vs oracle")
+    two = extension.csa_decode_forward_tiled(qd, kd, vd, idx, chunk, 16)
+    assert torch.allclose(out.float(), two.float(), atol=atol, rtol=rtol)
+    assert all(v == 0 for v in native.csa_step_status().values())
+
+
+def test_fused_step_repeated_calls_rearm_counters():
+    case = make_synthetic_case(batch=1, heads=8, seq_len=32768, head_dim=128, chunk_size=64, top_k=8, seed=1)
+    q, k, v = case.q.to(DEV), case.k_cache.to(DEV), case.v_cache.to(DEV)
+    summ = extension.csa_chunk_summary(k, 64)
+    first, idx = native.csa_decode_step(q, k, v, summ, 64, 8)
+    for _ in range(50):
+        out, idx2 = native.csa_decode_step(q, k, v, summ, 64, 8)
+    torch.cuda.synchronize()
+    assert torch.equal(out, first) and torch.equal(idx2, idx)
+    assert all(v == 0 for v in native.csa_step_status().values())
