@@ -330,9 +330,8 @@ template <int M, bool kInLds>
 __global__ __launch_bounds__(64) void csa_topk_kernel(const uint32_t* __restrict__ keys,
                                                       int32_t* __restrict__ out, int64_t C, int k) {
   extern __shared__ uint64_t lds64[];
-  uint32_t* ckey = reinterpret_cast<uint32_t*>(lds64);
-  int32_t* cpos = reinterpret_cast<int32_t*>(ckey + kWave);
-  uint32_t* hist = reinterpret_cast<uint32_t*>(cpos + kWave);
+  uint32_t* scratch = reinterpret_cast<uint32_t*>(lds64);
+  uint32_t* hist = scratch + kTopkScratchWords;
   uint32_t* skey = hist + 256;
   int32_t* sidx = reinterpret_cast<int32_t*>(skey + k);
   uint32_t* counter = reinterpret_cast<uint32_t*>(sidx + k);
@@ -344,9 +343,9 @@ __global__ __launch_bounds__(64) void csa_topk_kernel(const uint32_t* __restrict
   if constexpr (kInLds) {
     for (int i = threadIdx.x; i < C; i += kWave) kl[i] = kg[i];
     wave_lds_sync();
-    wave_topk<M>(kl, static_cast<int>(C), k, ckey, cpos, hist, skey, sidx, counter, emit);
+    wave_topk<M>(kl, static_cast<int>(C), k, scratch, hist, skey, sidx, counter, emit);
   } else {
-    wave_topk<M>(kg, static_cast<int>(C), k, ckey, cpos, hist, skey, sidx, counter, emit);
+    wave_topk<M>(kg, static_cast<int>(C), k, scratch, hist, skey, sidx, counter, emit);
   }
 }
 

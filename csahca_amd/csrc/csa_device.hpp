@@ -11,6 +11,12 @@ __device__ __forceinline__ uint32_t order_key(float x) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
+// Number of set bits of a ballot below this lane (v_mbcnt_lo/hi).
+__device__ __forceinline__ int lanes_below(unsigned long long bal) {
+  return static_cast<int>(__builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(bal >> 32),
+                                                    __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal), 0u)));
+}
+
 // Wavefront-local ordering point for LDS traffic between lanes of one wavefront.
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
@@ -109,7 +115,7 @@ __device__ void wave_topk_lds(const uint32_t* keys, int C, int k, uint32_t* hist
     const int i = base + lane;
     const bool eq = i < C && keys[i] == T;
     const unsigned long long bal = __ballot(eq);
-    const uint32_t before = static_cast<uint32_t>(__popcll(bal & ((1ull << lane) - 1ull)));
+    const uint32_t before = static_cast<uint32_t>(lanes_below(bal));
     if (eq && taken + before < need) {
       skey[n_above + taken + before] = T;
       sidx[n_above + taken + before] = i;
@@ -131,69 +137,149 @@ __device__ void wave_topk_lds(const uint32_t* keys, int C, int k, uint32_t* hist
   wave_lds_sync();
 }
 
-// LDS bytes the fast top-k needs for its survivors (64 keys + 64 positions).
-constexpr int kCandBytes = 64 * 8;
+// LDS scratch of the register-path top-k: 64 candidate composites (u64) and
+// one dummy slot that absorbs the stores of lanes without a candidate.
+constexpr int kTopkScratchWords = 2 * (64 + 1);
+constexpr int kCandBytes = kTopkScratchWords * 4;
+
+// Value held by lane (lane ^ D), D a power of two below 64, with no LDS
+// traffic: DPP quad permutes for 1 and 2, a half-row mirror (lane ^ 7) then a
+// quad reverse (lane ^ 3) for 4, a row rotate by 8 for 8, and the gfx950 row
+// swaps for 16 and 32 (v_permlane16/32_swap exchange the odd half of the first
+// operand with the even half of the second, so with both operands = x the
+// first result holds the even rows twice and the second the odd rows twice).
+template <int Ctrl>
+__device__ __forceinline__ uint32_t dpp_mov(uint32_t x) {
+  return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), Ctrl, 0xF, 0xF, false));
+}
+
+template <int D>
+__device__ __forceinline__ uint32_t lane_xor(uint32_t x, int lane) {
+  if constexpr (D == 1) {
+    return dpp_mov<0xB1>(x);  // quad_perm [1,0,3,2]
+  } else if constexpr (D == 2) {
+    return dpp_mov<0x4E>(x);  // quad_perm [2,3,0,1]
+  } else if constexpr (D == 4) {
+    return dpp_mov<0x1B>(dpp_mov<0x141>(x));  // quad_perm [3,2,1,0] after row_half_mirror
+  } else if constexpr (D == 8) {
+    return dpp_mov<0x128>(x);  // row_ror:8
+  } else if constexpr (D == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return (lane & 16) ? r[0] : r[1];
+  } else {
+    static_assert(D == 32, "lane_xor: D must be a power of two below 64");
+    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return (lane & 32) ? r[0] : r[1];
+  }
+}
+
+// Compare-exchange at distance D keeping the larger value in the lower lane.
+template <int D>
+__device__ __forceinline__ uint32_t cx_desc(uint32_t x, int lane) {
+  const uint32_t p = lane_xor<D>(x, lane);
+  return (lane & D) ? (x < p ? x : p) : (x < p ? p : x);
+}
+
+template <int D>
+__device__ __forceinline__ uint32_t merge_desc(uint32_t x, int lane) {
+  x = cx_desc<D>(x, lane);
+  if constexpr (D > 1) x = merge_desc<D / 2>(x, lane);
+  return x;
+}
+
+// All-ones in lanes whose bit B is set.
+template <int B>
+__device__ __forceinline__ uint32_t lane_bit_mask(int lane) {
+  return static_cast<uint32_t>(-((lane >> B) & 1));
+}
+
+// Sorts one value per lane across the wavefront, largest in lane 0: a bitonic
+// network whose blocks of size S end descending where (lane & S) == 0 and
+// ascending elsewhere.  Lanes of ascending blocks hold the complement (which
+// reverses the order), so every compare-exchange keeps the larger value in
+// the lower lane; the complement pattern is switched between stages.
+__device__ __forceinline__ uint32_t wave_sort_desc(uint32_t x, int lane) {
+  x ^= lane_bit_mask<1>(lane);
+  x = merge_desc<1>(x, lane);
+  x ^= lane_bit_mask<1>(lane) ^ lane_bit_mask<2>(lane);
+  x = merge_desc<2>(x, lane);
+  x ^= lane_bit_mask<2>(lane) ^ lane_bit_mask<3>(lane);
+  x = merge_desc<4>(x, lane);
+  x ^= lane_bit_mask<3>(lane) ^ lane_bit_mask<4>(lane);
+  x = merge_desc<8>(x, lane);
+  x ^= lane_bit_mask<4>(lane) ^ lane_bit_mask<5>(lane);
+  x = merge_desc<16>(x, lane);
+  x ^= lane_bit_mask<5>(lane);
+  return merge_desc<32>(x, lane);
+}
 
 // ---------------------------------------------------------------------------
-// Top-k for k <= 64 built on ballots and readlane, executed by ONE wavefront.
-//   1. each lane takes the largest key of its positions (lane + 64 j);
-//   2. t = the k-th largest of those lane maxima, by a 32-step bit bisection on
-//      ballot counts (t = largest value with >= k lane maxima >= t); at least k
-//      keys are >= t, and every key of the answer is >= t;
-//   3. keys >= t are compacted into LDS in ascending position (ballot + prefix
-//      popcount);
-//   4. with n <= 64 survivors, lane j ranks survivor j against the others by
-//      readlane: rank = #{key_i > key_j or (key_i == key_j and pos_i < pos_j)}.
-// Returns false (nothing emitted) when more than 64 keys survive; the caller
-// then runs wave_topk_lds.
+// Top-k for k <= 64, executed by ONE wavefront.  On gfx950 every dependent
+// hop between the vector and the scalar unit (a compare whose mask feeds a
+// scalar op that feeds the next vector op) costs ~100 cycles and an LDS round
+// trip ~120, so the steps avoid both:
+//   1. each lane holds M keys (positions lane + 64 j) in registers and takes
+//      their maximum;
+//   2. the 64 lane maxima are sorted by a bitonic network of lane permutes
+//      (no LDS) and t = the k-th largest lane maximum: at least k keys are
+//      >= t and every key of the answer is >= t;
+//   3. keys >= t are compacted into LDS as unique composites
+//      (key << 32 | ~position), ballot + mbcnt giving the slots;
+//   4. with n <= 64 candidates, lane j ranks composite j by counting the
+//      larger composites from broadcast reads (16 per batch, one LDS wait
+//      each); composite order is exactly the declared order (larger key
+//      first, equal keys by lower position).
+// Returns false (nothing emitted) when more than 64 keys are >= t, or when
+// t == 0 (fewer than k lanes hold a key, or keys equal to 0 decide the
+// answer); the caller then runs wave_topk_lds.
 // ---------------------------------------------------------------------------
-// M = keys held per lane (C <= 64 * M); all of them are loaded in one batch and
-// every later pass works from registers.
 template <int M, typename Out>
-__device__ bool wave_topk_regs(const uint32_t* keys, int C, int k, uint32_t* ckey, int32_t* cpos,
-                               Out out) {
+__device__ bool wave_topk_regs(const uint32_t* keys, int C, int k, uint32_t* scratch, Out out) {
   const int lane = threadIdx.x & (kWave - 1);
+  unsigned long long* cand = reinterpret_cast<unsigned long long*>(scratch);
   uint32_t v[M];
 #pragma unroll
   for (int j = 0; j < M; ++j) {
+    // Clamped load + select rather than a branch per key (C >= 1).
     const int i = lane + kWave * j;
-    v[j] = i < C ? keys[i] : 0u;
+    const uint32_t kv = keys[i < C ? i : C - 1];
+    v[j] = i < C ? kv : 0u;
   }
+  cand[lane] = 0ull;  // unused slots: below every composite (positions are < 2^31)
   uint32_t mx = 0;
 #pragma unroll
   for (int j = 0; j < M; ++j) mx = v[j] > mx ? v[j] : mx;
-  const bool valid = lane < C;
-  uint32_t t = 0;
-#pragma unroll 8
-  for (int b = 31; b >= 0; --b) {
-    const uint32_t cand = t | (1u << b);
-    const int cnt = __popcll(__ballot(valid && mx >= cand));
-    t = cnt >= k ? cand : t;
-  }
+  const uint32_t t =
+      static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(wave_sort_desc(mx, lane)), k - 1));
+  if (t == 0u) return false;
+  wave_lds_sync();  // the clears above land before any compacted store
   int n = 0;
 #pragma unroll
   for (int j = 0; j < M; ++j) {
-    const int i = lane + kWave * j;
-    const bool take = i < C && v[j] >= t;
+    // Positions past C hold key 0 < t, so no bound check is needed.  Lanes
+    // without a candidate (or past 64 candidates) store to the dummy slot.
+    const bool take = v[j] >= t;
     const unsigned long long bal = __ballot(take);
-    const int pos = n + __popcll(bal & ((1ull << lane) - 1ull));
-    if (take && pos < kWave) {
-      ckey[pos] = v[j];
-      cpos[pos] = i;
-    }
+    int slot = n + lanes_below(bal) + (take ? 0 : kWave);
+    slot = slot < kWave ? slot : kWave;
+    const uint32_t pos = static_cast<uint32_t>(lane + kWave * j);
+    cand[slot] = (static_cast<unsigned long long>(v[j]) << 32) | static_cast<uint32_t>(~pos);
     n += __popcll(bal);
   }
   if (n > kWave) return false;
   wave_lds_sync();
-  const uint32_t kj = lane < n ? ckey[lane] : 0u;
-  const int32_t pj = lane < n ? cpos[lane] : 0x7fffffff;
-  int r = 0;
-  for (int i = 0; i < n; ++i) {
-    const uint32_t ki = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(kj), i));
-    const int32_t pi = __builtin_amdgcn_readlane(pj, i);
-    r += (ki > kj) || (ki == kj && pi < pj);
+  if (lane < n) {
+    const unsigned long long cj = cand[lane];
+    int r = 0;
+    for (int b = 0; b < n; b += 16) {  // slots [n, 64) hold 0
+      ulonglong2 c2[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) c2[i] = *reinterpret_cast<const ulonglong2*>(cand + b + 2 * i);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) r += (c2[i].x > cj) + (c2[i].y > cj);
+    }
+    if (r < k) out(r, static_cast<int32_t>(~static_cast<uint32_t>(cj)));
   }
-  if (lane < n && r < k) out(r, pj);
   wave_lds_sync();
   return true;
 }
@@ -211,11 +297,11 @@ inline int topk_regs_for(int64_t C, int64_t k) {
 // Top-k with the declared order: the register path when M > 0 (falling back
 // when too many keys tie around its threshold), else the LDS radix select.
 template <int M, typename Out>
-__device__ __forceinline__ void wave_topk(const uint32_t* keys, int C, int k, uint32_t* ckey,
-                                          int32_t* cpos, uint32_t* hist, uint32_t* skey,
-                                          int32_t* sidx, uint32_t* counter, Out out) {
+__device__ __forceinline__ void wave_topk(const uint32_t* keys, int C, int k, uint32_t* scratch,
+                                          uint32_t* hist, uint32_t* skey, int32_t* sidx,
+                                          uint32_t* counter, Out out) {
   if constexpr (M > 0) {
-    if (k <= kWave && wave_topk_regs<M>(keys, C, k, ckey, cpos, out)) return;
+    if (k <= kWave && wave_topk_regs<M>(keys, C, k, scratch, out)) return;
   }
   wave_topk_lds(keys, C, k, hist, skey, sidx, counter, out);
 }

@@ -45,6 +45,8 @@ constexpr int kStepWaves = 4;
 constexpr int kStepThreads = kStepWaves * kWave;
 constexpr int kStepMaxP = 64;
 constexpr int kStepMaxK = 1024;
+constexpr int kStepScoreUnroll = 8;   // summary rows per lane per batch of loads
+constexpr int kStepAttendUnroll = 4;  // K/V row loads per lane per batch
 constexpr size_t kStepLds = 64 * 1024;
 constexpr uint32_t kSpinLimit = 1u << 20;
 
@@ -97,16 +99,15 @@ __global__ __launch_bounds__(kStepThreads) void csa_step_kernel(StepParams a) {
   using L = AttendLayout<T, D>;
   constexpr int VEC = L::VEC, LPR = L::LPR, RPL = L::RPL;
   constexpr int SLPR = D / 4, SRPL = kWave / SLPR;  // fp32 summary rows
-  constexpr int U = 4;
+  constexpr int U = kStepAttendUnroll;
   constexpr int B8 = 8;                              // tagged key loads issued per batch
   constexpr int kGather = 24;                        // tagged partial loads per thread per batch
 
-  // LDS: ckey[64] | cpos[64] | hist[256] | skey[k] | sidx[k] | sel[k] | count | comb |
+  // LDS: top-k scratch | hist[256] | skey[k] | sidx[k] | sel[k] | count | comb |
   //      keys[max(C, P*(D+2))] (the head's keys, later the gathered partials)
   extern __shared__ uint64_t smem64[];
-  uint32_t* ckey = reinterpret_cast<uint32_t*>(smem64);
-  int32_t* cpos = reinterpret_cast<int32_t*>(ckey + kWave);
-  uint32_t* hist = reinterpret_cast<uint32_t*>(cpos + kWave);
+  uint32_t* scratch = reinterpret_cast<uint32_t*>(smem64);
+  uint32_t* hist = scratch + kTopkScratchWords;
   uint32_t* skey = hist + 256;
   int32_t* sidx = reinterpret_cast<int32_t*>(skey + a.topk);
   int32_t* sel = sidx + a.topk;
@@ -139,13 +140,14 @@ __global__ __launch_bounds__(kStepThreads) void csa_step_kernel(StepParams a) {
     const float* __restrict__ sb = a.summary + h * C * D + col * 4;
     uint64_t* kg = a.keys + h * C;
     const int64_t c0 = C * p / P, c1 = C * (p + 1) / P;
-    for (int64_t blk = c0; blk < c1; blk += kStepWaves * SRPL * U) {
-      const int64_t base = blk + wave * SRPL * U;
-      float sc[U];
-      score_block<D, U>(qf4, sb, base, c1, grp, sc);
+    constexpr int US = kStepScoreUnroll;
+    for (int64_t blk = c0; blk < c1; blk += kStepWaves * SRPL * US) {
+      const int64_t base = blk + wave * SRPL * US;
+      float sc[US];
+      score_block<D, US>(qf4, sb, base, c1, grp, sc);
       if (col == 0) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
+        for (int u = 0; u < US; ++u) {
           const int64_t c = base + grp + SRPL * u;
           if (c < c1) {
             const uint32_t key = order_key(sc[u] * a.score_scale);
@@ -184,7 +186,7 @@ __global__ __launch_bounds__(kStepThreads) void csa_step_kernel(StepParams a) {
       sel[r] = i;
       if (write_ids) io[r] = i;
     };
-    wave_topk<TOPK_M>(keys_l, static_cast<int>(C), a.topk, ckey, cpos, hist, skey, sidx, lcount, emit);
+    wave_topk<TOPK_M>(keys_l, static_cast<int>(C), a.topk, scratch, hist, skey, sidx, lcount, emit);
   }
   __syncthreads();
 
@@ -387,8 +389,19 @@ extern "C" int csahca_csa_decode_step(const void* q, const void* k_cache, const 
   const bool fused_dim = head_dim == 64 || head_dim == 128 || head_dim == 256;
   const size_t lds_base = kCandBytes + (256 + 3 * static_cast<size_t>(k) + 1) * 4 +
                           static_cast<size_t>(kStepWaves * (head_dim + 2)) * 4;
+  // Workgroups per head: the smallest P at which every wavefront streams its
+  // share of summary rows and of selected K/V rows in ONE batch of loads (a
+  // dependent HBM round trip, ~1.5 us, costs more than the cross-workgroup
+  // exchange a larger P adds), capped at ~4 workgroups per CU over the grid.
   int64_t P = env_wgs_per_head();
-  if (P == 0 && ncu > 0) P = (2 * static_cast<int64_t>(ncu)) / std::max<int64_t>(bh, 1);
+  if (P == 0 && ncu > 0) {
+    const int64_t esz = dtype == CSAHCA_F32 ? 4 : 2;
+    const int64_t score_rows = int64_t{kStepWaves} * kStepScoreUnroll * std::max<int64_t>(1, kWave / (head_dim / 4));
+    const int64_t attend_rows =
+        int64_t{kStepWaves} * kStepAttendUnroll * std::max<int64_t>(1, kWave / (head_dim / (16 / esz)));
+    P = std::max(ceil_div(num_chunks, score_rows), ceil_div(k * chunk_size, attend_rows));
+    P = std::min<int64_t>(P, std::max<int64_t>(1, (4 * static_cast<int64_t>(ncu)) / std::max<int64_t>(bh, 1)));
+  }
   P = std::min<int64_t>({P, kStepMaxP, ceil_div(num_chunks, 8), ceil_div(k * chunk_size, 16)});
   P = std::max<int64_t>(1, P);
   // keys region: the head's C keys, later (P > 1) the P gathered partials
