@@ -57,6 +57,11 @@ def parse_args():
     ap.add_argument("--no-dsv4", action="store_true")
     ap.add_argument("--sweep", action="store_true", help="also run the BASELINE config-2 sweep (stderr + json)")
     ap.add_argument("--sweep-out", type=Path, default=None)
+    ap.add_argument("--no-graph", action="store_true",
+                    help="time eager launches only (for profiler counter passes, which serialise dispatches)")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run 8 plain device copies of MIB MiB (the known-size kernel that scales the "
+                         "FETCH_SIZE / WRITE_SIZE counters) and exit")
     return ap.parse_args()
 
 
@@ -163,15 +168,16 @@ def csa_bench(args, B=1, H=8, S=32768, D=128, chunk=64, top_k=8, copies=None, se
         step(i)
     torch.cuda.synchronize()
 
-    per_graph = copies
-    graph = graph_of([lambda i=i: step(i) for i in range(per_graph)])
-    rem = args.steps % per_graph
-    rem_graph = {rem: graph_of([lambda i=i: step(i) for i in range(rem)])} if rem else {}
-    ms_graph = time_graph_steps(graph, rem_graph, per_graph, args.steps)
+    graph, rem_graph = None, None
     res = dict(B=B, H=H, S=S, D=D, chunk=chunk, top_k=top_k, tile=tile, copies=copies,
-               ms_per_step_graph=ms_graph / args.steps, step_bytes=step_bytes, sel_bytes=sel_bytes,
-               summ_bytes=summ_bytes)
-    if eager:
+               step_bytes=step_bytes, sel_bytes=sel_bytes, summ_bytes=summ_bytes)
+    if not args.no_graph:
+        per_graph = copies
+        graph = graph_of([lambda i=i: step(i) for i in range(per_graph)])
+        rem = args.steps % per_graph
+        rem_graph = {rem: graph_of([lambda i=i: step(i) for i in range(rem)])} if rem else {}
+        res["ms_per_step_graph"] = time_graph_steps(graph, rem_graph, per_graph, args.steps) / args.steps
+    if eager or args.no_graph:
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for i in range(args.steps):
@@ -331,8 +337,19 @@ def main():
 
     native.lib()
     log(f"device: {torch.cuda.get_device_name(0)}")
+    if args.calibrate_copy > 0:
+        n = args.calibrate_copy * 2 ** 20
+        src = torch.empty(n // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        for _ in range(8):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy": {"bytes_read_per_launch": n, "bytes_written_per_launch": n,
+                                             "launches": 8}}), flush=True)
+        return
     r = csa_bench(args, copies=args.copies)
-    ms = r["ms_per_step_graph"]
+    ms = r["ms_per_step_eager"] if args.no_graph else r["ms_per_step_graph"]
     kern = r["kernels"]
     log("csa kernels:", json.dumps(kern))
     # dominant kernel = largest total device time
@@ -364,7 +381,7 @@ def main():
                                "summaries + split-KV attend + merge)",
                    "batch": 1, "heads": 8, "head_dim": 128, "seq_len": 32768, "chunk_size": 64, "top_k": 8,
                    "route": args.route, "tile": r["tile"] or None, "cache_copies_rotated": r["copies"],
-                   "timing": "hip graph replay",
+                   "timing": "eager launches" if args.no_graph else "hip graph replay",
                    "parallelism": "single GPU"},
         "tokens_per_s": round(1e3 / ms, 1),
         "ms_per_step_eager": round(r["ms_per_step_eager"], 6),

@@ -131,3 +131,18 @@ def test_product_package_does_not_import_oracle():
     for p in (ROOT / "csahca_amd").rglob("*.py"):
         text = p.read_text()
         assert "import oracle" not in text and "from oracle" not in text, p
+
+
+def test_reference_module_name_resolves_to_native_ops(monkeypatch):
+    """`import hybrid_attention_cuda` (hybrid_attention/extension.py:19-23) finds
+    the compat module, whose ops are the native bindings with the pybind names."""
+    import importlib
+    import sys
+
+    monkeypatch.syspath_prepend(str(ROOT / "csahca_amd" / "compat"))
+    sys.modules.pop("hybrid_attention_cuda", None)
+    mod = importlib.import_module("hybrid_attention_cuda")
+    for name in ("csa_decode_forward", "csa_decode_forward_tiled", "dsv4_swa_decode_forward",
+                 "dsv4_sparse_decode_forward", "dsv4_decode_forward_tiled"):
+        assert getattr(mod, name) is getattr(native, name)
+    sys.modules.pop("hybrid_attention_cuda", None)
