@@ -112,6 +112,37 @@ __device__ __forceinline__ void store16(T* __restrict__ p, const float* v) {
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Butterfly sums / maxima over lane groups (masks are XOR distances).
+// Value held by lane (lane ^ D), D a power of two below 64, with no LDS
+// traffic: DPP quad permutes for 1 and 2, a half-row mirror (lane ^ 7) then a
+// quad reverse (lane ^ 3) for 4, a row rotate by 8 for 8, and the gfx950 row
+// swaps for 16 and 32 (v_permlane16/32_swap exchange the odd half of the first
+// operand with the even half of the second, so with both operands = x the
+// first result holds the even rows twice and the second the odd rows twice).
+template <int Ctrl>
+__device__ __forceinline__ uint32_t dpp_mov(uint32_t x) {
+  return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), Ctrl, 0xF, 0xF, false));
+}
+
+template <int D>
+__device__ __forceinline__ uint32_t lane_xor(uint32_t x, int lane) {
+  if constexpr (D == 1) {
+    return dpp_mov<0xB1>(x);  // quad_perm [1,0,3,2]
+  } else if constexpr (D == 2) {
+    return dpp_mov<0x4E>(x);  // quad_perm [2,3,0,1]
+  } else if constexpr (D == 4) {
+    return dpp_mov<0x1B>(dpp_mov<0x141>(x));  // quad_perm [3,2,1,0] after row_half_mirror
+  } else if constexpr (D == 8) {
+    return dpp_mov<0x128>(x);  // row_ror:8
+  } else if constexpr (D == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return (lane & 16) ? r[0] : r[1];
+  } else {
+    static_assert(D == 32, "lane_xor: D must be a power of two below 64");
+    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return (lane & 32) ? r[0] : r[1];
+  }
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);

@@ -142,37 +142,6 @@ __device__ void wave_topk_lds(const uint32_t* keys, int C, int k, uint32_t* hist
 constexpr int kTopkScratchWords = 2 * (64 + 1);
 constexpr int kCandBytes = kTopkScratchWords * 4;
 
-// Value held by lane (lane ^ D), D a power of two below 64, with no LDS
-// traffic: DPP quad permutes for 1 and 2, a half-row mirror (lane ^ 7) then a
-// quad reverse (lane ^ 3) for 4, a row rotate by 8 for 8, and the gfx950 row
-// swaps for 16 and 32 (v_permlane16/32_swap exchange the odd half of the first
-// operand with the even half of the second, so with both operands = x the
-// first result holds the even rows twice and the second the odd rows twice).
-template <int Ctrl>
-__device__ __forceinline__ uint32_t dpp_mov(uint32_t x) {
-  return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), Ctrl, 0xF, 0xF, false));
-}
-
-template <int D>
-__device__ __forceinline__ uint32_t lane_xor(uint32_t x, int lane) {
-  if constexpr (D == 1) {
-    return dpp_mov<0xB1>(x);  // quad_perm [1,0,3,2]
-  } else if constexpr (D == 2) {
-    return dpp_mov<0x4E>(x);  // quad_perm [2,3,0,1]
-  } else if constexpr (D == 4) {
-    return dpp_mov<0x1B>(dpp_mov<0x141>(x));  // quad_perm [3,2,1,0] after row_half_mirror
-  } else if constexpr (D == 8) {
-    return dpp_mov<0x128>(x);  // row_ror:8
-  } else if constexpr (D == 16) {
-    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
-    return (lane & 16) ? r[0] : r[1];
-  } else {
-    static_assert(D == 32, "lane_xor: D must be a power of two below 64");
-    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
-    return (lane & 32) ? r[0] : r[1];
-  }
-}
-
 // Compare-exchange at distance D keeping the larger value in the lower lane.
 template <int D>
 __device__ __forceinline__ uint32_t cx_desc(uint32_t x, int lane) {
@@ -218,8 +187,12 @@ __device__ __forceinline__ uint32_t wave_sort_desc(uint32_t x, int lane) {
 // hop between the vector and the scalar unit (a compare whose mask feeds a
 // scalar op that feeds the next vector op) costs ~100 cycles and an LDS round
 // trip ~120, so the steps avoid both:
-//   1. each lane holds M keys (positions lane + 64 j) in registers and takes
-//      their maximum;
+//   1. each lane holds M keys in registers, row j of 64 positions rotated by
+//      j (lane L holds position 64 j + ((L - j) mod 64)), and takes their
+//      maximum.  The rotation puts the two natural shapes of a selection on
+//      distinct lanes: chunks at a common stride of at least M, and any
+//      contiguous run of at most 63 chunks; their maxima then sit in
+//      different lanes and step 2 finds a tight threshold;
 //   2. the 64 lane maxima are sorted by a bitonic network of lane permutes
 //      (no LDS) and t = the k-th largest lane maximum: at least k keys are
 //      >= t and every key of the answer is >= t;
@@ -241,7 +214,7 @@ __device__ bool wave_topk_regs(const uint32_t* keys, int C, int k, uint32_t* scr
 #pragma unroll
   for (int j = 0; j < M; ++j) {
     // Clamped load + select rather than a branch per key (C >= 1).
-    const int i = lane + kWave * j;
+    const int i = kWave * j + ((lane - j) & (kWave - 1));
     const uint32_t kv = keys[i < C ? i : C - 1];
     v[j] = i < C ? kv : 0u;
   }
@@ -262,7 +235,7 @@ __device__ bool wave_topk_regs(const uint32_t* keys, int C, int k, uint32_t* scr
     const unsigned long long bal = __ballot(take);
     int slot = n + lanes_below(bal) + (take ? 0 : kWave);
     slot = slot < kWave ? slot : kWave;
-    const uint32_t pos = static_cast<uint32_t>(lane + kWave * j);
+    const uint32_t pos = static_cast<uint32_t>(kWave * j + ((lane - j) & (kWave - 1)));
     cand[slot] = (static_cast<unsigned long long>(v[j]) << 32) | static_cast<uint32_t>(~pos);
     n += __popcll(bal);
   }

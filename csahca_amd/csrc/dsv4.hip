@@ -122,6 +122,44 @@ struct Dsv4Args {
   float qscale;  // softmax_scale * log2(e)
 };
 
+// 64-bit value of lane l (l uniform across the wavefront).
+__device__ __forceinline__ uint64_t readlane64(uint64_t v, int l) {
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v)), l));
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v >> 32), l));
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// One halving step of a wavefront reduce-scatter over N per-lane partial sums:
+// lanes with bit D set keep the upper half of the values, the others the lower
+// half; each lane sends the half it drops to lane ^ D and adds what it gets.
+template <int D, int N>
+__device__ __forceinline__ void rs_half(float* v, int lane) {
+  const bool upper = (lane & D) != 0;
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) {
+    const float keep = upper ? v[i + N / 2] : v[i];
+    const float send = upper ? v[i] : v[i + N / 2];
+    v[i] = keep + __uint_as_float(lane_xor<D>(__float_as_uint(send), lane));
+  }
+}
+
+// Reduce-scatter of 32 per-lane partial sums (31 lane moves instead of the
+// 192 of 32 butterfly all-reduces): lane L ends with the wavefront total of
+// v[L >> 1].
+__device__ __forceinline__ float wave_reduce_scatter32(float* v, int lane) {
+  rs_half<32, 32>(v, lane);
+  rs_half<16, 16>(v, lane);
+  rs_half<8, 8>(v, lane);
+  rs_half<4, 4>(v, lane);
+  rs_half<2, 2>(v, lane);
+  return v[0] + __uint_as_float(lane_xor<1>(__float_as_uint(v[0]), lane));
+}
+
+// Slots per batch of row loads: kSlotBatch x kHeadGroup = 32 dot products per
+// reduce-scatter.
+constexpr int kSlotBatch = 4;
+static_assert(kSlotBatch * kHeadGroup == 32, "one reduce-scatter of 32 sums per batch");
+
 template <typename T, bool kVec>
 __global__ __launch_bounds__(64) void dsv4_tile_kernel(const T* __restrict__ q, Dsv4Args a) {
   const int lane = threadIdx.x;
@@ -162,41 +200,79 @@ __global__ __launch_bounds__(64) void dsv4_tile_kernel(const T* __restrict__ q, 
     for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
   }
 
-  for (int s = s0; s < s1; ++s) {
-    const uint8_t* row;
-    const uint8_t* srow = nullptr;
-    if (s < a.topk_slots) {
-      if (s >= n_swa) continue;
-      row = row_ptr(a.swa, a.idx[query * a.topk_slots + s], &srow);
-    } else {
-      const int j = s - a.topk_slots;
-      if (j >= n_extra) continue;
-      row = row_ptr(a.extra, a.eidx[query * a.extra_slots + j], &srow);
+  for (int g = s0; g < s1; g += kWave) {
+    // Lane j resolves slot g + j (index load + page math) for the whole group.
+    const int s = g + lane;
+    const uint8_t* rp = nullptr;
+    const uint8_t* sp = nullptr;
+    if (s < s1) {
+      if (s < a.topk_slots) {
+        if (s < n_swa) rp = row_ptr(a.swa, a.idx[query * a.topk_slots + s], &sp);
+      } else {
+        const int j = s - a.topk_slots;
+        if (j < n_extra) rp = row_ptr(a.extra, a.eidx[query * a.extra_slots + j], &sp);
+      }
     }
-    if (row == nullptr) continue;
-    float kv[8];
-    load_row8<kVec>(row, srow, lane, kv);
-    float sc[kHeadGroup];
+    const unsigned long long valid = __ballot(rp != nullptr);
+    if (valid == 0ull) continue;
+    // Skipped slots fetch the first valid slot's row (in bounds); their scores are masked.
+    const int first = __ffsll(static_cast<long long>(valid)) - 1;
+    const uint64_t r_first = readlane64(reinterpret_cast<uint64_t>(rp), first);
+    const uint64_t s_first = readlane64(reinterpret_cast<uint64_t>(sp), first);
+    const uint64_t r_lane = rp ? reinterpret_cast<uint64_t>(rp) : r_first;
+    const uint64_t s_lane = rp ? reinterpret_cast<uint64_t>(sp) : s_first;
+    const int cnt = min(kWave, s1 - g);
+    for (int b = 0; b < cnt; b += kSlotBatch) {
+      const uint32_t ok = static_cast<uint32_t>(valid >> b) & ((1u << kSlotBatch) - 1u);
+      if (ok == 0u) continue;
+      float kv[kSlotBatch][8];
 #pragma unroll
-    for (int h = 0; h < kHeadGroup; ++h) {
-      float d = 0.f;
+      for (int j = 0; j < kSlotBatch; ++j) {
+        const uint8_t* row = reinterpret_cast<const uint8_t*>(readlane64(r_lane, b + j));
+        const uint8_t* srow = reinterpret_cast<const uint8_t*>(readlane64(s_lane, b + j));
+        load_row8<kVec>(row, srow, lane, kv[j]);
+      }
+      float part[kSlotBatch * kHeadGroup];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) d = fmaf(qr[h][e], kv[e], d);
-      sc[h] = d;
-    }
+      for (int j = 0; j < kSlotBatch; ++j)
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1)
+        for (int h = 0; h < kHeadGroup; ++h) {
+          float d = 0.f;
 #pragma unroll
-      for (int h = 0; h < kHeadGroup; ++h) sc[h] += __shfl_xor(sc[h], off, kWave);
+          for (int e = 0; e < 8; ++e) d = fmaf(qr[h][e], kv[j][e], d);
+          part[j * kHeadGroup + h] = d;
+        }
+      const float tot = wave_reduce_scatter32(part, lane);
 #pragma unroll
-    for (int h = 0; h < kHeadGroup; ++h) {
-      const float m_new = fmaxf(m[h], sc[h]);
-      const float alpha = fast_exp2(m[h] - m_new);
-      const float p = fast_exp2(sc[h] - m_new);
-      l[h] = l[h] * alpha + p;
+      for (int h = 0; h < kHeadGroup; ++h) {
+        float sc[kSlotBatch];
+        float mb = -INFINITY;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(p, kv[e], acc[h][e] * alpha);
-      m[h] = m_new;
+        for (int j = 0; j < kSlotBatch; ++j) {
+          const float x =
+              __int_as_float(__builtin_amdgcn_readlane(__float_as_int(tot), 2 * (j * kHeadGroup + h)));
+          sc[j] = ((ok >> j) & 1u) ? x : -INFINITY;
+          mb = fmaxf(mb, sc[j]);
+        }
+        const float m_new = fmaxf(m[h], mb);  // finite: the batch has a valid slot
+        const float alpha = fast_exp2(m[h] - m_new);
+        float p[kSlotBatch];
+        float psum = 0.f;
+#pragma unroll
+        for (int j = 0; j < kSlotBatch; ++j) {
+          p[j] = fast_exp2(sc[j] - m_new);
+          psum += p[j];
+        }
+        l[h] = l[h] * alpha + psum;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float x = acc[h][e] * alpha;
+#pragma unroll
+          for (int j = 0; j < kSlotBatch; ++j) x = fmaf(p[j], kv[j][e], x);
+          acc[h][e] = x;
+        }
+        m[h] = m_new;
+      }
     }
   }
 
@@ -215,60 +291,78 @@ __global__ __launch_bounds__(64) void dsv4_tile_kernel(const T* __restrict__ q, 
   }
 }
 
+constexpr int kMergeThreads = kDim / 4;  // 4 output columns per thread
+constexpr int kMergeChunk = 1024;        // tile weights staged in LDS per pass
+
 // Merge of the tile partials with the sink as a virtual token of logit
 // sink[h] and value 0 (csrc/dsv4_attention.cu:252-269): M = max(sink, m_t),
-// L = 2^(sink-M) + sum_{l_t>0} l_t 2^(m_t-M), out = sum 2^(m_t-M) acc_t / L.
+// L = 2^(sink-M) + sum_{l_t>0} l_t 2^(m_t-M), out = sum_t w_t acc_t / L with
+// w_t = 2^(m_t-M) (0 for empty tiles).  The weights are computed in parallel
+// into LDS; the column sums then stream the partial rows without branches.
 template <typename T>
-__global__ __launch_bounds__(128) void dsv4_merge_kernel(const float* __restrict__ part_ml,
-                                                         const float* __restrict__ part_acc,
-                                                         const float* __restrict__ sink,
-                                                         T* __restrict__ out, int heads,
-                                                         int num_tiles) {
+__global__ __launch_bounds__(kMergeThreads) void dsv4_merge_kernel(const float* __restrict__ part_ml,
+                                                                   const float* __restrict__ part_acc,
+                                                                   const float* __restrict__ sink,
+                                                                   T* __restrict__ out, int heads,
+                                                                   int num_tiles) {
+  __shared__ float s_w[kMergeChunk];
+  __shared__ float s_mx, s_inv;
   const int64_t qh = blockIdx.x;
   const int head = static_cast<int>(qh % heads);
-  const float* ml = part_ml + 2 * qh * num_tiles;
-  __shared__ float s_max, s_inv;
-  if (threadIdx.x < kWave) {
+  const int tid = threadIdx.x;
+  const float2* ml = reinterpret_cast<const float2*>(part_ml) + qh * num_tiles;
+  if (tid < kWave) {
     const float sk = sink ? sink[head] * kLog2e : -INFINITY;
     float mx = -INFINITY;
-    for (int t = threadIdx.x; t < num_tiles; t += kWave) mx = fmaxf(mx, ml[2 * t]);
+    for (int t = tid; t < num_tiles; t += kWave) {
+      const float2 v = ml[t];
+      if (v.y > 0.f) mx = fmaxf(mx, v.x);
+    }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
     mx = fmaxf(mx, sk);
     float L = 0.f;
-    for (int t = threadIdx.x; t < num_tiles; t += kWave) {
-      const float lt = ml[2 * t + 1];
-      if (lt > 0.f) L += lt * fast_exp2(ml[2 * t] - mx);
+    if (mx != -INFINITY) {
+      for (int t = tid; t < num_tiles; t += kWave) {
+        const float2 v = ml[t];
+        if (v.y > 0.f) L += v.y * fast_exp2(v.x - mx);
+      }
     }
     L = wave_sum(L);
-    if (threadIdx.x == 0) {
-      if (sink) L += fast_exp2(sk - mx);
-      s_max = mx;
+    if (tid == 0) {
+      if (sink && mx != -INFINITY) L += fast_exp2(sk - mx);
+      s_mx = mx;
       s_inv = L > 0.f ? 1.f / L : 0.f;
     }
   }
   __syncthreads();
-  const float mx = s_max, inv = s_inv;
-  const float* pa = part_acc + qh * num_tiles * static_cast<int64_t>(kDim);
-  for (int d = threadIdx.x * 4; d < kDim; d += blockDim.x * 4) {
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int t = 0; t < num_tiles; ++t) {
-      const float lt = ml[2 * t + 1];
-      if (lt > 0.f) {
-        const float w = fast_exp2(ml[2 * t] - mx);
-        const float4 v = *reinterpret_cast<const float4*>(pa + static_cast<int64_t>(t) * kDim + d);
-        acc.x = fmaf(w, v.x, acc.x);
-        acc.y = fmaf(w, v.y, acc.y);
-        acc.z = fmaf(w, v.z, acc.z);
-        acc.w = fmaf(w, v.w, acc.w);
-      }
+  const float mx = s_mx, inv = s_inv;
+  const int d = 4 * tid;
+  const float* pa = part_acc + qh * num_tiles * static_cast<int64_t>(kDim) + d;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int c0 = 0; c0 < num_tiles; c0 += kMergeChunk) {
+    const int cn = min(kMergeChunk, num_tiles - c0);
+    for (int t = tid; t < cn; t += kMergeThreads) {
+      const float2 v = ml[c0 + t];
+      s_w[t] = (v.y > 0.f && mx != -INFINITY) ? fast_exp2(v.x - mx) : 0.f;
     }
-    T* o = out + qh * kDim + d;
-    o[0] = from_f32<T>(acc.x * inv);
-    o[1] = from_f32<T>(acc.y * inv);
-    o[2] = from_f32<T>(acc.z * inv);
-    o[3] = from_f32<T>(acc.w * inv);
+    __syncthreads();
+#pragma unroll 8
+    for (int t = 0; t < cn; ++t) {
+      const float w = s_w[t];
+      const float4 x = *reinterpret_cast<const float4*>(pa + static_cast<int64_t>(c0 + t) * kDim);
+      acc.x = fmaf(w, x.x, acc.x);
+      acc.y = fmaf(w, x.y, acc.y);
+      acc.z = fmaf(w, x.z, acc.z);
+      acc.w = fmaf(w, x.w, acc.w);
+    }
+    __syncthreads();
   }
+  T* o = out + qh * kDim + d;
+  o[0] = from_f32<T>(acc.x * inv);
+  o[1] = from_f32<T>(acc.y * inv);
+  o[2] = from_f32<T>(acc.z * inv);
+  o[3] = from_f32<T>(acc.w * inv);
 }
 
 // Split selection: tile_size > 0 -> ceil(total/tile) tiles (csrc/dsv4_attention.cu:858-860);
@@ -359,7 +453,7 @@ int dsv4_run(const Dsv4Call& c) {
                                 stream, qp, a);
     if (rc != CSAHCA_OK) return rc;
     return launch("dsv4_merge_kernel", dsv4_merge_kernel<T>,
-                  dim3(static_cast<uint32_t>(c.nq * c.heads)), dim3(128), 0, stream,
+                  dim3(static_cast<uint32_t>(c.nq * c.heads)), dim3(kMergeThreads), 0, stream,
                   static_cast<const float*>(a.part_ml), static_cast<const float*>(a.part_acc), c.sink,
                   static_cast<T*>(c.out), a.heads, a.num_tiles);
   });
