@@ -16,6 +16,8 @@ from csahca_amd.native import (  # noqa: F401
     dsv4_decode_forward_tiled,
     dsv4_sparse_decode_forward,
     dsv4_swa_decode_forward,
+    hca_decode_forward,
+    hybrid_decode_forward,
     lib as _lib,
 )
 
@@ -30,4 +32,6 @@ __all__ = [
     "csa_chunk_summary",
     "csa_select_topk",
     "csa_decode_step",
+    "hca_decode_forward",
+    "hybrid_decode_forward",
 ]

@@ -132,3 +132,17 @@ def csa_decode_step(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
                     chunk_size: int, top_k: int, tile_size: int = 0):
     return load_cuda_extension().csa_decode_step(q.contiguous(), k_cache.contiguous(), v_cache.contiguous(),
                                                  summary.contiguous(), int(chunk_size), int(top_k), int(tile_size))
+
+
+def hca_decode_forward(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, chunk_size: int) -> torch.Tensor:
+    """hca_reference (hybrid_attention/reference.py:87-92) on the GPU."""
+    return load_cuda_extension().hca_decode_forward(q.contiguous(), k_cache.contiguous(), v_cache.contiguous(),
+                                                    int(chunk_size))
+
+
+def hybrid_decode_forward(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, *, csa_chunk_size: int,
+                          csa_top_k: int, hca_chunk_size: int, csa_weight: float = 0.7) -> torch.Tensor:
+    """hybrid_reference (hybrid_attention/reference.py:95-108) on the GPU."""
+    return load_cuda_extension().hybrid_decode_forward(
+        q.contiguous(), k_cache.contiguous(), v_cache.contiguous(), csa_chunk_size=int(csa_chunk_size),
+        csa_top_k=int(csa_top_k), hca_chunk_size=int(hca_chunk_size), csa_weight=float(csa_weight))

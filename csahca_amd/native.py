@@ -11,8 +11,9 @@ checks run in the C library.  Outputs and workspaces come from torch's caching
 allocator on the current stream; kernels run on torch's current HIP stream,
 so calls are graph-capturable.
 
-New ops next to them: ``csa_chunk_summary``, ``csa_select_topk`` and
-``csa_decode_step`` (summary scoring + top-k + sparse attention in one call).
+New ops next to them: ``csa_chunk_summary``, ``csa_select_topk``,
+``csa_decode_step`` (summary scoring + top-k + sparse attention in one call),
+``hca_decode_forward`` and ``hybrid_decode_forward``.
 
 There is no CPU fallback: without the built library every op raises.
 """
@@ -57,6 +58,8 @@ _SIGNATURES = {
     "csahca_csa_step_workspace_bytes": (_sz, [_i64] * 6),
     "csahca_csa_decode_step": (_int, [_vp] * 6 + [_int] + [_i64] * 7 + [_vp, _sz, _vp]),
     "csahca_csa_step_status": (_int, [_vp, ctypes.POINTER(ctypes.c_uint32), _vp]),
+    "csahca_hca_decode_workspace_bytes": (_sz, [_i64] * 5),
+    "csahca_hca_decode_forward": (_int, [_vp, _vp, _vp, _vp, _dbl, _vp, _int] + [_i64] * 5 + [_vp, _sz, _vp]),
     "csahca_profile_begin": (_int, []),
     "csahca_profile_end": (_int, []),
     "csahca_profile_result": (_int, [_int, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_i64),
@@ -301,6 +304,45 @@ def csa_step_status(device=None) -> dict:
             _rc(lib().csahca_csa_step_status(_ptr(ws), ctypes.byref(val), _stream()))
         out[key] = val.value
     return out
+
+
+def hca_decode_forward(q, k_cache, v_cache, chunk_size, *, blend=None, csa_weight: float = 0.7):
+    """hca_reference (hybrid_attention/reference.py:87-92) on the GPU: dense
+    attention over the chunk means of K and V, both rounded to the storage
+    type.  With ``blend`` (a [B,H,D] tensor of q's dtype) the result is
+    ``csa_weight*blend + (1-csa_weight)*hca`` rounded as in hybrid_reference
+    (reference.py:95-108)."""
+    chunk_size = int(chunk_size)
+    for name, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache)):
+        _check(t.is_cuda, f"{name} must be a CUDA tensor")
+        _check(t.is_contiguous(), f"{name} must be contiguous")
+    _check(q.dim() == 3, "q must be [batch, heads, head_dim]")
+    _check(k_cache.dim() == 4 and v_cache.shape == k_cache.shape, "k_cache and v_cache must be [batch, heads, seq_len, head_dim]")
+    _check(q.dtype in _DTYPES and k_cache.dtype == q.dtype and v_cache.dtype == q.dtype,
+           "q, k_cache and v_cache must have the same floating dtype")
+    B, H, S, D = k_cache.shape
+    _check(tuple(q.shape) == (B, H, D), "q shape must match k_cache")
+    if blend is not None:
+        _check(blend.is_cuda and blend.is_contiguous() and blend.dtype == q.dtype and blend.shape == q.shape,
+               "blend must be a contiguous CUDA tensor shaped and typed like q")
+    with torch.cuda.device(q.device):
+        out = torch.empty_like(q)
+        ws = _workspace(lib().csahca_hca_decode_workspace_bytes(B, H, S, D, chunk_size), q.device)
+        _rc(lib().csahca_hca_decode_forward(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(blend), float(csa_weight),
+                                            _ptr(out), _DTYPES[q.dtype], B, H, S, D, chunk_size, _ptr(ws),
+                                            ws.numel(), _stream()))
+    return out
+
+
+def hybrid_decode_forward(q, k_cache, v_cache, *, csa_chunk_size: int, csa_top_k: int, hca_chunk_size: int,
+                          csa_weight: float = 0.7, summary=None):
+    """hybrid_reference (hybrid_attention/reference.py:95-108) on the GPU: the
+    CSA decode step (selection from the chunk summaries of K, built here when
+    ``summary`` is None) blended with HCA at ``csa_weight``."""
+    if summary is None:
+        summary = csa_chunk_summary(k_cache, csa_chunk_size)
+    csa_out, _idx = csa_decode_step(q, k_cache, v_cache, summary, csa_chunk_size, csa_top_k)
+    return hca_decode_forward(q, k_cache, v_cache, hca_chunk_size, blend=csa_out, csa_weight=csa_weight)
 
 
 # ---------------------------------------------------------------------------

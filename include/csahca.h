@@ -137,6 +137,27 @@ int csahca_csa_decode_step(const void* q, const void* k_cache, const void* v_cac
 int csahca_csa_step_status(const void* workspace, uint32_t* status_out, void* stream);
 
 /* ------------------------------------------------------------------------- */
+/* HCA: dense attention over chunk summaries, and the CSA/HCA blend           */
+/* ------------------------------------------------------------------------- */
+
+/* Workspace of csahca_hca_decode_forward: B*H*(S/chunk)*(head_dim+1) floats. */
+size_t csahca_hca_decode_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len,
+                                         int64_t head_dim, int64_t chunk_size);
+
+/* Replaces hca_reference (hybrid_attention/reference.py:87-92): K and V are
+ * mean-pooled per chunk (fp32 mean rounded to the storage type), then full
+ * decode attention over the S/chunk summary rows with probabilities rounded to
+ * the storage type (reference.py:31-37).  seq_len must be a multiple of
+ * chunk_size (reference.py:41-42).  With blend_src non-NULL ([B,H,D], same
+ * dtype) the output is hybrid_reference's blend (reference.py:95-108):
+ * round(round(w*blend) + round((1-w)*hca)), w = blend_weight. */
+int csahca_hca_decode_forward(const void* q, const void* k_cache, const void* v_cache,
+                              const void* blend_src, double blend_weight, void* out, int dtype,
+                              int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
+                              int64_t chunk_size, void* workspace, size_t workspace_bytes,
+                              void* stream);
+
+/* ------------------------------------------------------------------------- */
 /* DSV4: MQA decode over the paged FP8 latent cache                           */
 /* ------------------------------------------------------------------------- */
 
