@@ -55,6 +55,7 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-dsv4", action="store_true")
+    ap.add_argument("--no-hca", action="store_true")
     ap.add_argument("--sweep", action="store_true", help="also run the BASELINE config-2 sweep (stderr + json)")
     ap.add_argument("--sweep-out", type=Path, default=None)
     ap.add_argument("--no-graph", action="store_true",
@@ -298,6 +299,60 @@ def dsv4_bench(steps=200, copies=64):
     return out
 
 
+def hca_bench(steps=256, copies=4, hca_chunk=256):
+    """HCA and the CSA/HCA hybrid at the headline shape (B1 H8 S32768 D128 bf16,
+    hca_chunk 256 as in the reference benchmark, CSA chunk 64 top-8 from cached
+    summaries).  HCA reads all of K and V once per call: 128 MiB, HBM-bound.
+    `copies` distinct K/V sets (512 MiB) rotate so the 256 MiB MALL cannot hold
+    a call's data; inputs are drawn on the device (timing only)."""
+    import torch
+
+    from csahca_amd import native
+
+    dev = torch.device("cuda", 0)
+    B, H, S, D = 1, 8, 32768, 128
+    g = torch.Generator(device=dev).manual_seed(1)
+    q = torch.randn(B, H, D, dtype=torch.bfloat16, device=dev, generator=g)
+    ks = [torch.empty(B, H, S, D, dtype=torch.bfloat16, device=dev).normal_(generator=g) for _ in range(copies)]
+    vs = [torch.empty(B, H, S, D, dtype=torch.bfloat16, device=dev).normal_(generator=g) for _ in range(copies)]
+    summs = [native.csa_chunk_summary(k, 64) for k in ks]
+
+    def hca(j):
+        return native.hca_decode_forward(q, ks[j], vs[j], hca_chunk)
+
+    def hybrid(j):
+        return native.hybrid_decode_forward(q, ks[j], vs[j], csa_chunk_size=64, csa_top_k=8,
+                                            hca_chunk_size=hca_chunk, summary=summs[j])
+
+    kv_bytes = 2 * B * H * S * D * 2
+    out = {"config": f"B{B} H{H} S{S} D{D} bf16, hca_chunk {hca_chunk}; hybrid adds the CSA step "
+                     f"(chunk 64, top-8, cached summaries) and the 0.7/0.3 blend"}
+    for name, fn in (("hca", hca), ("hybrid", hybrid)):
+        for j in range(copies):
+            fn(j)
+        gr = graph_of([lambda j=j: fn(j) for j in range(copies)])
+        reps = max(1, steps // copies)
+        ms = time_graph_steps(gr, {}, copies, reps * copies) / (reps * copies)
+        with native.profile_launches() as prof:
+            for j in range(copies):
+                fn(j)
+        kern = {n: round(v["avg_us"], 3) for n, v in prof.results.items()}
+        row = {"ms_per_token": round(ms, 5), "tokens_per_s": round(B / (ms / 1e3), 1), "kernels_avg_us": kern}
+        if name == "hca":
+            us = prof.results["hca_chunk_kernel"]["avg_us"]
+            gbps = kv_bytes / (us * 1e-6) / 1e9
+            row["roofline"] = {"bound": "hbm", "kernel": "hca_chunk_kernel", "bytes_per_launch": kv_bytes,
+                               "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                               "frac": round(gbps / PEAK_HBM_GBPS, 4)}
+        out[name] = row
+        log(f"{name}: {row}")
+        del gr
+    del ks, vs, summs
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return out
+
+
 def sweep(args):
     rows = []
     for B in (1, 8, 32):
@@ -392,6 +447,8 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": traffic,
                      "bytes_per_launch": dom_bytes, "avg_launch_us": round(dom_us, 3)},
     }
+    if not args.no_hca:
+        line["hca"] = hca_bench()
     if not args.no_dsv4:
         line["dsv4"] = dsv4_bench()
     if args.sweep:

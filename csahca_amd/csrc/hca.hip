@@ -29,6 +29,42 @@ namespace {
 constexpr int kHcaThreads = 256;
 constexpr int kHcaProbChunk = 2048;  // probabilities staged in LDS per pass
 
+constexpr int kRowBatch = 8;          // rows of K and V in flight per thread
+
+// Widen one 16-byte load of T to fp32.
+template <typename T>
+__device__ __forceinline__ void widen16(const uint4 w, float* out);
+template <>
+__device__ __forceinline__ void widen16<bf16>(const uint4 w, float* out) {
+  const uint32_t x[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = __uint_as_float(x[i] << 16);
+    out[2 * i + 1] = __uint_as_float(x[i] & 0xffff0000u);
+  }
+}
+template <>
+__device__ __forceinline__ void widen16<f16>(const uint4 w, float* out) {
+  const uint32_t x[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(x[i] & 0xffffu)));
+    out[2 * i + 1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(x[i] >> 16)));
+  }
+}
+template <>
+__device__ __forceinline__ void widen16<float>(const uint4 w, float* out) {
+  out[0] = __uint_as_float(w.x);
+  out[1] = __uint_as_float(w.y);
+  out[2] = __uint_as_float(w.z);
+  out[3] = __uint_as_float(w.w);
+}
+template <>
+__device__ __forceinline__ void widen16<double>(const uint4 w, float* out) {
+  out[0] = static_cast<float>(__builtin_bit_cast(double, (static_cast<uint64_t>(w.y) << 32) | w.x));
+  out[1] = static_cast<float>(__builtin_bit_cast(double, (static_cast<uint64_t>(w.w) << 32) | w.z));
+}
+
 template <typename T>
 __device__ __forceinline__ float round_to(float x) {
   return to_f32(from_f32<T>(x));
@@ -81,21 +117,49 @@ __global__ __launch_bounds__(kHcaThreads) void hca_chunk_kernel(const T* __restr
       float ak[VEC], av[VEC];
 #pragma unroll
       for (int e = 0; e < VEC; ++e) ak[e] = av[e] = 0.f;
-#pragma unroll 4
-      for (int r = rg; r < chunk; r += R) {
-        const int64_t off = (row0 + r) * D + static_cast<int64_t>(vc) * VEC;
-        float xk[VEC], xv[VEC];
+      const T* kc = k + row0 * D + static_cast<int64_t>(vc) * VEC;
+      const T* vcp = v + row0 * D + static_cast<int64_t>(vc) * VEC;
+      // kRowBatch rows of K and V are requested before any is consumed, so a
+      // thread waits for one HBM round trip per batch rather than per row.
+      for (int r0 = rg; r0 < chunk; r0 += kRowBatch * R) {
         if constexpr (kVec) {
-          load16<T>(k + off, xk);
-          load16<T>(v + off, xv);
-        } else {
-          xk[0] = to_f32(k[off]);
-          xv[0] = to_f32(v[off]);
-        }
+          uint4 rk[kRowBatch], rv[kRowBatch];
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          ak[e] += xk[e];
-          av[e] += xv[e];
+          for (int i = 0; i < kRowBatch; ++i) {
+            const int r = r0 + i * R;
+            const int64_t off = static_cast<int64_t>(r < chunk ? r : r0) * D;
+            rk[i] = *reinterpret_cast<const uint4*>(kc + off);
+            rv[i] = *reinterpret_cast<const uint4*>(vcp + off);
+          }
+#pragma unroll
+          for (int i = 0; i < kRowBatch; ++i) {
+            if (r0 + i * R < chunk) {
+              float xk[VEC], xv[VEC];
+              widen16<T>(rk[i], xk);
+              widen16<T>(rv[i], xv);
+#pragma unroll
+              for (int e = 0; e < VEC; ++e) {
+                ak[e] += xk[e];
+                av[e] += xv[e];
+              }
+            }
+          }
+        } else {
+          float xk[kRowBatch], xv[kRowBatch];
+#pragma unroll
+          for (int i = 0; i < kRowBatch; ++i) {
+            const int r = r0 + i * R;
+            const int64_t off = static_cast<int64_t>(r < chunk ? r : r0) * D;
+            xk[i] = to_f32(kc[off]);
+            xv[i] = to_f32(vcp[off]);
+          }
+#pragma unroll
+          for (int i = 0; i < kRowBatch; ++i) {
+            if (r0 + i * R < chunk) {
+              ak[0] += xk[i];
+              av[0] += xv[i];
+            }
+          }
         }
       }
 #pragma unroll
@@ -126,18 +190,90 @@ __global__ __launch_bounds__(kHcaThreads) void hca_chunk_kernel(const T* __restr
   if (tid == 0) out[0] = dot * scale;
 }
 
+// Thread layout of the PV sum: RG = 256/D row groups (1 when D > 256) x D
+// columns; each thread keeps kMergeBatch rows of its column in flight, and the
+// RG partial sums meet in LDS at the end.
+constexpr int kMergeBatch = 64;         // rows per thread in the one-round-trip path
+constexpr int kMergeBatchGeneral = 32;  // rows per thread per batch otherwise
+
 template <typename T>
 __global__ __launch_bounds__(kHcaThreads) void hca_merge_kernel(const float* __restrict__ part,
                                                               const T* __restrict__ blend,
                                                               float w_csa, T* __restrict__ out,
                                                               int64_t C, int D) {
-  constexpr int kCols = 1024 / kHcaThreads;  // D <= 1024
+  constexpr int kCols = 1024 / kHcaThreads;  // columns per thread when D > 256 (D <= 1024)
   __shared__ float s_p[kHcaProbChunk];
+  __shared__ float s_sum[kHcaThreads];
   __shared__ float red[kHcaThreads / kWave];
   const int tid = threadIdx.x;
   const int64_t bh = blockIdx.x;
   const int64_t stride = static_cast<int64_t>(D) + 1;
   const float* pb = part + bh * C * stride;
+  const int RG = D <= kHcaThreads ? kHcaThreads / D : 1;
+  const int tpc = D <= kHcaThreads ? D : kHcaThreads;  // threads per row group
+  const int rg = tid / tpc;
+  const int c0l = tid - rg * tpc;
+
+  if (D <= kHcaThreads && C <= kHcaProbChunk && C <= static_cast<int64_t>(kMergeBatch) * RG) {
+    // Common shape: every score and every V-mean value this thread needs is
+    // requested before the first wait -- one memory round trip in total.
+    constexpr int kScores = kHcaProbChunk / kHcaThreads;
+    const int n = static_cast<int>(C);
+    float sc[kScores], x[kMergeBatch];
+#pragma unroll
+    for (int j = 0; j < kScores; ++j) {
+      const int c = tid + j * kHcaThreads;
+      sc[j] = c < n ? pb[static_cast<int64_t>(c) * stride] : -INFINITY;
+    }
+    const bool mine = rg < RG;
+    const float* col = pb + 1 + (mine ? c0l : 0);
+#pragma unroll
+    for (int i = 0; i < kMergeBatch; ++i) {
+      const int r = rg + i * RG;
+      x[i] = col[static_cast<int64_t>(mine && r < n ? r : 0) * stride];
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kScores; ++j) m = fmaxf(m, sc[j]);
+    const float M = block_reduce(m, red, true);
+    float l = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int j = 0; j < kScores; ++j)
+        if (tid + j * kHcaThreads < n) l += fast_exp2((sc[j] - M) * kLog2e);
+    }
+    const float Lt = block_reduce(l, red, false);
+    const float iv = Lt > 0.f ? 1.f / Lt : 0.f;
+#pragma unroll
+    for (int j = 0; j < kScores; ++j) {
+      const int c = tid + j * kHcaThreads;
+      // softmax in fp32, then the cast of the probabilities to the V dtype
+      if (c < n) s_p[c] = M != -INFINITY ? round_to<T>(fast_exp2((sc[j] - M) * kLog2e) * iv) : 0.f;
+    }
+    __syncthreads();
+    float a = 0.f;
+#pragma unroll
+    for (int i = 0; i < kMergeBatch; ++i) {
+      const int r = rg + i * RG;
+      if (mine && r < n) a = fmaf(s_p[r], x[i], a);
+    }
+    s_sum[tid] = a;
+    __syncthreads();
+    if (tid < D) {
+      float o = 0.f;
+      for (int g = 0; g < RG; ++g) o += s_sum[g * D + tid];
+      o = round_to<T>(o);
+      if (blend) {
+        // w*csa + (1-w)*hca with each product and the sum rounded to T
+        const float ab = round_to<T>(w_csa * to_f32(blend[bh * D + tid]));
+        const float bb = round_to<T>((1.f - w_csa) * o);
+        o = ab + bb;
+      }
+      out[bh * D + tid] = from_f32<T>(o);
+    }
+    return;
+  }
+
   float mx = -INFINITY;
   for (int64_t c = tid; c < C; c += kHcaThreads) mx = fmaxf(mx, pb[c * stride]);
   mx = block_reduce(mx, red, true);
@@ -150,39 +286,64 @@ __global__ __launch_bounds__(kHcaThreads) void hca_merge_kernel(const float* __r
   float acc[kCols];
 #pragma unroll
   for (int j = 0; j < kCols; ++j) acc[j] = 0.f;
-  for (int64_t c0 = 0; c0 < C; c0 += kHcaProbChunk) {
-    const int cn = static_cast<int>(std::min<int64_t>(kHcaProbChunk, C - c0));
-    for (int c = tid; c < cn; c += kHcaThreads) {
-      const float x = pb[(c0 + c) * stride];
+  for (int64_t p0 = 0; p0 < C; p0 += kHcaProbChunk) {
+    const int pn = static_cast<int>(std::min<int64_t>(kHcaProbChunk, C - p0));
+    for (int c = tid; c < pn; c += kHcaThreads) {
+      const float x = pb[(p0 + c) * stride];
       // softmax in fp32, then the cast of the probabilities to the V dtype
       s_p[c] = mx != -INFINITY ? round_to<T>(fast_exp2((x - mx) * kLog2e) * inv) : 0.f;
     }
     __syncthreads();
+    if (rg < RG) {
 #pragma unroll
-    for (int j = 0; j < kCols; ++j) {
-      const int d = tid + j * kHcaThreads;
-      if (d < D) {
-        const float* col = pb + c0 * stride + 1 + d;
-        float a = acc[j];
-#pragma unroll 8
-        for (int c = 0; c < cn; ++c) a = fmaf(s_p[c], col[c * stride], a);
-        acc[j] = a;
+      for (int j = 0; j < kCols; ++j) {
+        const int d = c0l + j * tpc;
+        if (d < D) {
+          const float* col = pb + p0 * stride + 1 + d;
+          float a = acc[j];
+          for (int r0 = rg; r0 < pn; r0 += kMergeBatchGeneral * RG) {
+            float x[kMergeBatchGeneral];
+#pragma unroll
+            for (int i = 0; i < kMergeBatchGeneral; ++i) {
+              const int r = r0 + i * RG;
+              x[i] = col[static_cast<int64_t>(r < pn ? r : r0) * stride];
+            }
+#pragma unroll
+            for (int i = 0; i < kMergeBatchGeneral; ++i) {
+              const int r = r0 + i * RG;
+              if (r < pn) a = fmaf(s_p[r], x[i], a);
+            }
+          }
+          acc[j] = a;
+        }
       }
     }
     __syncthreads();
   }
+  // Sum the row groups (RG > 1 only when D <= 128: one column per thread).
+  if (RG > 1) {
+    s_sum[tid] = acc[0];
+    __syncthreads();
+    if (tid < D) {
+      float a = 0.f;
+      for (int g = 0; g < RG; ++g) a += s_sum[g * D + tid];
+      acc[0] = a;
+    }
+  }
+  if (rg == 0) {
 #pragma unroll
-  for (int j = 0; j < kCols; ++j) {
-    const int d = tid + j * kHcaThreads;
-    if (d < D) {
-      float o = round_to<T>(acc[j]);
-      if (blend) {
-        // w*csa + (1-w)*hca with each product and the sum rounded to T
-        const float a = round_to<T>(w_csa * to_f32(blend[bh * D + d]));
-        const float b = round_to<T>((1.f - w_csa) * o);
-        o = a + b;
+    for (int j = 0; j < kCols; ++j) {
+      const int d = c0l + j * tpc;
+      if (d < D) {
+        float o = round_to<T>(acc[j]);
+        if (blend) {
+          // w*csa + (1-w)*hca with each product and the sum rounded to T
+          const float a = round_to<T>(w_csa * to_f32(blend[bh * D + d]));
+          const float b = round_to<T>((1.f - w_csa) * o);
+          o = a + b;
+        }
+        out[bh * D + d] = from_f32<T>(o);
       }
-      out[bh * D + d] = from_f32<T>(o);
     }
   }
 }
