@@ -283,14 +283,16 @@ def dsv4_bench(steps=200, copies=64):
                         call(j)
                 slots = idx.shape[1] + (eidx.shape[1] if ratio else 0)
                 bytes_q = nq * slots * 584 + nq * H * 1024 * 2 + nq * slots * 4 + H * 4
-                tile_us = prof.results.get("dsv4_tile_kernel", {}).get("avg_us", float("nan"))
                 key = f"c{ratio}_nq{nq}_h{H}"
+                kern = {n: round(v["avg_us"], 3) for n, v in prof.results.items()}
+                main = "dsv4_mfma_kernel" if "dsv4_mfma_kernel" in kern else "dsv4_tile_kernel"
                 out[key] = {"ms_per_call": round(ms, 5), "ms_per_query": round(ms / nq, 5),
                             "query_heads_per_s": round(nq * H / (ms / 1e3), 1),
-                            "tile_kernel_us": round(tile_us, 3),
-                            "merge_kernel_us": round(prof.results.get("dsv4_merge_kernel", {}).get("avg_us", 0), 3),
+                            "kernels_avg_us": kern,
                             "algorithmic_bytes": bytes_q,
-                            "achieved_gbps_call": round(bytes_q / (ms / 1e3) / 1e9, 1)}
+                            "achieved_gbps_call": round(bytes_q / (ms / 1e3) / 1e9, 1),
+                            "main_kernel": main,
+                            "main_kernel_gbps": round(bytes_q / (kern.get(main, float("nan")) * 1e-6) / 1e9, 1)}
                 log(f"dsv4 {key}: {out[key]}")
                 del g
         del caches, ecaches, c

@@ -143,6 +143,21 @@ __device__ __forceinline__ uint32_t lane_xor(uint32_t x, int lane) {
   }
 }
 
+// Wavefront-local ordering point for LDS traffic between lanes of one wavefront.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+}
+
+// Workgroup barrier that orders LDS traffic only.  Global loads issued before
+// it stay in flight (__syncthreads() also waits for every outstanding global
+// access), so a kernel can prefetch across it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);

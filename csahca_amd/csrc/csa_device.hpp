@@ -17,12 +17,6 @@ __device__ __forceinline__ int lanes_below(unsigned long long bal) {
                                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(bal), 0u)));
 }
 
-// Wavefront-local ordering point for LDS traffic between lanes of one wavefront.
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-  __builtin_amdgcn_wave_barrier();
-}
-
 // Slot s -> token of chunk ids[s / chunk] (chunk_shift >= 0 when chunk is a
 // power of two).  False when the chunk id is negative or the token is past
 // seq_len (csrc/csa_attention.cu:176-185).

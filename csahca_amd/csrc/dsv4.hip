@@ -17,6 +17,7 @@
 
 #include <algorithm>
 #include <climits>
+#include <cstdlib>
 
 namespace csahca {
 namespace {
@@ -79,11 +80,21 @@ __device__ __forceinline__ void load_row8(const uint8_t* __restrict__ row,
       lo = p[0] | (p[1] << 8) | (p[2] << 16) | (static_cast<uint32_t>(p[3]) << 24);
       hi = p[4] | (p[5] << 8) | (p[6] << 16) | (static_cast<uint32_t>(p[7]) << 24);
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      kv[i] = e4m3_to_f32((lo >> (8 * i)) & 0xffu) * s;
-      kv[4 + i] = e4m3_to_f32((hi >> (8 * i)) & 0xffu) * s;
-    }
+    // v_cvt_pk_f32_fp8 decodes OCP e4m3fn exactly (all 256 codes checked on
+    // the device); the products with 2^(b-127) are exact in fp32.
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    const f32x2_t p0 = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(lo), false);
+    const f32x2_t p1 = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(lo), true);
+    const f32x2_t p2 = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(hi), false);
+    const f32x2_t p3 = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(hi), true);
+    kv[0] = p0[0] * s;
+    kv[1] = p0[1] * s;
+    kv[2] = p1[0] * s;
+    kv[3] = p1[1] * s;
+    kv[4] = p2[0] * s;
+    kv[5] = p2[1] * s;
+    kv[6] = p3[0] * s;
+    kv[7] = p3[1] * s;
   } else {
     const uint8_t* p = row + kNope + 16 * (lane - kNope / 8);
     uint32_t w[4];
@@ -291,6 +302,278 @@ __global__ __launch_bounds__(64) void dsv4_tile_kernel(const T* __restrict__ q, 
   }
 }
 
+// ---------------------------------------------------------------------------
+// Grouped-head MFMA path (bf16 queries): one workgroup = (query, 16 heads,
+// split of the slot list), tiles of 32 slots.  QK^T and PV are real
+// contractions here (16 heads share each latent row), so they run on
+// v_mfma_f32_16x16x32_bf16 with fp32 accumulation:
+//   * the 4 wavefronts split the 512-dim contraction of QK^T (wave w owns
+//     dims [128w, 128w+128)); lane l loads 8 consecutive latent bytes of slot
+//     l%16 (+16) -- exactly the MFMA B layout -- dequantises them in registers
+//     (e4m3 x 2^(b-127), rounded to bf16 as the reference dequant does) and
+//     also stores them transposed ([dim][slot]) into LDS for PV;
+//   * the 4 partial score blocks meet in LDS; every wavefront computes the
+//     same online-softmax update, whose probabilities already sit in the MFMA
+//     A layout of PV (lane l: head l%16, slots 8(l/16)..+7);
+//   * wave w accumulates O[16 heads][128w .. 128w+127] over the tiles.
+// Output: (m, l, acc[512]) partials per (query, head, split), merged with the
+// sink by dsv4_merge_kernel.
+// MFMA lane layout (16x16x32 bf16): A lane l elem j = A[l%16][8(l/16)+j];
+// B lane l elem j = B[8(l/16)+j][l%16]; C lane l elem i = C[4(l/16)+i][l%16].
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kMfmaHeads = 16;
+constexpr int kMfmaSlots = 32;
+constexpr int kMfmaWaves = 4;
+constexpr int kMfmaThreads = kMfmaWaves * kWave;
+constexpr int kKStepsPerWave = kDim / 32 / kMfmaWaves;  // 4 k-steps of 32 dims
+constexpr int kNopeSteps = kNope / 32;                  // k-steps 0..13 are e4m3, 14..15 bf16 rope
+constexpr int kOutTiles = kDim / kMfmaWaves / 16;       // 8 blocks of 16 output dims per wave
+
+// 8 e4m3 bytes x 2^(b-127) -> 8 bf16, packed two per word.  The gfx950 scaled
+// conversion gives exactly round_bf16(e4m3 * 2^(b-127)) for scale bytes
+// 0..254 (all 256 codes checked on the device); byte 255 (fp32 scale 2^128 =
+// inf in the reference's arithmetic) takes the software decode.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t bf16x2_bits(bf16x2_t v) { return __builtin_bit_cast(uint32_t, v); }
+
+__device__ __forceinline__ uint4 dequant8_bf16(uint2 w, uint32_t sbyte) {
+  if (sbyte != 255u) {
+    const float s = ue8m0_to_f32(sbyte);
+    return make_uint4(bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w.x, s, false)),
+                      bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w.x, s, true)),
+                      bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w.y, s, false)),
+                      bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w.y, s, true)));
+  }
+  const float s = ue8m0_to_f32(sbyte);
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t word = i < 2 ? w.x : w.y;
+    const uint32_t b0 = (word >> (16 * (i & 1))) & 0xffu;
+    const uint32_t b1 = (word >> (16 * (i & 1) + 8)) & 0xffu;
+    o[i] = static_cast<uint32_t>(float_to_bf16_bits(e4m3_to_f32(b0) * s)) |
+           (static_cast<uint32_t>(float_to_bf16_bits(e4m3_to_f32(b1) * s)) << 16);
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+struct MfmaArgs {
+  int splits;           // slot-list splits per (query, head group)
+  int tiles_per_split;  // 32-slot tiles per split
+  int mfma_groups;      // head groups of 16
+};
+
+__global__ __launch_bounds__(kMfmaThreads) void dsv4_mfma_kernel(const bf16* __restrict__ q, Dsv4Args a,
+                                                                 MfmaArgs m) {
+  __shared__ __align__(16) uint16_t vt[kDim * kMfmaSlots];               // [dim][slot] bf16 bits
+  __shared__ __align__(16) float sp[kMfmaWaves][kMfmaHeads][kMfmaSlots];  // per-wave score partials
+  __shared__ float xch[kMfmaWaves][kMfmaHeads];                           // per-wave head exchange
+
+  const int tid = threadIdx.x;
+  const int wave = tid / kWave;
+  const int lane = tid % kWave;
+  const int grp = lane / 16;  // lane group (MFMA k / row block)
+  const int l16 = lane % 16;
+  const int64_t item = blockIdx.x;
+  const int split = static_cast<int>(item % m.splits);
+  const int64_t rest = item / m.splits;
+  const int hg = static_cast<int>(rest % m.mfma_groups);
+  const int64_t query = rest / m.mfma_groups;
+  const int h0 = hg * kMfmaHeads;
+  const int nh = min(kMfmaHeads, a.heads - h0);
+
+  // Q A-operands of this wave's k-steps: head h0 + l16, dims 32 kk + 8 grp .. +7.
+  bf16x8_t qa[kKStepsPerWave];
+#pragma unroll
+  for (int i = 0; i < kKStepsPerWave; ++i) {
+    const int d0 = 32 * (wave * kKStepsPerWave + i) + 8 * grp;
+    uint4 w = make_uint4(0u, 0u, 0u, 0u);
+    if (l16 < nh) w = *reinterpret_cast<const uint4*>(q + ((query * a.heads) + h0 + l16) * kDim + d0);
+    qa[i] = __builtin_bit_cast(bf16x8_t, w);
+  }
+
+  const int n_swa = a.lens ? max(0, min(a.lens[query], a.topk_slots)) : a.topk_slots;
+  const int n_extra =
+      a.extra_slots > 0 ? (a.elens ? max(0, min(a.elens[query], a.extra_slots)) : a.extra_slots) : 0;
+  const int total = a.topk_slots + a.extra_slots;
+  const int t0 = split * m.tiles_per_split;
+  const int t1 = min(t0 + m.tiles_per_split, (total + kMfmaSlots - 1) / kMfmaSlots);
+
+  float mh = -INFINITY, lh = 0.f;  // softmax state of head l16 (identical in every lane group)
+  f32x4_t o[kOutTiles];
+#pragma unroll
+  for (int j = 0; j < kOutTiles; ++j) o[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // Token location of slot l16 + 16 nt of tile t, or -1 when skipped.
+  auto slot_loc = [&](int t, int nt) -> int32_t {
+    const int s = t * kMfmaSlots + l16 + 16 * nt;
+    if (t >= t1 || s >= total) return -1;
+    if (s < a.topk_slots) return s < n_swa ? a.idx[query * a.topk_slots + s] : -1;
+    const int j = s - a.topk_slots;
+    return j < n_extra ? a.eidx[query * a.extra_slots + j] : -1;
+  };
+  // This lane's latent bytes of a tile: for each slot, the wave's 4 k-steps
+  // (8 e4m3 bytes in .x/.y, or 16 bytes of bf16 rope) and the scale row.
+  struct Rows {
+    uint4 raw[2][kKStepsPerWave];
+    uint2 sc8[2];
+    uint32_t valid;
+  };
+  auto issue_rows = [&](int t, const int32_t* loc, Rows& r) {
+    const uint8_t* rp[2];
+    const uint8_t* srp[2];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      const int s = t * kMfmaSlots + l16 + 16 * nt;
+      rp[nt] = nullptr;
+      srp[nt] = nullptr;
+      if (loc[nt] >= 0) rp[nt] = row_ptr(s < a.topk_slots ? a.swa : a.extra, loc[nt], &srp[nt]);
+    }
+    r.valid = static_cast<uint32_t>(__ballot(rp[0] != nullptr) & 0xffffull) |
+              (static_cast<uint32_t>(__ballot(rp[1] != nullptr) & 0xffffull) << 16);
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) {
+      r.sc8[nt] = make_uint2(0u, 0u);
+#pragma unroll
+      for (int i = 0; i < kKStepsPerWave; ++i) r.raw[nt][i] = make_uint4(0u, 0u, 0u, 0u);
+      if (rp[nt]) {
+        r.sc8[nt] = *reinterpret_cast<const uint2*>(srp[nt]);
+#pragma unroll
+        for (int i = 0; i < kKStepsPerWave; ++i) {
+          const int kk = wave * kKStepsPerWave + i;
+          const int d0 = 32 * kk + 8 * grp;
+          if (kk < kNopeSteps) {
+            const uint2 w = *reinterpret_cast<const uint2*>(rp[nt] + d0);
+            r.raw[nt][i] = make_uint4(w.x, w.y, 0u, 0u);
+          } else {
+            r.raw[nt][i] = *reinterpret_cast<const uint4*>(rp[nt] + kNope + 2 * (d0 - kNope));
+          }
+        }
+      }
+    }
+  };
+
+  // Two-stage pipeline: while tile t is processed, the rows of tile t+1 and
+  // the slot locations of tile t+2 are in flight (lds_barrier keeps them so).
+  Rows cur, nxt;
+  int32_t loc[2] = {slot_loc(t0, 0), slot_loc(t0, 1)};
+  issue_rows(t0, loc, cur);
+  int32_t loc_n[2] = {slot_loc(t0 + 1, 0), slot_loc(t0 + 1, 1)};
+  for (int t = t0; t < t1; ++t) {
+    if (t + 1 < t1) issue_rows(t + 1, loc_n, nxt);
+    const int32_t loc_nn[2] = {slot_loc(t + 2, 0), slot_loc(t + 2, 1)};
+    const uint32_t valid = cur.valid;  // same mask in every wavefront: workgroup-uniform
+    if (valid != 0u) {
+      // Dequantise, store V^T, and accumulate this wave's share of QK^T.
+      f32x4_t sacc[2];
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) {
+        sacc[nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        const int slot = l16 + 16 * nt;
+#pragma unroll
+        for (int i = 0; i < kKStepsPerWave; ++i) {
+          const int kk = wave * kKStepsPerWave + i;
+          const int d0 = 32 * kk + 8 * grp;
+          uint4 kb;
+          if (kk < kNopeSteps) {
+            const int blk = kk / 2;
+            const uint32_t sbyte = (blk < 4 ? cur.sc8[nt].x >> (8 * blk) : cur.sc8[nt].y >> (8 * (blk - 4))) & 0xffu;
+            kb = dequant8_bf16(make_uint2(cur.raw[nt][i].x, cur.raw[nt][i].y), sbyte);
+          } else {
+            kb = cur.raw[nt][i];
+          }
+          const uint32_t kw[4] = {kb.x, kb.y, kb.z, kb.w};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            vt[(d0 + 2 * j) * kMfmaSlots + slot] = static_cast<uint16_t>(kw[j] & 0xffffu);
+            vt[(d0 + 2 * j + 1) * kMfmaSlots + slot] = static_cast<uint16_t>(kw[j] >> 16);
+          }
+          sacc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[i], __builtin_bit_cast(bf16x8_t, kb), sacc[nt],
+                                                             0, 0, 0);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sp[wave][4 * grp + e][slot] = sacc[nt][e];
+      }
+      lds_barrier();
+
+      // Scores of head l16, slots 8 grp .. 8 grp + 7 (the PV A layout).
+      float x[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[j] = 0.f;
+#pragma unroll
+      for (int w = 0; w < kMfmaWaves; ++w) {
+        const float4 u = *reinterpret_cast<const float4*>(&sp[w][l16][8 * grp]);
+        const float4 v = *reinterpret_cast<const float4*>(&sp[w][l16][8 * grp + 4]);
+        x[0] += u.x; x[1] += u.y; x[2] += u.z; x[3] += u.w;
+        x[4] += v.x; x[5] += v.y; x[6] += v.z; x[7] += v.w;
+      }
+      float mb = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        x[j] = ((valid >> (8 * grp + j)) & 1u) ? x[j] * a.qscale : -INFINITY;
+        mb = fmaxf(mb, x[j]);
+      }
+      mb = fmaxf(mb, __uint_as_float(lane_xor<16>(__float_as_uint(mb), lane)));
+      mb = fmaxf(mb, __uint_as_float(lane_xor<32>(__float_as_uint(mb), lane)));
+      const float m_new = fmaxf(mh, mb);  // finite: the tile has a valid slot
+      const float alpha = fast_exp2(mh - m_new);
+      float ps = 0.f;
+      uint32_t pw[4];
+#pragma unroll
+      for (int j = 0; j < 8; j += 2) {
+        const float p0 = fast_exp2(x[j] - m_new), p1 = fast_exp2(x[j + 1] - m_new);
+        ps += p0 + p1;
+        pw[j / 2] = static_cast<uint32_t>(float_to_bf16_bits(p0)) |
+                    (static_cast<uint32_t>(float_to_bf16_bits(p1)) << 16);
+      }
+      ps += __uint_as_float(lane_xor<16>(__float_as_uint(ps), lane));
+      ps += __uint_as_float(lane_xor<32>(__float_as_uint(ps), lane));
+      lh = lh * alpha + ps;
+      mh = m_new;
+      // alpha per output row (head 4 grp + e of the C layout) through LDS.
+      if (lane < kMfmaHeads) xch[wave][lane] = alpha;
+      wave_lds_sync();
+      float ar[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ar[e] = xch[wave][4 * grp + e];
+      const bf16x8_t pa = __builtin_bit_cast(bf16x8_t, make_uint4(pw[0], pw[1], pw[2], pw[3]));
+#pragma unroll
+      for (int j = 0; j < kOutTiles; ++j) {
+        const int d = wave * (kDim / kMfmaWaves) + 16 * j + l16;
+        const uint4 vb = *reinterpret_cast<const uint4*>(&vt[d * kMfmaSlots + 8 * grp]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[j][e] *= ar[e];
+        o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, __builtin_bit_cast(bf16x8_t, vb), o[j], 0, 0, 0);
+      }
+      lds_barrier();  // vt / sp are rewritten by the next tile
+    }
+    cur = nxt;
+    loc_n[0] = loc_nn[0];
+    loc_n[1] = loc_nn[1];
+  }
+
+  // Partials: m, l of head l16 (wave 0, lane group 0), acc rows of the C layout.
+  const int64_t pbase = (query * a.heads + h0) * m.splits + split;  // + h * splits
+  if (wave == 0 && lane < nh) {
+    const int64_t pi = pbase + static_cast<int64_t>(lane) * m.splits;
+    a.part_ml[2 * pi] = mh;
+    a.part_ml[2 * pi + 1] = lh;
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int h = 4 * grp + e;
+    if (h < nh) {
+      float* dst = a.part_acc + (pbase + static_cast<int64_t>(h) * m.splits) * kDim + wave * (kDim / kMfmaWaves) + l16;
+#pragma unroll
+      for (int j = 0; j < kOutTiles; ++j) dst[16 * j] = o[j][e];
+    }
+  }
+}
+
 constexpr int kMergeThreads = kDim / 4;  // 4 output columns per thread
 constexpr int kMergeChunk = 1024;        // tile weights staged in LDS per pass
 
@@ -389,6 +672,24 @@ size_t ws_bytes(int64_t nq, int64_t heads, int64_t tiles) {
   return ((ml + 255) & ~size_t{255}) + static_cast<size_t>(nq * heads * tiles * kDim) * sizeof(float);
 }
 
+// MFMA path split of each query's slot list: enough (query, head group,
+// split) workgroups for ~256 CUs, whole 32-slot tiles per split.
+void mfma_splits(int64_t nq, int64_t heads, int64_t total_slots, int64_t* splits_out, int64_t* tps_out) {
+  const int64_t groups = ceil_div(std::max<int64_t>(1, heads), kMfmaHeads);
+  const int64_t ntiles = std::max<int64_t>(1, ceil_div(total_slots, kMfmaSlots));
+  const int64_t wgs = std::max<int64_t>(1, nq * groups);
+  int64_t splits = wgs < 256 ? std::min(ntiles, ceil_div(256, wgs)) : 1;
+  const int64_t tps = ceil_div(ntiles, splits);
+  *splits_out = ceil_div(ntiles, tps);
+  *tps_out = tps;
+}
+
+// CSAHCA_DSV4_MFMA=0 keeps every call on the VALU kernels (read per call).
+bool mfma_enabled() {
+  const char* e = std::getenv("CSAHCA_DSV4_MFMA");
+  return !(e && e[0] == '0');
+}
+
 struct Dsv4Call {
   const void* q;
   int dtype;
@@ -415,8 +716,19 @@ int dsv4_run(const Dsv4Call& c) {
   CSAHCA_REQUIRE(c.idx || c.topk_slots == 0 || c.nq == 0, "null token_indices pointer");
   const int64_t total = c.topk_slots + c.extra_slots;
   CSAHCA_REQUIRE(total <= INT_MAX && c.nq <= INT_MAX && c.heads <= INT_MAX, "too many slots");
-  int64_t tile, tiles;
-  dsv4_tiling(c.nq, c.heads, total, c.tile_size, &tile, &tiles);
+  const bool vec = reinterpret_cast<uintptr_t>(c.swa.base) % 16 == 0 && c.swa.bpp % 16 == 0 &&
+                   (c.extra_slots == 0 ||
+                    (reinterpret_cast<uintptr_t>(c.extra.base) % 16 == 0 && c.extra.bpp % 16 == 0));
+  // Grouped-head MFMA path: bf16 queries, automatic split, 16-byte aligned rows.
+  const bool use_mfma = c.dtype == CSAHCA_BF16 && c.tile_size == 0 && vec &&
+                        reinterpret_cast<uintptr_t>(c.q) % 16 == 0 && mfma_enabled();
+  int64_t tile, tiles, tps = 0;
+  if (use_mfma) {
+    mfma_splits(c.nq, c.heads, total, &tiles, &tps);
+    tile = tps * kMfmaSlots;
+  } else {
+    dsv4_tiling(c.nq, c.heads, total, c.tile_size, &tile, &tiles);
+  }
   const int64_t head_groups = ceil_div(c.heads, kHeadGroup);
   CSAHCA_REQUIRE(c.nq * head_groups * tiles <= INT32_MAX, "too many DSV4 work items");
   const size_t need = ws_bytes(c.nq, c.heads, tiles);
@@ -439,10 +751,20 @@ int dsv4_run(const Dsv4Call& c) {
   a.tile = static_cast<int>(tile);
   a.num_tiles = static_cast<int>(tiles);
   a.qscale = static_cast<float>(c.softmax_scale) * kLog2e;
-  const bool vec = reinterpret_cast<uintptr_t>(c.swa.base) % 16 == 0 && c.swa.bpp % 16 == 0 &&
-                   (c.extra_slots == 0 ||
-                    (reinterpret_cast<uintptr_t>(c.extra.base) % 16 == 0 && c.extra.bpp % 16 == 0));
   hipStream_t stream = static_cast<hipStream_t>(c.stream);
+  if (use_mfma) {
+    MfmaArgs mm;
+    mm.splits = static_cast<int>(tiles);
+    mm.tiles_per_split = static_cast<int>(tps);
+    mm.mfma_groups = static_cast<int>(ceil_div(c.heads, kMfmaHeads));
+    const dim3 mgrid(static_cast<uint32_t>(c.nq * mm.mfma_groups * tiles));
+    const int rc = launch("dsv4_mfma_kernel", dsv4_mfma_kernel, mgrid, dim3(kMfmaThreads), 0, stream,
+                          static_cast<const bf16*>(c.q), a, mm);
+    if (rc != CSAHCA_OK) return rc;
+    return launch("dsv4_merge_kernel", dsv4_merge_kernel<bf16>, dim3(static_cast<uint32_t>(c.nq * c.heads)),
+                  dim3(kMergeThreads), 0, stream, static_cast<const float*>(a.part_ml),
+                  static_cast<const float*>(a.part_acc), c.sink, static_cast<bf16*>(c.out), a.heads, a.num_tiles);
+  }
   const dim3 grid(static_cast<uint32_t>(c.nq * head_groups * tiles));
   return dispatch_dtype(c.dtype, [&](auto tag) -> int {
     using T = decltype(tag);
@@ -480,9 +802,11 @@ extern "C" size_t csahca_dsv4_decode_workspace_bytes(int64_t num_queries, int64_
                                                      int64_t topk_slots, int64_t extra_topk_slots,
                                                      int64_t tile_size) {
   if (num_queries < 0 || heads < 0 || topk_slots < 0 || extra_topk_slots < 0) return 0;
-  int64_t tile, tiles;
+  int64_t tile, tiles, splits, tps;
   dsv4_tiling(num_queries, heads, topk_slots + extra_topk_slots, tile_size, &tile, &tiles);
-  return ws_bytes(num_queries, heads, tiles);
+  mfma_splits(num_queries, heads, topk_slots + extra_topk_slots, &splits, &tps);
+  // either path may run (the MFMA one for bf16 queries with automatic tiling)
+  return ws_bytes(num_queries, heads, tile_size > 0 ? tiles : std::max(tiles, splits));
 }
 
 extern "C" int csahca_dsv4_decode_forward_tiled(

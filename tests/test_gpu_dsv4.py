@@ -176,3 +176,20 @@ def test_e4m3_and_scale_decode_exhaustive():
     got = out[:, 0].cpu().numpy().astype(np.float64)
     # the oracle dequant rounds nope values to bf16 (exact for e4m3 * 2^k)
     assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("ratio,nq,heads", [(0, 1, 8), (4, 3, 24), (128, 2, 64), (4, 7, 70), (0, 5, 16)])
+def test_mfma_path_matches_valu_path_and_oracle(ratio, nq, heads, monkeypatch):
+    """bf16 queries with automatic tiling take the grouped-head MFMA kernel;
+    CSAHCA_DSV4_MFMA=0 keeps the VALU kernels.  Both against the oracle, with
+    ragged lengths, -1 slots and heads not a multiple of 16."""
+    page = 256 if ratio == 128 else 64  # extra pages hold page/ratio tokens (>= 1)
+    c = make_dsv4_case(compress_ratio=ratio, num_queries=nq, heads=heads, num_tokens=512, top_k=96, page_size=page,
+                       extra_tokens=512, extra_top_k=40, seed=11 + heads, device=DEV)
+    c.token_indices[0, 5] = -1
+    ref = oracle_out(c)
+    got_mfma = gpu_out(c)
+    monkeypatch.setenv("CSAHCA_DSV4_MFMA", "0")
+    got_valu = gpu_out(c)
+    assert_close(got_mfma, ref, what="mfma")
+    assert_close(got_valu, ref, what="valu")
