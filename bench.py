@@ -56,6 +56,7 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-dsv4", action="store_true")
     ap.add_argument("--no-hca", action="store_true")
+    ap.add_argument("--no-block", action="store_true")
     ap.add_argument("--sweep", action="store_true", help="also run the BASELINE config-2 sweep (stderr + json)")
     ap.add_argument("--sweep-out", type=Path, default=None)
     ap.add_argument("--no-graph", action="store_true",
@@ -355,6 +356,92 @@ def hca_bench(steps=256, copies=4, hca_chunk=256):
     return out
 
 
+def block_bench(steps=200, warmup=20):
+    """BASELINE config 3 on the decode blocks of csahca_amd.block, at S=32768,
+    H=8, D=128 (hidden 1024), chunk 64, top-8, bf16, 200 steps after 20 warm-up
+    steps, the hidden state fed back each step (the reference harness,
+    hybrid_attention/model_inference.py:140-162).  Like that harness it reuses
+    one static cache (no rotation).  Reference block: precomputed selection
+    (tiled op, tile 8) and dynamic selection (fused step from cached summaries,
+    and from summaries rebuilt every step as the reference does), eager and as
+    one HIP graph per step.  BASELINE block (RMSNorm/QKV/SiLU MLP, growing
+    cache): eager, since shapes change as chunks complete."""
+    import torch
+
+    from csahca_amd import native
+    from csahca_amd.block import HybridDecodeBlock, MiniCSADecodeBlock
+
+    dev = torch.device("cuda", 0)
+    B, H, D, S, chunk, k = 1, 8, 128, 32768, 64, 8
+    g = torch.Generator(device=dev).manual_seed(0)
+    hidden0 = torch.randn(B, H * D, dtype=torch.bfloat16, device=dev, generator=g)
+    kc = torch.randn(B, H, S, D, dtype=torch.bfloat16, device=dev, generator=g)
+    vc = torch.randn(B, H, S, D, dtype=torch.bfloat16, device=dev, generator=g)
+    summ = native.csa_chunk_summary(kc, chunk)
+
+    def timed(fn, n):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / n
+
+    out = {"config": f"B{B} H{H} D{D} S{S} chunk{chunk} top{k} bf16, {steps} steps + {warmup} warm-up"}
+    for mlp in (2.0, 0.0):
+        blk = MiniCSADecodeBlock(heads=H, head_dim=D, dtype=torch.bfloat16, device=dev, mlp_ratio=mlp, seed=0)
+        q0 = torch.nn.functional.linear(hidden0, blk.w_q).view(B, H, D)
+        sel = native.csa_select_topk(q0, summ, k)
+        modes = {"precomputed": dict(selection="precomputed", selected_chunks=sel),
+                 "dynamic_cached_summary": dict(selection="dynamic", summary=summ)}
+        if mlp == 0.0:
+            modes["dynamic_recomputed_summary"] = dict(selection="dynamic", summary=None)
+        for mode, kw in modes.items():
+            hbuf = hidden0.clone()
+
+            def one():
+                hbuf.copy_(blk(hbuf, kc, vc, chunk_size=chunk, top_k=k, **kw))
+
+            for _ in range(warmup):
+                one()
+            ms_eager = timed(one, steps)
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                one()
+            torch.cuda.current_stream().wait_stream(s)
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                one()
+            ms_graph = timed(gr.replay, steps)
+            row = {"ms_per_token_eager": round(ms_eager, 5), "ms_per_token_graph": round(ms_graph, 5),
+                   "tokens_per_s_graph": round(B / (ms_graph / 1e3), 1)}
+            out[f"mini_mlp{mlp:g}_{mode}"] = row
+            log(f"block mini mlp{mlp:g} {mode}: {row}")
+            del gr
+    for mlp in (2.0, 0.0):
+        hb = HybridDecodeBlock(batch=B, heads=H, head_dim=D, capacity=S + warmup + steps, chunk_size=chunk,
+                               top_k=k, mlp_ratio=mlp, device=dev, seed=0)
+        hb.prefill(kc, vc)
+        hbuf = hidden0.clone()
+
+        def one_h():
+            hbuf.copy_(hb(hbuf))
+
+        for _ in range(warmup):
+            one_h()
+        ms = timed(one_h, steps)
+        row = {"ms_per_token_eager": round(ms, 5), "tokens_per_s": round(B / (ms / 1e3), 1),
+               "final_length": hb.length}
+        out[f"baseline_block_mlp{mlp:g}_growing_cache"] = row
+        log(f"block baseline mlp{mlp:g}: {row}")
+        del hb
+    del kc, vc, summ
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return out
+
+
 def sweep(args):
     rows = []
     for B in (1, 8, 32):
@@ -451,6 +538,8 @@ def main():
     }
     if not args.no_hca:
         line["hca"] = hca_bench()
+    if not args.no_block:
+        line["block"] = block_bench()
     if not args.no_dsv4:
         line["dsv4"] = dsv4_bench()
     if args.sweep:

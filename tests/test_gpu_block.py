@@ -1,0 +1,140 @@
+"""GPU parity of the decode blocks (csahca_amd/block.py).
+
+MiniCSADecodeBlock restates hybrid_attention/model_inference.py:14-76; its
+reference here is the same block on the CPU in torch with identical weights and
+the oracle's CSA (cuda-csa semantics: fp32 probabilities).  HybridDecodeBlock
+is checked step by step against a CPU restatement that
+rounds exactly where the GPU block stores bf16 (q, the appended K/V, every
+linear output).  Tolerance: |got - ref| <= 2e-2 + 1e-2 |ref| on block outputs.
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+from csahca_amd import native
+from csahca_amd.block import HybridDecodeBlock, MiniCSADecodeBlock, rms_norm
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+BF = torch.bfloat16
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.fail("no HIP device visible")
+    native.lib()
+
+
+def assert_close(got, ref, atol=2e-2, rtol=1e-2, what=""):
+    g = got.detach().double().cpu().numpy()
+    r = ref.detach().double().cpu().numpy() if isinstance(ref, torch.Tensor) else np.asarray(ref, np.float64)
+    diff = np.abs(g - r)
+    bad = diff > atol + rtol * np.abs(r)
+    assert not bad.any(), f"{what} max_abs={diff.max():.3e} bad={int(bad.sum())}/{bad.size}"
+
+
+def cpu_csa(q, k, v, selected, chunk):
+    """cuda-csa semantics (fp32 probabilities) from the oracle, rounded to bf16."""
+    out = oracle.csa_attend(q, k, v, selected, chunk, prob_dtype=oracle.F32)
+    return torch.from_numpy(out).to(torch.float32).to(BF)
+
+
+def make_static(B=1, H=8, S=4096, D=128, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    hidden = torch.randn(B, H * D, generator=g).to(BF)
+    k = torch.randn(B, H, S, D, generator=g).to(BF)
+    v = torch.randn(B, H, S, D, generator=g).to(BF)
+    return hidden, k, v
+
+
+@pytest.mark.parametrize("mlp_ratio", [0.0, 2.0])
+def test_mini_block_matches_cpu_restatement(mlp_ratio):
+    hidden, k, v = make_static()
+    blk = MiniCSADecodeBlock(heads=8, head_dim=128, dtype=BF, device=DEV, mlp_ratio=mlp_ratio, seed=1)
+    # CPU restatement with the same weights
+    q = F.linear(hidden, blk.w_q.cpu()).view(1, 8, 128)
+    sel = oracle.select_topk_chunks(q, k, 64, 8)
+    attn = cpu_csa(q, k, v, sel, 64)
+    out = F.linear(attn.reshape(1, 1024), blk.w_out.cpu())
+    if mlp_ratio:
+        out = out + F.linear(F.gelu(F.linear(hidden, blk.w_up.cpu())), blk.w_down.cpu())
+    want = hidden + 0.01 * out
+    sel_t = torch.from_numpy(sel).to(torch.int32).to(DEV)
+    got = blk(hidden.to(DEV), k.to(DEV), v.to(DEV), selection="precomputed", selected_chunks=sel_t)
+    assert_close(got, want, what="precomputed")
+    # dynamic selection (fused step) from cached or per-step summaries selects the same chunks here
+    summ = native.csa_chunk_summary(k.to(DEV), 64)
+    got_dyn = blk(hidden.to(DEV), k.to(DEV), v.to(DEV), selection="dynamic", summary=summ)
+    got_dyn2 = blk(hidden.to(DEV), k.to(DEV), v.to(DEV), selection="dynamic", summary=None)
+    assert torch.equal(got_dyn, got_dyn2)
+    assert_close(got_dyn, want, what="dynamic")
+
+
+def test_mini_block_graph_replays_match_eager():
+    hidden, k, v = (t.to(DEV) for t in make_static(seed=3))
+    blk = MiniCSADecodeBlock(heads=8, head_dim=128, dtype=BF, device=DEV, mlp_ratio=2.0, seed=2)
+    summ = native.csa_chunk_summary(k, 64)
+    eager = blk(hidden, k, v, selection="dynamic", summary=summ)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        blk(hidden, k, v, selection="dynamic", summary=summ)  # warm the stream's workspace
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = blk(hidden, k, v, selection="dynamic", summary=summ)
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        blk(hidden, k, v, selection="dynamic", summary=summ)  # eager work between replays
+
+
+def cpu_hybrid_reference(blk: HybridDecodeBlock, k0, v0, hiddens):
+    """The HybridDecodeBlock step on the CPU: bf16 storage where the GPU block
+    stores bf16, oracle selection over complete chunks, cuda-csa attention."""
+    w = {n: getattr(blk, n).cpu() for n in ("w_qkv", "w_out", "norm1", "norm2")}
+    if blk.use_mlp:
+        w["w_up"], w["w_down"] = blk.w_up.cpu(), blk.w_down.cpu()
+    B, H, D, chunk = blk.batch, blk.heads, blk.head_dim, blk.chunk_size
+    k, v = k0.clone(), v0.clone()
+    outs = []
+    for hidden in hiddens:
+        x = rms_norm(hidden, w["norm1"])
+        qkv = F.linear(x, w["w_qkv"]).view(B, 3, H, D)
+        q = qkv[:, 0].contiguous()
+        k = torch.cat([k, qkv[:, 1].unsqueeze(2)], dim=2)
+        v = torch.cat([v, qkv[:, 2].unsqueeze(2)], dim=2)
+        C = k.shape[2] // chunk
+        summ = oracle.chunk_mean(k[:, :, : C * chunk].contiguous(), chunk)
+        idx, _ = oracle.select_topk(q, summ, blk.top_k)
+        attn = cpu_csa(q, k, v, idx, chunk)
+        h = hidden + F.linear(attn.reshape(B, H * D), w["w_out"])
+        if blk.use_mlp:
+            h = h + F.linear(F.silu(F.linear(rms_norm(h, w["norm2"]), w["w_up"])), w["w_down"])
+        outs.append(h)
+    return outs
+
+
+@pytest.mark.parametrize("mlp_ratio", [0.0, 2.0])
+def test_hybrid_block_steps_match_cpu_across_a_chunk_boundary(mlp_ratio):
+    B, H, D, S0, steps = 1, 4, 64, 250, 10  # the 256th token completes chunk 4 during the run
+    blk = HybridDecodeBlock(batch=B, heads=H, head_dim=D, capacity=512, chunk_size=64, top_k=3, mlp_ratio=mlp_ratio,
+                            device=DEV, seed=5)
+    g = torch.Generator().manual_seed(9)
+    k0 = torch.randn(B, H, S0, D, generator=g).to(BF)
+    v0 = torch.randn(B, H, S0, D, generator=g).to(BF)
+    hiddens = [torch.randn(B, H * D, generator=g).to(BF) for _ in range(steps)]
+    blk.prefill(k0.to(DEV), v0.to(DEV))
+    assert blk.summary.shape[2] == 3
+    want = cpu_hybrid_reference(blk, k0, v0, hiddens)
+    for i, hdn in enumerate(hiddens):
+        got = blk(hdn.to(DEV))
+        assert_close(got, want[i], what=f"step {i}")
+    assert blk.length == S0 + steps and blk.summary.shape[2] == 4
+    # the summary of the chunk completed during decoding equals a fresh build
+    fresh = native.csa_chunk_summary(blk.k_cache[:, :, :256].contiguous(), 64)
+    torch.testing.assert_close(blk.summary, fresh, rtol=0, atol=0)
