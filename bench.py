@@ -299,6 +299,22 @@ def dsv4_bench(steps=200, copies=64):
         del caches, ecaches, c
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
+    # quantize-on-write of the SWA pool's 65536 tokens (1 KiB bf16 in, 584 B out each)
+    T, ps = 65536, 64
+    tok = torch.randn(T, 512, device=dev).to(torch.bfloat16)
+    cache = native.dsv4_pack_tokens(tok, ps)
+    for _ in range(3):
+        native.dsv4_pack_tokens(tok, ps, cache=cache)
+    with native.profile_launches() as prof:
+        for _ in range(20):
+            native.dsv4_pack_tokens(tok, ps, cache=cache)
+    us = prof.results["dsv4_pack_kernel"]["avg_us"]
+    nbytes = T * (1024 + 584)
+    out["pack_65536_tokens"] = {"kernel_us": round(us, 3), "bytes": nbytes,
+                                "achieved_gbps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                                "frac_of_hbm_peak": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)}
+    log(f"dsv4 pack: {out['pack_65536_tokens']}")
+    del tok, cache
     return out
 
 

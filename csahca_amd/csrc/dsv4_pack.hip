@@ -1,0 +1,145 @@
+// dsv4_pack.hip -- quantize-on-write of BF16 latent tokens into the DSV4 paged
+// FP8 cache, for gfx950.
+//
+// Format and rule (hybrid_attention/dsv4_correctness.py:19-59): token loc
+// lives on page loc / page_size at row loc % page_size of 576 bytes -- 448 OCP
+// e4m3fn "nope" bytes, then the 64 bf16 "rope" values verbatim -- and its 7
+// scale bytes sit after the page's rows, 8 bytes per token.  Per 64-value
+// tile: max_abs = max(|v|, 1e-8) (fp32), r = max_abs / 448 (fp32), exponent
+// E = ceil(log2 r), scale byte = clamp(E + 127, 0, 255), stored value =
+// e4m3fn_rne(clamp(v / 2^E, -448, 448)).  Exactly the bytes the reference
+// writes are written (not the scale pad byte, not the page padding).
+//
+// One wavefront per token: lanes 0..55 own 8 nope values each (tile = lane /
+// 8, so a tile's max is a reduction over 8 adjacent lanes), lanes 56..63 copy
+// 16 bytes of rope each.
+#include "common.hpp"
+
+#include <climits>
+
+namespace csahca {
+namespace {
+
+constexpr int kPackNope = 448;
+constexpr int kPackRowBytes = kPackNope + 2 * 64;  // 576
+constexpr int kPackScaleBytes = 8;
+constexpr int kPackWaves = 4;  // tokens per workgroup
+
+// fp32 -> OCP e4m3fn byte, round to nearest even, for |x| <= 448 (larger
+// magnitudes and NaN give the NaN code).  Normal range: keep 3 mantissa bits of
+// the fp32 encoding with RNE on the 20 dropped bits (a carry moves into the
+// exponent); below 2^-6 the quantum is 2^-9.
+__device__ __forceinline__ uint32_t e4m3fn_rne(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const uint32_t sign = (u >> 24) & 0x80u;
+  const uint32_t a = u & 0x7fffffffu;
+  if (a > 0x7f800000u) return sign | 0x7fu;
+  if (a >= 0x3c800000u) {  // |x| >= 2^-6
+    const uint32_t r = (a + 0x7ffffu + ((a >> 20) & 1u)) >> 20;  // (fp32 exponent << 3) | 3-bit mantissa
+    const uint32_t code = r - (120u << 3);                       // rebias 127 -> 7
+    return sign | (code > 0x7eu ? 0x7fu : code);
+  }
+  return sign | static_cast<uint32_t>(__builtin_rintf(__uint_as_float(a) * 512.0f));
+}
+
+// ceil(log2(r)) for a positive finite fp32 r, exactly.
+__device__ __forceinline__ int ceil_log2(float r) {
+  int e;
+  const float m = frexpf(r, &e);  // r = m 2^e, m in [0.5, 1)
+  return m == 0.5f ? e - 1 : e;
+}
+
+template <bool kVec>
+__global__ __launch_bounds__(kPackWaves * kWave) void dsv4_pack_kernel(const uint16_t* __restrict__ tokens,
+                                                                       const int32_t* __restrict__ locs,
+                                                                       int64_t num_tokens, uint8_t* __restrict__ cache,
+                                                                       int64_t num_pages, int64_t bpp,
+                                                                       int page_size) {
+  const int lane = threadIdx.x % kWave;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kPackWaves + threadIdx.x / kWave;
+  if (t >= num_tokens) return;
+  const int64_t loc = locs ? static_cast<int64_t>(locs[t]) : t;
+  if (loc < 0) return;
+  const int64_t page = loc / page_size;
+  if (page >= num_pages) return;
+  const int64_t in_page = loc - page * page_size;
+  uint8_t* pg = cache + page * bpp;
+  uint8_t* row = pg + in_page * kPackRowBytes;
+  const uint16_t* src = tokens + t * 512;
+
+  // 8 bf16 of this lane (nope dims 8 lane.., or rope dims 448 + 8 (lane - 56)..)
+  const uint4 w = *reinterpret_cast<const uint4*>(src + 8 * lane);
+  const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+  if (lane >= kPackNope / 8) {  // rope: the bf16 bytes verbatim
+    uint8_t* dst = row + kPackNope + 16 * (lane - kPackNope / 8);
+    if (kVec) {
+      *reinterpret_cast<uint4*>(dst) = w;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) dst[i] = static_cast<uint8_t>(ww[i / 4] >> (8 * (i % 4)));
+    }
+  }
+  float v[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = __uint_as_float(ww[i] << 16);
+    v[2 * i + 1] = __uint_as_float(ww[i] & 0xffff0000u);
+  }
+  float mx = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(v[i]));
+  // max over the tile's 8 lanes (DPP within aligned groups of 8)
+  mx = fmaxf(mx, __uint_as_float(lane_xor<1>(__float_as_uint(mx), lane)));
+  mx = fmaxf(mx, __uint_as_float(lane_xor<2>(__float_as_uint(mx), lane)));
+  mx = fmaxf(mx, __uint_as_float(lane_xor<4>(__float_as_uint(mx), lane)));
+  if (lane >= kPackNope / 8) return;
+  const float r = fmaxf(mx, 1e-8f) / 448.0f;
+  const int E = ceil_log2(r);
+  const float inv = __builtin_ldexpf(1.0f, -E);  // exact: E in [-35, 121] for bf16 inputs
+  uint32_t b[2] = {0u, 0u};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float qv = fminf(fmaxf(v[i] * inv, -448.0f), 448.0f);
+    b[i / 4] |= e4m3fn_rne(qv) << (8 * (i % 4));
+  }
+  uint8_t* dst = row + 8 * lane;
+  if (kVec) {
+    *reinterpret_cast<uint2*>(dst) = make_uint2(b[0], b[1]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dst[i] = static_cast<uint8_t>(b[i / 4] >> (8 * (i % 4)));
+  }
+  if ((lane & 7) == 0) {
+    const int byte = E + 127;
+    pg[static_cast<int64_t>(page_size) * kPackRowBytes + in_page * kPackScaleBytes + (lane >> 3)] =
+        static_cast<uint8_t>(byte < 0 ? 0 : (byte > 255 ? 255 : byte));
+  }
+}
+
+}  // namespace
+}  // namespace csahca
+
+using namespace csahca;
+
+extern "C" int csahca_dsv4_pack_tokens(const void* k_tokens, const int32_t* locs, int64_t num_tokens,
+                                       uint8_t* cache, int64_t num_pages, int64_t bytes_per_page,
+                                       int64_t page_size, void* stream_ptr) {
+  clear_error();
+  CSAHCA_REQUIRE(num_tokens >= 0 && num_pages >= 0 && bytes_per_page >= 0, "negative dimension");
+  CSAHCA_REQUIRE(page_size > 0 && page_size <= INT_MAX, "page_size must be positive");
+  CSAHCA_REQUIRE(bytes_per_page >= page_size * (kPackRowBytes + kPackScaleBytes),
+                 "bytes_per_page is too small for DSV4 page layout");
+  if (num_tokens == 0 || num_pages == 0) return CSAHCA_OK;
+  CSAHCA_REQUIRE(k_tokens && cache, "null tensor pointer");
+  CSAHCA_REQUIRE(reinterpret_cast<uintptr_t>(k_tokens) % 16 == 0, "k_tokens must be 16-byte aligned");
+  const int64_t blocks = ceil_div(num_tokens, kPackWaves);
+  CSAHCA_REQUIRE(blocks <= INT32_MAX, "too many tokens in one call");
+  const bool vec = reinterpret_cast<uintptr_t>(cache) % 16 == 0 && bytes_per_page % 16 == 0;
+  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  const dim3 grid(static_cast<uint32_t>(blocks));
+  const uint16_t* tp = static_cast<const uint16_t*>(k_tokens);
+  return vec ? launch("dsv4_pack_kernel", dsv4_pack_kernel<true>, grid, dim3(kPackWaves * kWave), 0, stream, tp,
+                      locs, num_tokens, cache, num_pages, bytes_per_page, static_cast<int>(page_size))
+             : launch("dsv4_pack_kernel", dsv4_pack_kernel<false>, grid, dim3(kPackWaves * kWave), 0, stream, tp,
+                      locs, num_tokens, cache, num_pages, bytes_per_page, static_cast<int>(page_size));
+}

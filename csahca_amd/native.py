@@ -59,6 +59,7 @@ _SIGNATURES = {
     "csahca_csa_decode_step": (_int, [_vp] * 6 + [_int] + [_i64] * 7 + [_vp, _sz, _vp]),
     "csahca_csa_step_status": (_int, [_vp, ctypes.POINTER(ctypes.c_uint32), _vp]),
     "csahca_hca_decode_workspace_bytes": (_sz, [_i64] * 5),
+    "csahca_dsv4_pack_tokens": (_int, [_vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp]),
     "csahca_hca_decode_forward": (_int, [_vp, _vp, _vp, _vp, _dbl, _vp, _int] + [_i64] * 5 + [_vp, _sz, _vp]),
     "csahca_profile_begin": (_int, []),
     "csahca_profile_end": (_int, []),
@@ -522,3 +523,33 @@ class profile_launches:
             self.results[name.value.decode()] = dict(launches=cnt.value, total_ms=tot.value, min_ms=mn.value,
                                                      max_ms=mx.value, avg_us=1e3 * tot.value / max(cnt.value, 1))
         return False
+
+
+def dsv4_pack_tokens(k_tokens, page_size, *, cache=None, locs=None):
+    """pack_dsv4_cache (hybrid_attention/dsv4_correctness.py:24-59) on the GPU:
+    quantise [T, 512] bf16 tokens into the paged FP8 layout.  Without ``cache``
+    a zeroed [ceil(T/page_size), bytes_per_page] uint8 cache is allocated and
+    token t written at location t, exactly as the reference does; with
+    ``cache`` (and optionally int32 ``locs``) tokens are written in place at
+    their locations -- the quantize-on-write of a serving cache."""
+    page_size = int(page_size)
+    _check(k_tokens.is_cuda and k_tokens.dtype == torch.bfloat16, "k_tokens must be bfloat16")
+    _check(k_tokens.dim() == 2 and k_tokens.shape[1] == _DSV4_HEAD_DIM, "k_tokens must be [tokens, 512]")
+    _check(page_size > 0, "page_size must be positive")
+    k_tokens = k_tokens.contiguous()
+    T = k_tokens.shape[0]
+    lib()  # fail before allocating when the library is missing
+    with torch.cuda.device(k_tokens.device):
+        if cache is None:
+            from .dsv4_layout import bytes_per_page
+            cache = torch.zeros(((T + page_size - 1) // page_size, bytes_per_page(page_size)), dtype=torch.uint8,
+                                device=k_tokens.device)
+        _check(cache.is_cuda and cache.dim() == 2 and cache.is_contiguous(),
+               "paged_k_cache_u8 must be [num_pages, bytes_per_page]")
+        cache_u8 = cache.view(torch.uint8)
+        if locs is not None:
+            _check(locs.is_cuda and locs.dtype == torch.int32 and locs.numel() == T, "locs must be int32 [tokens]")
+            locs = locs.contiguous()
+        _rc(lib().csahca_dsv4_pack_tokens(_ptr(k_tokens), _ptr(locs), T, _ptr(cache_u8), cache_u8.shape[0],
+                                          cache_u8.shape[1], page_size, _stream()))
+    return cache

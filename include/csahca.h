@@ -204,6 +204,17 @@ int csahca_dsv4_sparse_decode_forward(
     const int32_t* extra_topk_lengths, const float* attn_sink, double softmax_scale, void* out,
     void* workspace, size_t workspace_bytes, void* stream);
 
+/* Quantize-on-write into the DSV4 cache: replaces pack_dsv4_cache
+ * (hybrid_attention/dsv4_correctness.py:24-59).  k_tokens: [num_tokens, 512]
+ * bf16 (16-byte aligned); token t goes to cache location locs[t] (or t when
+ * locs is NULL): page loc / page_size, row loc % page_size.  Per 64-value nope
+ * tile: E = ceil(log2(max(max|v|, 1e-8) / 448)), scale byte clamp(E+127, 0, 255),
+ * bytes e4m3fn_rne(clamp(v / 2^E, -448, 448)); rope bf16 copied verbatim.  Writes
+ * only those bytes (the reference's zero-initialised padding is the caller's).
+ * Negative locations and pages at or beyond num_pages are skipped. */
+int csahca_dsv4_pack_tokens(const void* k_tokens, const int32_t* locs, int64_t num_tokens, uint8_t* cache,
+                            int64_t num_pages, int64_t bytes_per_page, int64_t page_size, void* stream);
+
 /* ------------------------------------------------------------------------- */
 /* Launch profiler (measurement aid; no counterpart in the reference)         */
 /* ------------------------------------------------------------------------- */
