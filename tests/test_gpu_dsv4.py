@@ -193,3 +193,27 @@ def test_mfma_path_matches_valu_path_and_oracle(ratio, nq, heads, monkeypatch):
     got_valu = gpu_out(c)
     assert_close(got_mfma, ref, what="mfma")
     assert_close(got_valu, ref, what="valu")
+
+
+def test_sglang_adapter_end_to_end(monkeypatch):
+    """FlashMLA-shaped decode metadata through csahca_amd.sglang_dsv4 equals the
+    2-D op call and the oracle."""
+    import types
+
+    from csahca_amd import sglang_dsv4
+
+    monkeypatch.setenv("CSAHCA_DSV4_NATIVE", "1")
+    c = make_dsv4_case(compress_ratio=4, num_queries=4, heads=16, num_tokens=512, top_k=64, page_size=64,
+                       extra_tokens=512, extra_top_k=32, seed=21, device=DEV)
+    ps, eps = c.page_size, c.extra_page_size
+    pool = types.SimpleNamespace(get_extra_key_page_size=lambda layer: eps)
+    mode = types.SimpleNamespace(name="DECODE", is_decode_or_idle=lambda: True)
+    out = sglang_dsv4.maybe_dsv4_decode_forward(
+        q=c.q.unsqueeze(1), layer_id=0, compress_ratio=4, forward_batch=types.SimpleNamespace(forward_mode=mode),
+        token_to_kv_pool=pool, swa_k_cache=c.cache.view(c.cache.shape[0], ps, 1, -1),
+        swa_page_indices=c.token_indices.unsqueeze(1), swa_topk_lengths=c.topk_lengths,
+        extra_k_cache=c.extra_cache.view(c.extra_cache.shape[0], eps, 1, -1),
+        extra_indices=c.extra_token_indices.unsqueeze(1), extra_topk_lengths=c.extra_topk_lengths,
+        attn_sink=c.attn_sink, page_size=ps, softmax_scale=SCALE)
+    assert torch.equal(out, gpu_out(c))
+    assert_close(out, oracle_out(c))
