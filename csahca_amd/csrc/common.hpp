@@ -158,9 +158,25 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Value of lane (lane ^ off), off in {1, 2, 4, 8, 16, 32} (a constant once the
+// caller's loop is unrolled): DPP / row-swap moves, no LDS round trip.  The
+// whole wavefront must be active.
+__device__ __forceinline__ float xor_lanes(float v, int off) {
+  const int lane = static_cast<int>(__lane_id());
+  const uint32_t u = __float_as_uint(v);
+  switch (off) {
+    case 1: return __uint_as_float(lane_xor<1>(u, lane));
+    case 2: return __uint_as_float(lane_xor<2>(u, lane));
+    case 4: return __uint_as_float(lane_xor<4>(u, lane));
+    case 8: return __uint_as_float(lane_xor<8>(u, lane));
+    case 16: return __uint_as_float(lane_xor<16>(u, lane));
+    default: return __uint_as_float(lane_xor<32>(u, lane));
+  }
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+  for (int off = 32; off >= 1; off >>= 1) v += xor_lanes(v, off);
   return v;
 }
 

@@ -141,10 +141,12 @@ __global__ __launch_bounds__(64) void csa_attend_generic_kernel(
   }
 }
 
+constexpr int kMergeRows = 64;  // partial rows per thread in the one-round-trip merge
+
 // Block-wide reductions for 256-thread blocks.
 __device__ __forceinline__ float block_max256(float v, float* red) {
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, xor_lanes(v, off));
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
   v = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
@@ -171,8 +173,43 @@ __global__ __launch_bounds__(256) void csa_merge_kernel(const float* __restrict_
                                                         T* __restrict__ out, int D, int num_tiles) {
   __shared__ float red[4];
   __shared__ float colsum[256];
+  __shared__ float wts[256];
   const int64_t bh = blockIdx.x;
   const float* ml = part_ml + 2 * bh * num_tiles;
+  const float* pa = part_acc + bh * num_tiles * static_cast<int64_t>(D);
+  const int tid = threadIdx.x;
+  if (D <= 256 && num_tiles <= 256 && num_tiles <= kMergeRows * (256 / D)) {
+    // One memory round trip: every thread requests its column of each of its
+    // partial rows and (m, l) of tile `tid` before anything waits; the tile
+    // weights then meet in LDS.
+    const int G = 256 / D, g = tid / D, d = tid - g * D;
+    float x[kMergeRows];
+#pragma unroll
+    for (int i = 0; i < kMergeRows; ++i) {
+      const int t = g + i * G;
+      x[i] = (g < G && t < num_tiles) ? pa[static_cast<int64_t>(t) * D + d] : 0.f;
+    }
+    const float mt = tid < num_tiles ? ml[2 * tid] : -INFINITY;
+    const float lt = tid < num_tiles ? ml[2 * tid + 1] : 0.f;
+    const float M = block_max256(lt > 0.f ? mt : -INFINITY, red);
+    const float w = (lt > 0.f && M != -INFINITY) ? fast_exp2(mt - M) : 0.f;
+    wts[tid] = w;
+    const float Lt = block_sum256(w * lt, red);  // its barriers also publish wts
+    float a = 0.f;
+#pragma unroll
+    for (int i = 0; i < kMergeRows; ++i) {
+      const int t = g + i * G;
+      if (g < G && t < num_tiles) a = fmaf(wts[t], x[i], a);
+    }
+    colsum[tid] = a;
+    __syncthreads();
+    if (tid < D) {
+      float o = 0.f;
+      for (int j = 0; j < G; ++j) o += colsum[j * D + tid];
+      out[bh * D + tid] = from_f32<T>(Lt > 0.f ? o / Lt : 0.f);
+    }
+    return;
+  }
   float mx = -INFINITY;
   for (int t = threadIdx.x; t < num_tiles; t += 256) mx = fmaxf(mx, ml[2 * t]);
   mx = block_max256(mx, red);
@@ -185,7 +222,6 @@ __global__ __launch_bounds__(256) void csa_merge_kernel(const float* __restrict_
   }
   L = block_sum256(L, red);
   const float inv = (mx != -INFINITY && L > 0.f) ? 1.f / L : 0.f;
-  const float* pa = part_acc + bh * num_tiles * static_cast<int64_t>(D);
   const int G = D >= 256 ? 1 : 256 / D;
   const int g = threadIdx.x / (D >= 256 ? 256 : D);
   for (int d0 = 0; d0 < D; d0 += (D >= 256 ? 256 : D)) {
@@ -252,7 +288,7 @@ __global__ __launch_bounds__(64) void csa_summary_vec_kernel(const T* __restrict
 #pragma unroll
   for (int off = LPR; off < kWave; off <<= 1)
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) acc[e] += __shfl_xor(acc[e], off, kWave);
+    for (int e = 0; e < VEC; ++e) acc[e] += xor_lanes(acc[e], off);
   if (grp == 0) {
     float* dst = summary + (bh * summary_chunks + c) * D + col * VEC;
     const float fc = static_cast<float>(chunk);

@@ -335,7 +335,7 @@ __device__ __forceinline__ void attend_block(WaveSoftmax<T, D>& st, const float*
 #pragma unroll
   for (int off = LPR / 2; off >= 1; off >>= 1) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) sc[u] += __shfl_xor(sc[u], off, kWave);
+    for (int u = 0; u < U; ++u) sc[u] += xor_lanes(sc[u], off);
   }
   float mx = -INFINITY;
 #pragma unroll
@@ -344,7 +344,7 @@ __device__ __forceinline__ void attend_block(WaveSoftmax<T, D>& st, const float*
     mx = fmaxf(mx, sc[u]);
   }
 #pragma unroll
-  for (int off = LPR; off < kWave; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
+  for (int off = LPR; off < kWave; off <<= 1) mx = fmaxf(mx, xor_lanes(mx, off));
   const float m_new = fmaxf(st.m, mx);
   if (m_new == -INFINITY) return;  // wavefront-uniform: nothing valid yet
   const float alpha = fast_exp2(st.m - m_new);
@@ -368,9 +368,9 @@ __device__ __forceinline__ void fold_row_groups(WaveSoftmax<T, D>& st) {
   using L = AttendLayout<T, D>;
 #pragma unroll
   for (int off = L::LPR; off < kWave; off <<= 1) {
-    st.l += __shfl_xor(st.l, off, kWave);
+    st.l += xor_lanes(st.l, off);
 #pragma unroll
-    for (int e = 0; e < L::VEC; ++e) st.acc[e] += __shfl_xor(st.acc[e], off, kWave);
+    for (int e = 0; e < L::VEC; ++e) st.acc[e] += xor_lanes(st.acc[e], off);
   }
 }
 
@@ -395,7 +395,7 @@ __device__ __forceinline__ void score_block(const float* qf4, const float* __res
 #pragma unroll
   for (int off = LPR / 2; off >= 1; off >>= 1)
 #pragma unroll
-    for (int u = 0; u < U; ++u) sc[u] += __shfl_xor(sc[u], off, kWave);
+    for (int u = 0; u < U; ++u) sc[u] += xor_lanes(sc[u], off);
 }
 
 }  // namespace csahca

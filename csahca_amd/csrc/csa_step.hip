@@ -10,8 +10,9 @@
 //   C. workgroup p attends the selected-token slots [T*p/P, T*(p+1)/P) (T = k *
 //      chunk) -- chunk ids from LDS, K/V rows by 16-byte lane loads -- and folds
 //      its 4 wavefronts' online-softmax states in LDS;
-//   D. the workgroup whose arrival is the P-th merges the P partials
-//      (log-sum-exp) into the output.
+//   D. every workgroup publishes its partial (m, l, acc[D]); workgroup 0 of the
+//      head gathers the P partials and merges them (log-sum-exp) into the
+//      output.
 // With P == 1 a workgroup owns its head and nothing crosses workgroups.
 //
 // Cross-workgroup exchange without cache maintenance: on gfx950 an agent-scope
@@ -23,8 +24,7 @@
 // entry; the merging workgroup publishes it as the new epoch when done), so a
 // reader accepts a word only once it belongs to the current launch and needs no
 // separate ordering; every wait is bounded (on time-out a sticky status bit is
-// set and the kernel still completes).  The arrival counter is never reset:
-// after the launch with tag t it holds t * P.
+// set and the kernel still completes).
 // The workspace must be zero before the first launch.
 #include "csa_device.hpp"
 
@@ -59,7 +59,6 @@ struct StepParams {
   int32_t* idx_out;
   uint32_t* status;
   uint32_t* epoch;     // [BH]
-  uint32_t* arrive;    // [BH]
   uint64_t* keys;      // [BH][C] tagged keys
   uint64_t* part;      // [BH][P][D + 2] tagged partials (m, l, acc[D])
   int64_t S;
@@ -114,7 +113,6 @@ __global__ __launch_bounds__(kStepThreads) void csa_step_kernel(StepParams a) {
   uint32_t* lcount = reinterpret_cast<uint32_t*>(sel + a.topk);
   float* comb = reinterpret_cast<float*>(lcount + 1);
   uint32_t* keys_l = reinterpret_cast<uint32_t*>(comb + kStepWaves * (D + 2));
-  __shared__ int s_last;
 
   const int tid = threadIdx.x;
   const int wave = tid / kWave;
@@ -243,17 +241,17 @@ __global__ __launch_bounds__(kStepThreads) void csa_step_kernel(StepParams a) {
     return;
   }
 
-  // ---- D: publish the partial; the P-th arrival merges --------------------
+  // ---- D: publish the partial; workgroup 0 of the head merges -------------
+  // Workgroup 0 gathers the P tagged partials directly, each word re-read
+  // until it carries this launch's tag: no arrival counter, so no atomic round
+  // trip between the last partial and the merge.
   uint64_t* pp = a.part + (h * P + p) * static_cast<int64_t>(D + 2);
   if (d < D) put_tagged(pp + 2 + d, tag, __float_as_uint(A));
   if (tid == 0) {
     put_tagged(pp, tag, __float_as_uint(M));
     put_tagged(pp + 1, tag, __float_as_uint(Lsum));
-    const uint32_t old = __hip_atomic_fetch_add(&a.arrive[h], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = (old + 1u == tag * static_cast<uint32_t>(P));
   }
-  __syncthreads();
-  if (!s_last) return;
+  if (p != 0) return;
   // Gather all P partials ((m, l, acc[D]) each) into LDS in one batch of loads
   // spread over the 256 threads, then merge from LDS.
   const uint64_t* ph = a.part + h * P * static_cast<int64_t>(D + 2);
@@ -281,7 +279,7 @@ __global__ __launch_bounds__(kStepThreads) void csa_step_kernel(StepParams a) {
     const float lj = lane < P ? pb[lane * (D + 2) + 1] : 0.f;
     float mx = lj > 0.f ? mj : -INFINITY;
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, xor_lanes(mx, off));
     const float w = (lj > 0.f && mx != -INFINITY) ? fast_exp2(mj - mx) : 0.f;
     if (lane < P) wts[lane] = w;
     const float Lt = wave_sum(w * lj);
@@ -314,14 +312,13 @@ int device_cu_count() {
 size_t align256(size_t n) { return (n + 255) & ~size_t{255}; }
 
 struct StepLayout {
-  size_t epoch, arrive, keys, part, total;
+  size_t epoch, keys, part, total;
 };
 
 StepLayout step_layout(int64_t bh, int64_t C, int64_t D, int64_t k, int64_t chunk) {
   StepLayout L;
   L.epoch = 256;
-  L.arrive = L.epoch + align256(static_cast<size_t>(bh) * 4);
-  L.keys = L.arrive + align256(static_cast<size_t>(bh) * 4);
+  L.keys = L.epoch + align256(static_cast<size_t>(bh) * 4);
   L.part = L.keys + align256(static_cast<size_t>(bh * C) * 8);
   const size_t fused = static_cast<size_t>(bh * kStepMaxP * (D + 2)) * 8;
   const int64_t tile = csahca_csa_auto_tile_size(1, bh, k, chunk);
@@ -417,7 +414,6 @@ extern "C" int csahca_csa_decode_step(const void* q, const void* k_cache, const 
     pr.idx_out = out_indices;
     pr.status = reinterpret_cast<uint32_t*>(ws);
     pr.epoch = reinterpret_cast<uint32_t*>(ws + lay.epoch);
-    pr.arrive = reinterpret_cast<uint32_t*>(ws + lay.arrive);
     pr.keys = reinterpret_cast<uint64_t*>(ws + lay.keys);
     pr.part = reinterpret_cast<uint64_t*>(ws + lay.part);
     pr.S = seq_len;

@@ -602,7 +602,7 @@ __global__ __launch_bounds__(kMergeThreads) void dsv4_merge_kernel(const float* 
       if (v.y > 0.f) mx = fmaxf(mx, v.x);
     }
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, xor_lanes(mx, off));
     mx = fmaxf(mx, sk);
     float L = 0.f;
     if (mx != -INFINITY) {

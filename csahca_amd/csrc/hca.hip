@@ -74,7 +74,7 @@ __device__ __forceinline__ float block_reduce(float v, float* red, bool is_max) 
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
-    const float o = __shfl_xor(v, off, kWave);
+    const float o = xor_lanes(v, off);
     v = is_max ? fmaxf(v, o) : v + o;
   }
   __syncthreads();

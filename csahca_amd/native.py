@@ -249,7 +249,7 @@ _STEP_WS: dict = {}
 
 def _step_workspace(nbytes: int, device, signature: tuple) -> torch.Tensor:
     """Step workspace kept per (device, stream).  The fused step keeps per-head
-    launch epochs and arrival counters in it, laid out by the problem shape, so
+    launch epochs and tagged exchange words in it, laid out by the problem shape, so
     it is zero-filled (a fill kernel) whenever it is created or the shape changes."""
     key = (device.index, _stream())
     ent = _STEP_WS.get(key)
