@@ -328,13 +328,10 @@ StepLayout step_layout(int64_t bh, int64_t C, int64_t D, int64_t k, int64_t chun
   return L;
 }
 
+// CSAHCA_STEP_WGS_PER_HEAD=n (> 0) overrides the workgroups per head (read per call).
 int64_t env_wgs_per_head() {
-  static int64_t v = -1;
-  if (v < 0) {
-    const char* s = std::getenv("CSAHCA_STEP_WGS_PER_HEAD");
-    v = s ? std::max<int64_t>(0, std::atoll(s)) : 0;
-  }
-  return v;
+  const char* s = std::getenv("CSAHCA_STEP_WGS_PER_HEAD");
+  return s ? std::max<int64_t>(0, std::atoll(s)) : 0;
 }
 
 }  // namespace
