@@ -326,6 +326,7 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kMfmaHeads = 16;
 constexpr int kMfmaSlots = 32;
+constexpr int kVtStride = kMfmaSlots + 8;  // V^T row stride in bf16 (80 B: rows spread over LDS banks)
 constexpr int kMfmaWaves = 4;
 constexpr int kMfmaThreads = kMfmaWaves * kWave;
 constexpr int kKStepsPerWave = kDim / 32 / kMfmaWaves;  // 4 k-steps of 32 dims
@@ -361,6 +362,29 @@ __device__ __forceinline__ uint4 dequant8_bf16(uint2 w, uint32_t sbyte) {
   return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
+// One unconditional global load from an address the compiler cannot see
+// through (an empty asm launders it): selects of addresses stay selects, and
+// no load ends up under a branch, where the wait-count pass would serialise
+// the loads in flight at the join.
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+template <typename V>
+__device__ __forceinline__ V load_global_raw(const void* p) {
+  uint64_t a = reinterpret_cast<uint64_t>(p);
+  asm volatile("" : "+v"(a));
+  return *reinterpret_cast<const __attribute__((address_space(1))) V*>(a);
+}
+__device__ __forceinline__ int32_t load_global_i32(const void* p) { return load_global_raw<int32_t>(p); }
+__device__ __forceinline__ uint2 load_global_u2(const void* p) {
+  const u32x2_t v = load_global_raw<u32x2_t>(p);
+  return make_uint2(v[0], v[1]);
+}
+__device__ __forceinline__ uint4 load_global_u4(const void* p) {
+  const u32x4_t v = load_global_raw<u32x4_t>(p);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
 struct MfmaArgs {
   int splits;           // slot-list splits per (query, head group)
   int tiles_per_split;  // 32-slot tiles per split
@@ -369,12 +393,12 @@ struct MfmaArgs {
 
 __global__ __launch_bounds__(kMfmaThreads) void dsv4_mfma_kernel(const bf16* __restrict__ q, Dsv4Args a,
                                                                  MfmaArgs m) {
-  __shared__ __align__(16) uint16_t vt[kDim * kMfmaSlots];               // [dim][slot] bf16 bits
+  __shared__ __align__(16) uint16_t vt[kDim * kVtStride];                // [dim][slot] bf16 bits
   __shared__ __align__(16) float sp[kMfmaWaves][kMfmaHeads][kMfmaSlots];  // per-wave score partials
   __shared__ float xch[kMfmaWaves][kMfmaHeads];                           // per-wave head exchange
 
   const int tid = threadIdx.x;
-  const int wave = tid / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // uniform: branches on it stay scalar
   const int lane = tid % kWave;
   const int grp = lane / 16;  // lane group (MFMA k / row block)
   const int l16 = lane % 16;
@@ -408,51 +432,62 @@ __global__ __launch_bounds__(kMfmaThreads) void dsv4_mfma_kernel(const bf16* __r
 #pragma unroll
   for (int j = 0; j < kOutTiles; ++j) o[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  // Token location of slot l16 + 16 nt of tile t, or -1 when skipped.
+  // A skipped slot reads this workgroup's own q row instead (always in bounds,
+  // 1 KiB >= one 584-byte latent row + scales) and its bytes are zeroed after
+  // the load, so every load is unconditional (see slot_loc).
+  const uint8_t* dummy = reinterpret_cast<const uint8_t*>(q + (query * a.heads + h0) * kDim);
+  // Token location of slot l16 + 16 nt of tile t, or -1 when skipped.  The
+  // index loads are unconditional (clamped positions, results selected after
+  // the load): loads under per-lane branches make the compiler wait for every
+  // outstanding load at the join, which would serialise the prefetch below.
   auto slot_loc = [&](int t, int nt) -> int32_t {
     const int s = t * kMfmaSlots + l16 + 16 * nt;
-    if (t >= t1 || s >= total) return -1;
-    if (s < a.topk_slots) return s < n_swa ? a.idx[query * a.topk_slots + s] : -1;
-    const int j = s - a.topk_slots;
-    return j < n_extra ? a.eidx[query * a.extra_slots + j] : -1;
+    const int32_t* ip = a.topk_slots > 0 ? a.idx + query * a.topk_slots + min(s, a.topk_slots - 1)
+                                         : reinterpret_cast<const int32_t*>(dummy);
+    const int32_t* ep = a.extra_slots > 0
+                            ? a.eidx + query * a.extra_slots + min(max(s - a.topk_slots, 0), a.extra_slots - 1)
+                            : reinterpret_cast<const int32_t*>(dummy);
+    const int32_t li = load_global_i32(ip);
+    const int32_t le = load_global_i32(ep);
+    const bool in_swa = s < a.topk_slots;
+    const bool valid = t < t1 && s < total && (in_swa ? s < n_swa : s - a.topk_slots < n_extra);
+    return valid ? (in_swa ? li : le) : -1;
   };
   // This lane's latent bytes of a tile: for each slot, the wave's 4 k-steps
   // (8 e4m3 bytes in .x/.y, or 16 bytes of bf16 rope) and the scale row.
   struct Rows {
-    uint4 raw[2][kKStepsPerWave];
+    uint4 raw[2][kKStepsPerWave];  // as loaded (a skipped slot's bytes are masked at use)
     uint2 sc8[2];
-    uint32_t valid;
+    uint32_t valid;  // tile-wide slot mask (ballot)
+    uint32_t ok;     // this lane's slots: bit nt
   };
   auto issue_rows = [&](int t, const int32_t* loc, Rows& r) {
     const uint8_t* rp[2];
     const uint8_t* srp[2];
+    bool ok[2];
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
       const int s = t * kMfmaSlots + l16 + 16 * nt;
-      rp[nt] = nullptr;
-      srp[nt] = nullptr;
-      if (loc[nt] >= 0) rp[nt] = row_ptr(s < a.topk_slots ? a.swa : a.extra, loc[nt], &srp[nt]);
+      const uint8_t* sr = nullptr;
+      const uint8_t* rr = loc[nt] >= 0 ? row_ptr(s < a.topk_slots ? a.swa : a.extra, loc[nt], &sr) : nullptr;
+      ok[nt] = rr != nullptr;
+      rp[nt] = ok[nt] ? rr : dummy;
+      srp[nt] = ok[nt] ? sr : dummy;
     }
-    r.valid = static_cast<uint32_t>(__ballot(rp[0] != nullptr) & 0xffffull) |
-              (static_cast<uint32_t>(__ballot(rp[1] != nullptr) & 0xffffull) << 16);
+    r.valid = static_cast<uint32_t>(__ballot(ok[0]) & 0xffffull) |
+              (static_cast<uint32_t>(__ballot(ok[1]) & 0xffffull) << 16);
+    r.ok = (ok[0] ? 1u : 0u) | (ok[1] ? 2u : 0u);
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) {
-      r.sc8[nt] = make_uint2(0u, 0u);
+      r.sc8[nt] = load_global_u2(srp[nt]);
 #pragma unroll
-      for (int i = 0; i < kKStepsPerWave; ++i) r.raw[nt][i] = make_uint4(0u, 0u, 0u, 0u);
-      if (rp[nt]) {
-        r.sc8[nt] = *reinterpret_cast<const uint2*>(srp[nt]);
-#pragma unroll
-        for (int i = 0; i < kKStepsPerWave; ++i) {
-          const int kk = wave * kKStepsPerWave + i;
-          const int d0 = 32 * kk + 8 * grp;
-          if (kk < kNopeSteps) {
-            const uint2 w = *reinterpret_cast<const uint2*>(rp[nt] + d0);
-            r.raw[nt][i] = make_uint4(w.x, w.y, 0u, 0u);
-          } else {
-            r.raw[nt][i] = *reinterpret_cast<const uint4*>(rp[nt] + kNope + 2 * (d0 - kNope));
-          }
-        }
+      for (int i = 0; i < kKStepsPerWave; ++i) {
+        const int kk = wave * kKStepsPerWave + i;
+        const int d0 = 32 * kk + 8 * grp;
+        // 16 bytes either way: e4m3 bytes d0.. (the first 8 are used; the rest
+        // stay inside the 576-byte row) or bf16 rope values d0-448..
+        const int off = kk < kNopeSteps ? d0 : kNope + 2 * (d0 - kNope);
+        r.raw[nt][i] = load_global_u4(rp[nt] + off);
       }
     }
   };
@@ -486,11 +521,12 @@ __global__ __launch_bounds__(kMfmaThreads) void dsv4_mfma_kernel(const bf16* __r
           } else {
             kb = cur.raw[nt][i];
           }
+          if (!((cur.ok >> nt) & 1u)) kb = make_uint4(0u, 0u, 0u, 0u);  // skipped slot: zero K and V
           const uint32_t kw[4] = {kb.x, kb.y, kb.z, kb.w};
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            vt[(d0 + 2 * j) * kMfmaSlots + slot] = static_cast<uint16_t>(kw[j] & 0xffffu);
-            vt[(d0 + 2 * j + 1) * kMfmaSlots + slot] = static_cast<uint16_t>(kw[j] >> 16);
+            vt[(d0 + 2 * j) * kVtStride + slot] = static_cast<uint16_t>(kw[j] & 0xffffu);
+            vt[(d0 + 2 * j + 1) * kVtStride + slot] = static_cast<uint16_t>(kw[j] >> 16);
           }
           sacc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[i], __builtin_bit_cast(bf16x8_t, kb), sacc[nt],
                                                              0, 0, 0);
@@ -544,7 +580,7 @@ __global__ __launch_bounds__(kMfmaThreads) void dsv4_mfma_kernel(const bf16* __r
 #pragma unroll
       for (int j = 0; j < kOutTiles; ++j) {
         const int d = wave * (kDim / kMfmaWaves) + 16 * j + l16;
-        const uint4 vb = *reinterpret_cast<const uint4*>(&vt[d * kMfmaSlots + 8 * grp]);
+        const uint4 vb = *reinterpret_cast<const uint4*>(&vt[d * kVtStride + 8 * grp]);
 #pragma unroll
         for (int e = 0; e < 4; ++e) o[j][e] *= ar[e];
         o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, __builtin_bit_cast(bf16x8_t, vb), o[j], 0, 0, 0);
