@@ -57,6 +57,7 @@ def parse_args():
     ap.add_argument("--no-dsv4", action="store_true")
     ap.add_argument("--no-hca", action="store_true")
     ap.add_argument("--no-block", action="store_true")
+    ap.add_argument("--no-large-batch", action="store_true")
     ap.add_argument("--sweep", action="store_true", help="also run the BASELINE config-2 sweep (stderr + json)")
     ap.add_argument("--sweep-out", type=Path, default=None)
     ap.add_argument("--no-graph", action="store_true",
@@ -335,6 +336,43 @@ def dsv4_bench(steps=200, copies=64):
     return out
 
 
+def large_batch_bench(steps=40, copies=2):
+    """The fused step where enough heads are in flight to be bandwidth-bound:
+    BASELINE config-2 point B32 H8 D128 S131072 chunk 64 top-32 (the sweep's
+    largest), two distinct 17 GiB K/V copies alternating (no cache reuse).
+    Reports the step time and HBM roofline on the algorithmic bytes (fp32
+    summaries + selected K/V rows)."""
+    import torch
+
+    from csahca_amd import native
+
+    dev = torch.device("cuda", 0)
+    B, H, D, S, chunk, k = 32, 8, 128, 131072, 64, 32
+    g = torch.Generator(device=dev).manual_seed(0)
+    q = torch.randn(B, H, D, dtype=torch.bfloat16, device=dev, generator=g)
+    ks = [torch.empty(B, H, S, D, dtype=torch.bfloat16, device=dev).normal_(generator=g) for _ in range(copies)]
+    vs = [torch.empty(B, H, S, D, dtype=torch.bfloat16, device=dev).normal_(generator=g) for _ in range(copies)]
+    ss = [native.csa_chunk_summary(kk, chunk) for kk in ks]
+    for i in range(4):
+        native.csa_decode_step(q, ks[i % copies], vs[i % copies], ss[i % copies], chunk, k)
+    with native.profile_launches() as prof:
+        for i in range(steps):
+            native.csa_decode_step(q, ks[i % copies], vs[i % copies], ss[i % copies], chunk, k)
+    us = prof.results["csa_step_kernel"]["avg_us"]
+    nbytes = B * H * (S // chunk) * D * 4 + B * H * k * chunk * D * 2 * 2 + B * H * D * 2 * 2 + B * H * k * 4
+    gbps = nbytes / (us * 1e-6) / 1e9
+    out = {"config": f"csa_decode_step B{B} H{H} D{D} S{S} chunk{chunk} top_k{k} bf16, {copies} alternating "
+                     f"cache copies", "avg_launch_us": round(us, 3), "tokens_per_s": round(B / (us * 1e-6), 1),
+           "roofline": {"bound": "hbm", "kernel": "csa_step_kernel", "bytes_per_launch": nbytes,
+                        "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                        "frac": round(gbps / PEAK_HBM_GBPS, 4)}}
+    log(f"large batch: {out}")
+    del ks, vs, ss, q
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return out
+
+
 def hca_bench(steps=256, copies=4, hca_chunk=256):
     """HCA and the CSA/HCA hybrid at the headline shape (B1 H8 S32768 D128 bf16,
     hca_chunk 256 as in the reference benchmark, CSA chunk 64 top-8 from cached
@@ -572,6 +610,8 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": traffic,
                      "bytes_per_launch": dom_bytes, "avg_launch_us": round(dom_us, 3)},
     }
+    if not args.no_large_batch:
+        line["large_batch"] = large_batch_bench()
     if not args.no_hca:
         line["hca"] = hca_bench()
     if not args.no_block:
