@@ -341,6 +341,20 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ uint32_t bf16x2_bits(bf16x2_t v) { return __builtin_bit_cast(uint32_t, v); }
 
+__device__ __forceinline__ uint4 dequant8_bf16_hw(uint2 w, uint32_t sbyte) {
+  const float s = ue8m0_to_f32(sbyte);
+  return make_uint4(bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w.x, s, false)),
+                    bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w.x, s, true)),
+                    bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w.y, s, false)),
+                    bf16x2_bits(__builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w.y, s, true)));
+}
+
+// True when one of the 7 scale bytes of a token (bytes 0..6 of w) is 255.
+__device__ __forceinline__ bool has_scale_255(uint2 w) {
+  const uint32_t a = ~w.x, b = ~(w.y | 0xff000000u);  // bytes equal to 255 become 0
+  return (((a - 0x01010101u) & ~a) | ((b - 0x01010101u) & ~b)) & 0x80808080u;
+}
+
 __device__ __forceinline__ uint4 dequant8_bf16(uint2 w, uint32_t sbyte) {
   if (sbyte != 255u) {
     const float s = ue8m0_to_f32(sbyte);
@@ -504,6 +518,11 @@ __global__ __launch_bounds__(kMfmaThreads) void dsv4_mfma_kernel(const bf16* __r
     const uint32_t valid = cur.valid;  // same mask in every wavefront: workgroup-uniform
     if (valid != 0u) {
       // Dequantise, store V^T, and accumulate this wave's share of QK^T.
+      // Scale byte 255 (fp32 scale 2^128) needs the software decode: decided
+      // once per tile for the whole wavefront, so the common path has no
+      // per-lane branch.
+      const bool any255 =
+          __ballot(((cur.ok & 1u) && has_scale_255(cur.sc8[0])) || ((cur.ok & 2u) && has_scale_255(cur.sc8[1]))) != 0ull;
       f32x4_t sacc[2];
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
@@ -517,17 +536,28 @@ __global__ __launch_bounds__(kMfmaThreads) void dsv4_mfma_kernel(const bf16* __r
           if (kk < kNopeSteps) {
             const int blk = kk / 2;
             const uint32_t sbyte = (blk < 4 ? cur.sc8[nt].x >> (8 * blk) : cur.sc8[nt].y >> (8 * (blk - 4))) & 0xffu;
-            kb = dequant8_bf16(make_uint2(cur.raw[nt][i].x, cur.raw[nt][i].y), sbyte);
+            const uint2 bytes = make_uint2(cur.raw[nt][i].x, cur.raw[nt][i].y);
+            kb = any255 ? dequant8_bf16(bytes, sbyte) : dequant8_bf16_hw(bytes, sbyte);
           } else {
             kb = cur.raw[nt][i];
           }
           if (!((cur.ok >> nt) & 1u)) kb = make_uint4(0u, 0u, 0u, 0u);  // skipped slot: zero K and V
-          const uint32_t kw[4] = {kb.x, kb.y, kb.z, kb.w};
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            vt[(d0 + 2 * j) * kVtStride + slot] = static_cast<uint16_t>(kw[j] & 0xffffu);
-            vt[(d0 + 2 * j + 1) * kVtStride + slot] = static_cast<uint16_t>(kw[j] >> 16);
-          }
+          // V^T store, two slots per 32-bit word: lanes l and l^1 hold slots
+          // s and s^1 of the same 8 dims; the even lane writes dims d0..d0+3
+          // and the odd lane d0+4..d0+7, each as (even slot | odd slot << 16).
+          const bool odd = (lane & 1) != 0;
+          const uint32_t give0 = odd ? kb.x : kb.z, give1 = odd ? kb.y : kb.w;
+          const uint32_t got0 = lane_xor<1>(give0, lane), got1 = lane_xor<1>(give1, lane);
+          const uint32_t m0 = odd ? kb.z : kb.x, m1 = odd ? kb.w : kb.y;  // own dims of the written half
+          const uint32_t e0 = odd ? got0 : m0, e1 = odd ? got1 : m1;      // even slot's words
+          const uint32_t o0 = odd ? m0 : got0, o1 = odd ? m1 : got1;      // odd slot's words
+          const int db = d0 + (odd ? 4 : 0);
+          uint32_t* vrow = reinterpret_cast<uint32_t*>(&vt[db * kVtStride + (slot & ~1)]);
+          constexpr int kRowWords = kVtStride / 2;
+          vrow[0 * kRowWords] = __builtin_amdgcn_perm(o0, e0, 0x05040100u);
+          vrow[1 * kRowWords] = __builtin_amdgcn_perm(o0, e0, 0x07060302u);
+          vrow[2 * kRowWords] = __builtin_amdgcn_perm(o1, e1, 0x05040100u);
+          vrow[3 * kRowWords] = __builtin_amdgcn_perm(o1, e1, 0x07060302u);
           sacc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[i], __builtin_bit_cast(bf16x8_t, kb), sacc[nt],
                                                              0, 0, 0);
         }
