@@ -311,22 +311,32 @@ __global__ __launch_bounds__(64) void dsv4_tile_kernel(const T* __restrict__ q, 
 //     dims [128w, 128w+128)); lane l loads 8 consecutive latent bytes of slot
 //     l%16 (+16) -- exactly the MFMA B layout -- dequantises them in registers
 //     (e4m3 x 2^(b-127), rounded to bf16 as the reference dequant does) and
-//     also stores them transposed ([dim][slot]) into LDS for PV;
+//     also stores them, 16 bytes per lane, into a row-major [slot][dim] V
+//     tile in LDS;
 //   * the 4 partial score blocks meet in LDS; every wavefront computes the
 //     same online-softmax update, whose probabilities already sit in the MFMA
 //     A layout of PV (lane l: head l%16, slots 8(l/16)..+7);
-//   * wave w accumulates O[16 heads][128w .. 128w+127] over the tiles.
+//   * wave w accumulates O[16 heads][128w .. 128w+127] over the tiles; its PV
+//     B operands come out of the row-major V tile already transposed, via the
+//     gfx950 LDS transpose read ds_read_b64_tr_b16.
 // Output: (m, l, acc[512]) partials per (query, head, split), merged with the
 // sink by dsv4_merge_kernel.
 // MFMA lane layout (16x16x32 bf16): A lane l elem j = A[l%16][8(l/16)+j];
 // B lane l elem j = B[8(l/16)+j][l%16]; C lane l elem i = C[4(l/16)+i][l%16].
+// ds_read_b64_tr_b16 (probed on the device): within each 16-lane group, with
+// local lane a passing the address of 4 consecutive 16-bit values E[a][0..3],
+// local lane i receives elem j = E[4j + i/4][i%4].  Passing &V[8g + a/4][n0 +
+// 4(a%4)] in group g therefore hands lane i the values V[8g + j][n0 + i],
+// j = 0..3: half of the PV B operand (the other half starts 4 rows lower).
 // ---------------------------------------------------------------------------
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kMfmaHeads = 16;
 constexpr int kMfmaSlots = 32;
-constexpr int kVtStride = kMfmaSlots + 8;  // V^T row stride in bf16 (80 B: rows spread over LDS banks)
+// Row stride of the LDS V tile in bf16: 1056 B = 264 dwords (8 mod 64 banks),
+// so the 16 lanes of a transpose read touch 16 distinct bank pairs.
+constexpr int kVRowStride = kDim + 16;
 constexpr int kMfmaWaves = 4;
 constexpr int kMfmaThreads = kMfmaWaves * kWave;
 constexpr int kKStepsPerWave = kDim / 32 / kMfmaWaves;  // 4 k-steps of 32 dims
@@ -407,7 +417,7 @@ struct MfmaArgs {
 
 __global__ __launch_bounds__(kMfmaThreads) void dsv4_mfma_kernel(const bf16* __restrict__ q, Dsv4Args a,
                                                                  MfmaArgs m) {
-  __shared__ __align__(16) uint16_t vt[kDim * kVtStride];                // [dim][slot] bf16 bits
+  __shared__ __align__(16) uint16_t vtile[kMfmaSlots * kVRowStride];     // [slot][dim] bf16 bits
   __shared__ __align__(16) float sp[kMfmaWaves][kMfmaHeads][kMfmaSlots];  // per-wave score partials
   __shared__ float xch[kMfmaWaves][kMfmaHeads];                           // per-wave head exchange
 
@@ -542,22 +552,8 @@ __global__ __launch_bounds__(kMfmaThreads) void dsv4_mfma_kernel(const bf16* __r
             kb = cur.raw[nt][i];
           }
           if (!((cur.ok >> nt) & 1u)) kb = make_uint4(0u, 0u, 0u, 0u);  // skipped slot: zero K and V
-          // V^T store, two slots per 32-bit word: lanes l and l^1 hold slots
-          // s and s^1 of the same 8 dims; the even lane writes dims d0..d0+3
-          // and the odd lane d0+4..d0+7, each as (even slot | odd slot << 16).
-          const bool odd = (lane & 1) != 0;
-          const uint32_t give0 = odd ? kb.x : kb.z, give1 = odd ? kb.y : kb.w;
-          const uint32_t got0 = lane_xor<1>(give0, lane), got1 = lane_xor<1>(give1, lane);
-          const uint32_t m0 = odd ? kb.z : kb.x, m1 = odd ? kb.w : kb.y;  // own dims of the written half
-          const uint32_t e0 = odd ? got0 : m0, e1 = odd ? got1 : m1;      // even slot's words
-          const uint32_t o0 = odd ? m0 : got0, o1 = odd ? m1 : got1;      // odd slot's words
-          const int db = d0 + (odd ? 4 : 0);
-          uint32_t* vrow = reinterpret_cast<uint32_t*>(&vt[db * kVtStride + (slot & ~1)]);
-          constexpr int kRowWords = kVtStride / 2;
-          vrow[0 * kRowWords] = __builtin_amdgcn_perm(o0, e0, 0x05040100u);
-          vrow[1 * kRowWords] = __builtin_amdgcn_perm(o0, e0, 0x07060302u);
-          vrow[2 * kRowWords] = __builtin_amdgcn_perm(o1, e1, 0x05040100u);
-          vrow[3 * kRowWords] = __builtin_amdgcn_perm(o1, e1, 0x07060302u);
+          // V row: this lane's 8 dims of its slot, as they are.
+          *reinterpret_cast<uint4*>(&vtile[slot * kVRowStride + d0]) = kb;
           sacc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[i], __builtin_bit_cast(bf16x8_t, kb), sacc[nt],
                                                              0, 0, 0);
         }
@@ -607,15 +603,23 @@ __global__ __launch_bounds__(kMfmaThreads) void dsv4_mfma_kernel(const bf16* __r
 #pragma unroll
       for (int e = 0; e < 4; ++e) ar[e] = xch[wave][4 * grp + e];
       const bf16x8_t pa = __builtin_bit_cast(bf16x8_t, make_uint4(pw[0], pw[1], pw[2], pw[3]));
+      // PV B operand of output block j (dims n0 = 128 wave + 16 j): lane l
+      // needs V[8 grp + 0..7][n0 + l16], read transposed from the row-major
+      // tile (local lane a passes &V[8 grp + a/4 (+4)][n0 + 4 (a%4)]).
+      typedef short i16x4_t __attribute__((ext_vector_type(4)));
+      typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
+      const uint16_t* vsrc = &vtile[(8 * grp + l16 / 4) * kVRowStride + wave * (kDim / kMfmaWaves) + 4 * (l16 % 4)];
 #pragma unroll
       for (int j = 0; j < kOutTiles; ++j) {
-        const int d = wave * (kDim / kMfmaWaves) + 16 * j + l16;
-        const uint4 vb = *reinterpret_cast<const uint4*>(&vt[d * kVtStride + 8 * grp]);
+        const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(vsrc + 16 * j));
+        const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(vsrc + 4 * kVRowStride + 16 * j));
+        const u32x2_t lw = __builtin_bit_cast(u32x2_t, lo), hw = __builtin_bit_cast(u32x2_t, hi);
+        const uint4 vb = make_uint4(lw[0], lw[1], hw[0], hw[1]);
 #pragma unroll
         for (int e = 0; e < 4; ++e) o[j][e] *= ar[e];
         o[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, __builtin_bit_cast(bf16x8_t, vb), o[j], 0, 0, 0);
       }
-      lds_barrier();  // vt / sp are rewritten by the next tile
+      lds_barrier();  // vtile / sp are rewritten by the next tile
     }
     cur = nxt;
     loc_n[0] = loc_nn[0];
@@ -738,13 +742,21 @@ size_t ws_bytes(int64_t nq, int64_t heads, int64_t tiles) {
   return ((ml + 255) & ~size_t{255}) + static_cast<size_t>(nq * heads * tiles * kDim) * sizeof(float);
 }
 
+// Workgroup target of the MFMA split (CSAHCA_DSV4_MFMA_WGS, read per call).
+int64_t mfma_target_wgs() {
+  const char* e = std::getenv("CSAHCA_DSV4_MFMA_WGS");
+  const long v = e ? std::strtol(e, nullptr, 10) : 0;
+  return v > 0 ? v : 256;
+}
+
 // MFMA path split of each query's slot list: enough (query, head group,
 // split) workgroups for ~256 CUs, whole 32-slot tiles per split.
 void mfma_splits(int64_t nq, int64_t heads, int64_t total_slots, int64_t* splits_out, int64_t* tps_out) {
   const int64_t groups = ceil_div(std::max<int64_t>(1, heads), kMfmaHeads);
   const int64_t ntiles = std::max<int64_t>(1, ceil_div(total_slots, kMfmaSlots));
   const int64_t wgs = std::max<int64_t>(1, nq * groups);
-  int64_t splits = wgs < 256 ? std::min(ntiles, ceil_div(256, wgs)) : 1;
+  const int64_t target = mfma_target_wgs();
+  int64_t splits = wgs < target ? std::min(ntiles, ceil_div(target, wgs)) : 1;
   const int64_t tps = ceil_div(ntiles, splits);
   *splits_out = ceil_div(ntiles, tps);
   *tps_out = tps;
