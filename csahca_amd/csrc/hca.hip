@@ -12,11 +12,15 @@
 //   hca_chunk_kernel  one workgroup per (b, h, chunk) streams the chunk's K and
 //                     V rows with 16-byte lane loads (the whole op is one pass
 //                     over K and V: HBM-bound), reduces them to the two rounded
-//                     means, scores the K mean against q and writes
-//                     (score, V mean) to the workspace;
-//   hca_merge_kernel  one workgroup per (b, h): softmax over the C scores,
-//                     probabilities rounded to the storage type, sum of the V
-//                     means, optional blend with a CSA output.
+//                     means, scores the K mean against q and writes the
+//                     score (scores[b,h,c]) and the V mean (means[b,h,c,:])
+//                     to the workspace;
+//   hca_merge_kernel  one workgroup per (b, h, block of 32 output columns):
+//                     softmax over the C scores, probabilities rounded to the
+//                     storage type, sum of its columns of the V means,
+//                     optional blend with a CSA output.  Spreading a head's
+//                     columns over workgroups keeps each one to a single round
+//                     trip of ~C x 128 bytes even at batch 1.
 #include "common.hpp"
 
 #include <algorithm>
@@ -93,7 +97,8 @@ template <typename T, bool kVec>
 __global__ __launch_bounds__(kHcaThreads) void hca_chunk_kernel(const T* __restrict__ q,
                                                               const T* __restrict__ k,
                                                               const T* __restrict__ v,
-                                                              float* __restrict__ part, int64_t S,
+                                                              float* __restrict__ scores,
+                                                              float* __restrict__ means, int64_t S,
                                                               int D, int chunk, int64_t C,
                                                               float scale) {
   constexpr int VEC = kVec ? Vec16<T>::N : 1;
@@ -173,7 +178,7 @@ __global__ __launch_bounds__(kHcaThreads) void hca_chunk_kernel(const T* __restr
   // Column means, rounded to the storage type; the score partial q . kmean.
   const float inv_n = 1.f / static_cast<float>(chunk);
   const T* qp = q + bh * D;
-  float* out = part + item * (static_cast<int64_t>(D) + 1);
+  float* out = means + item * static_cast<int64_t>(D);
   float dot = 0.f;
   for (int d = tid; d < D; d += kHcaThreads) {
     float a = 0.f, b = 0.f;
@@ -184,167 +189,107 @@ __global__ __launch_bounds__(kHcaThreads) void hca_chunk_kernel(const T* __restr
     const float km = round_to<T>(a * inv_n);
     const float vm = round_to<T>(b * inv_n);
     dot = fmaf(to_f32(qp[d]), km, dot);
-    out[1 + d] = vm;
+    out[d] = vm;
   }
   dot = block_reduce(dot, red, false);
-  if (tid == 0) out[0] = dot * scale;
+  if (tid == 0) scores[item] = dot * scale;
 }
 
-// Thread layout of the PV sum: RG = 256/D row groups (1 when D > 256) x D
-// columns; each thread keeps kMergeBatch rows of its column in flight, and the
-// RG partial sums meet in LDS at the end.
-constexpr int kMergeBatch = 64;         // rows per thread in the one-round-trip path
-constexpr int kMergeBatchGeneral = 32;  // rows per thread per batch otherwise
+// Merge thread layout: 32 columns x 8 row groups; a wavefront reads 2 rows of
+// 128 contiguous bytes per load.  When C <= 256 every score and every V-mean
+// value a thread needs is requested before the first wait (one round trip);
+// larger C runs in passes of kHcaProbChunk rows, kMergeRows rows per batch.
+constexpr int kMergeCols = 32;
+constexpr int kMergeRowGroups = kHcaThreads / kMergeCols;  // 8
+constexpr int kMergeRows = 32;                             // rows per thread per batch
+constexpr int kMergeFastRows = kMergeRows * kMergeRowGroups;  // 256
+static_assert(kMergeFastRows <= kHcaThreads, "one score per thread in the one-round-trip path");
 
 template <typename T>
-__global__ __launch_bounds__(kHcaThreads) void hca_merge_kernel(const float* __restrict__ part,
+__global__ __launch_bounds__(kHcaThreads) void hca_merge_kernel(const float* __restrict__ scores,
+                                                              const float* __restrict__ means,
                                                               const T* __restrict__ blend,
                                                               float w_csa, T* __restrict__ out,
-                                                              int64_t C, int D) {
-  constexpr int kCols = 1024 / kHcaThreads;  // columns per thread when D > 256 (D <= 1024)
+                                                              int64_t C, int D, int col_blocks) {
   __shared__ float s_p[kHcaProbChunk];
   __shared__ float s_sum[kHcaThreads];
   __shared__ float red[kHcaThreads / kWave];
   const int tid = threadIdx.x;
-  const int64_t bh = blockIdx.x;
-  const int64_t stride = static_cast<int64_t>(D) + 1;
-  const float* pb = part + bh * C * stride;
-  const int RG = D <= kHcaThreads ? kHcaThreads / D : 1;
-  const int tpc = D <= kHcaThreads ? D : kHcaThreads;  // threads per row group
-  const int rg = tid / tpc;
-  const int c0l = tid - rg * tpc;
+  const int64_t bh = blockIdx.x / col_blocks;
+  const int cb = static_cast<int>(blockIdx.x - bh * col_blocks);
+  const int rg = tid / kMergeCols, cl = tid % kMergeCols;
+  const int d = cb * kMergeCols + cl;
+  const bool has_col = d < D;
+  const float* sb = scores + bh * C;
+  const float* col = means + bh * C * D + (has_col ? d : 0);  // column 0 stands in: loads stay in bounds
 
-  if (D <= kHcaThreads && C <= kHcaProbChunk && C <= static_cast<int64_t>(kMergeBatch) * RG) {
-    // Common shape: every score and every V-mean value this thread needs is
-    // requested before the first wait -- one memory round trip in total.
-    constexpr int kScores = kHcaProbChunk / kHcaThreads;
+  float a = 0.f;
+  if (C <= kMergeFastRows) {
     const int n = static_cast<int>(C);
-    float sc[kScores], x[kMergeBatch];
+    const float sc = tid < n ? sb[tid] : -INFINITY;
+    float x[kMergeRows];
 #pragma unroll
-    for (int j = 0; j < kScores; ++j) {
-      const int c = tid + j * kHcaThreads;
-      sc[j] = c < n ? pb[static_cast<int64_t>(c) * stride] : -INFINITY;
+    for (int i = 0; i < kMergeRows; ++i) {
+      const int r = rg + i * kMergeRowGroups;
+      x[i] = col[static_cast<int64_t>(r < n ? r : 0) * D];
     }
-    const bool mine = rg < RG;
-    const float* col = pb + 1 + (mine ? c0l : 0);
-#pragma unroll
-    for (int i = 0; i < kMergeBatch; ++i) {
-      const int r = rg + i * RG;
-      x[i] = col[static_cast<int64_t>(mine && r < n ? r : 0) * stride];
-    }
-    float m = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < kScores; ++j) m = fmaxf(m, sc[j]);
-    const float M = block_reduce(m, red, true);
-    float l = 0.f;
-    if (M != -INFINITY) {
-#pragma unroll
-      for (int j = 0; j < kScores; ++j)
-        if (tid + j * kHcaThreads < n) l += fast_exp2((sc[j] - M) * kLog2e);
-    }
-    const float Lt = block_reduce(l, red, false);
-    const float iv = Lt > 0.f ? 1.f / Lt : 0.f;
-#pragma unroll
-    for (int j = 0; j < kScores; ++j) {
-      const int c = tid + j * kHcaThreads;
-      // softmax in fp32, then the cast of the probabilities to the V dtype
-      if (c < n) s_p[c] = M != -INFINITY ? round_to<T>(fast_exp2((sc[j] - M) * kLog2e) * iv) : 0.f;
-    }
+    const float M = block_reduce(sc, red, true);
+    const float e = (tid < n && M != -INFINITY) ? fast_exp2((sc - M) * kLog2e) : 0.f;
+    const float L = block_reduce(e, red, false);
+    const float iv = L > 0.f ? 1.f / L : 0.f;
+    // softmax in fp32, then the cast of the probabilities to the V dtype
+    if (tid < n) s_p[tid] = round_to<T>(e * iv);
     __syncthreads();
-    float a = 0.f;
 #pragma unroll
-    for (int i = 0; i < kMergeBatch; ++i) {
-      const int r = rg + i * RG;
-      if (mine && r < n) a = fmaf(s_p[r], x[i], a);
+    for (int i = 0; i < kMergeRows; ++i) {
+      const int r = rg + i * kMergeRowGroups;
+      if (r < n) a = fmaf(s_p[r], x[i], a);
     }
-    s_sum[tid] = a;
-    __syncthreads();
-    if (tid < D) {
-      float o = 0.f;
-      for (int g = 0; g < RG; ++g) o += s_sum[g * D + tid];
-      o = round_to<T>(o);
-      if (blend) {
-        // w*csa + (1-w)*hca with each product and the sum rounded to T
-        const float ab = round_to<T>(w_csa * to_f32(blend[bh * D + tid]));
-        const float bb = round_to<T>((1.f - w_csa) * o);
-        o = ab + bb;
-      }
-      out[bh * D + tid] = from_f32<T>(o);
-    }
-    return;
-  }
-
-  float mx = -INFINITY;
-  for (int64_t c = tid; c < C; c += kHcaThreads) mx = fmaxf(mx, pb[c * stride]);
-  mx = block_reduce(mx, red, true);
-  float L = 0.f;
-  if (mx != -INFINITY)
-    for (int64_t c = tid; c < C; c += kHcaThreads) L += fast_exp2((pb[c * stride] - mx) * kLog2e);
-  L = block_reduce(L, red, false);
-  const float inv = L > 0.f ? 1.f / L : 0.f;
-
-  float acc[kCols];
+  } else {
+    float mx = -INFINITY;
+    for (int64_t c = tid; c < C; c += kHcaThreads) mx = fmaxf(mx, sb[c]);
+    mx = block_reduce(mx, red, true);
+    float L = 0.f;
+    if (mx != -INFINITY)
+      for (int64_t c = tid; c < C; c += kHcaThreads) L += fast_exp2((sb[c] - mx) * kLog2e);
+    L = block_reduce(L, red, false);
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    for (int64_t p0 = 0; p0 < C; p0 += kHcaProbChunk) {
+      const int pn = static_cast<int>(std::min<int64_t>(kHcaProbChunk, C - p0));
+      for (int c = tid; c < pn; c += kHcaThreads)
+        s_p[c] = mx != -INFINITY ? round_to<T>(fast_exp2((sb[p0 + c] - mx) * kLog2e) * inv) : 0.f;
+      __syncthreads();
+      const float* cp = col + p0 * D;
+      for (int r0 = rg; r0 < pn; r0 += kMergeRows * kMergeRowGroups) {
+        float x[kMergeRows];
 #pragma unroll
-  for (int j = 0; j < kCols; ++j) acc[j] = 0.f;
-  for (int64_t p0 = 0; p0 < C; p0 += kHcaProbChunk) {
-    const int pn = static_cast<int>(std::min<int64_t>(kHcaProbChunk, C - p0));
-    for (int c = tid; c < pn; c += kHcaThreads) {
-      const float x = pb[(p0 + c) * stride];
-      // softmax in fp32, then the cast of the probabilities to the V dtype
-      s_p[c] = mx != -INFINITY ? round_to<T>(fast_exp2((x - mx) * kLog2e) * inv) : 0.f;
-    }
-    __syncthreads();
-    if (rg < RG) {
+        for (int i = 0; i < kMergeRows; ++i) {
+          const int r = r0 + i * kMergeRowGroups;
+          x[i] = cp[static_cast<int64_t>(r < pn ? r : r0) * D];
+        }
 #pragma unroll
-      for (int j = 0; j < kCols; ++j) {
-        const int d = c0l + j * tpc;
-        if (d < D) {
-          const float* col = pb + p0 * stride + 1 + d;
-          float a = acc[j];
-          for (int r0 = rg; r0 < pn; r0 += kMergeBatchGeneral * RG) {
-            float x[kMergeBatchGeneral];
-#pragma unroll
-            for (int i = 0; i < kMergeBatchGeneral; ++i) {
-              const int r = r0 + i * RG;
-              x[i] = col[static_cast<int64_t>(r < pn ? r : r0) * stride];
-            }
-#pragma unroll
-            for (int i = 0; i < kMergeBatchGeneral; ++i) {
-              const int r = r0 + i * RG;
-              if (r < pn) a = fmaf(s_p[r], x[i], a);
-            }
-          }
-          acc[j] = a;
+        for (int i = 0; i < kMergeRows; ++i) {
+          const int r = r0 + i * kMergeRowGroups;
+          if (r < pn) a = fmaf(s_p[r], x[i], a);
         }
       }
-    }
-    __syncthreads();
-  }
-  // Sum the row groups (RG > 1 only when D <= 128: one column per thread).
-  if (RG > 1) {
-    s_sum[tid] = acc[0];
-    __syncthreads();
-    if (tid < D) {
-      float a = 0.f;
-      for (int g = 0; g < RG; ++g) a += s_sum[g * D + tid];
-      acc[0] = a;
+      __syncthreads();
     }
   }
-  if (rg == 0) {
+  s_sum[tid] = a;
+  __syncthreads();
+  if (rg == 0 && has_col) {
+    float o = 0.f;
 #pragma unroll
-    for (int j = 0; j < kCols; ++j) {
-      const int d = c0l + j * tpc;
-      if (d < D) {
-        float o = round_to<T>(acc[j]);
-        if (blend) {
-          // w*csa + (1-w)*hca with each product and the sum rounded to T
-          const float a = round_to<T>(w_csa * to_f32(blend[bh * D + d]));
-          const float b = round_to<T>((1.f - w_csa) * o);
-          o = a + b;
-        }
-        out[bh * D + d] = from_f32<T>(o);
-      }
+    for (int g = 0; g < kMergeRowGroups; ++g) o += s_sum[g * kMergeCols + cl];
+    o = round_to<T>(o);
+    if (blend) {
+      // w*csa + (1-w)*hca with each product and the sum rounded to T
+      const float ab = round_to<T>(w_csa * to_f32(blend[bh * D + d]));
+      const float bb = round_to<T>((1.f - w_csa) * o);
+      o = ab + bb;
     }
+    out[bh * D + d] = from_f32<T>(o);
   }
 }
 
@@ -353,11 +298,18 @@ __global__ __launch_bounds__(kHcaThreads) void hca_merge_kernel(const float* __r
 
 using namespace csahca;
 
+namespace {
+// Workspace: scores f32[B*H*C], then (256-byte aligned) means f32[B*H*C*D].
+size_t hca_means_offset(int64_t n_scores) {
+  return (static_cast<size_t>(n_scores) * sizeof(float) + 255) & ~size_t{255};
+}
+}  // namespace
+
 extern "C" size_t csahca_hca_decode_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len,
                                                    int64_t head_dim, int64_t chunk_size) {
   if (batch < 0 || heads < 0 || seq_len < 0 || head_dim < 0 || chunk_size <= 0) return 0;
   const int64_t C = seq_len / chunk_size;
-  return static_cast<size_t>(batch * heads * C * (head_dim + 1)) * sizeof(float);
+  return hca_means_offset(batch * heads * C) + static_cast<size_t>(batch * heads * C * head_dim) * sizeof(float);
 }
 
 extern "C" int csahca_hca_decode_forward(const void* q, const void* k_cache, const void* v_cache,
@@ -381,7 +333,8 @@ extern "C" int csahca_hca_decode_forward(const void* q, const void* k_cache, con
   if (workspace == nullptr || workspace_bytes < need)
     return fail(CSAHCA_ERR_WORKSPACE, "workspace too small for hca decode");
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
-  float* part = static_cast<float*>(workspace);
+  float* scores = static_cast<float*>(workspace);
+  float* means = reinterpret_cast<float*>(static_cast<char*>(workspace) + hca_means_offset(bh * C));
   const float scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(head_dim)));
   const int D = static_cast<int>(head_dim);
   return dispatch_dtype(dtype, [&](auto tag) -> int {
@@ -398,13 +351,15 @@ extern "C" int csahca_hca_decode_forward(const void* q, const void* k_cache, con
     const T* vp = static_cast<const T*>(v_cache);
     const int rc =
         vec ? launch("hca_chunk_kernel", hca_chunk_kernel<T, true>, grid, dim3(kHcaThreads), lds, stream, qp,
-                     kp, vp, part, seq_len, D, static_cast<int>(chunk_size), C, scale)
+                     kp, vp, scores, means, seq_len, D, static_cast<int>(chunk_size), C, scale)
             : launch("hca_chunk_kernel", hca_chunk_kernel<T, false>, grid, dim3(kHcaThreads), lds, stream, qp,
-                     kp, vp, part, seq_len, D, static_cast<int>(chunk_size), C, scale);
+                     kp, vp, scores, means, seq_len, D, static_cast<int>(chunk_size), C, scale);
     if (rc != CSAHCA_OK) return rc;
-    return launch("hca_merge_kernel", hca_merge_kernel<T>, dim3(static_cast<uint32_t>(bh)),
-                  dim3(kHcaThreads), 0, stream, static_cast<const float*>(part),
-                  static_cast<const T*>(blend_src), static_cast<float>(blend_weight), static_cast<T*>(out), C,
-                  D);
+    const int col_blocks = (D + kMergeCols - 1) / kMergeCols;
+    CSAHCA_REQUIRE(bh * col_blocks <= INT32_MAX, "too many heads in one call");
+    return launch("hca_merge_kernel", hca_merge_kernel<T>, dim3(static_cast<uint32_t>(bh * col_blocks)),
+                  dim3(kHcaThreads), 0, stream, static_cast<const float*>(scores),
+                  static_cast<const float*>(means), static_cast<const T*>(blend_src),
+                  static_cast<float>(blend_weight), static_cast<T*>(out), C, D, col_blocks);
   });
 }

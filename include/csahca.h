@@ -140,7 +140,8 @@ int csahca_csa_step_status(const void* workspace, uint32_t* status_out, void* st
 /* HCA: dense attention over chunk summaries, and the CSA/HCA blend           */
 /* ------------------------------------------------------------------------- */
 
-/* Workspace of csahca_hca_decode_forward: B*H*(S/chunk)*(head_dim+1) floats. */
+/* Workspace of csahca_hca_decode_forward: B*H*(S/chunk) fp32 scores, then
+ * (256-byte aligned) B*H*(S/chunk)*head_dim fp32 V means. */
 size_t csahca_hca_decode_workspace_bytes(int64_t batch, int64_t heads, int64_t seq_len,
                                          int64_t head_dim, int64_t chunk_size);
 
