@@ -646,12 +646,14 @@ __global__ __launch_bounds__(kMfmaThreads) void dsv4_mfma_kernel(const bf16* __r
 
 constexpr int kMergeThreads = kDim / 4;  // 4 output columns per thread
 constexpr int kMergeChunk = 1024;        // tile weights staged in LDS per pass
+constexpr int kMergeFastTiles = 16;      // tiles merged straight from registers
 
 // Merge of the tile partials with the sink as a virtual token of logit
 // sink[h] and value 0 (csrc/dsv4_attention.cu:252-269): M = max(sink, m_t),
 // L = 2^(sink-M) + sum_{l_t>0} l_t 2^(m_t-M), out = sum_t w_t acc_t / L with
-// w_t = 2^(m_t-M) (0 for empty tiles).  The weights are computed in parallel
-// into LDS; the column sums then stream the partial rows without branches.
+// w_t = 2^(m_t-M) (0 for empty tiles).  Up to kMergeFastTiles tiles merge
+// from registers in one round trip; beyond that the weights are computed in
+// parallel into LDS and the column sums stream the partial rows.
 template <typename T>
 __global__ __launch_bounds__(kMergeThreads) void dsv4_merge_kernel(const float* __restrict__ part_ml,
                                                                    const float* __restrict__ part_acc,
@@ -664,6 +666,50 @@ __global__ __launch_bounds__(kMergeThreads) void dsv4_merge_kernel(const float* 
   const int head = static_cast<int>(qh % heads);
   const int tid = threadIdx.x;
   const float2* ml = reinterpret_cast<const float2*>(part_ml) + qh * num_tiles;
+  if (num_tiles <= kMergeFastTiles) {
+    // Few tiles: every (m, l) pair and every partial value this thread needs
+    // is requested before the first wait (clamped tile indices, no branch
+    // around a load), and each thread forms the weights itself -- one memory
+    // round trip and no barrier.
+    const int d = 4 * tid;
+    const float* pa = part_acc + qh * num_tiles * static_cast<int64_t>(kDim) + d;
+    float4 x[kMergeFastTiles];
+    float2 v[kMergeFastTiles];
+#pragma unroll
+    for (int t = 0; t < kMergeFastTiles; ++t) {
+      const int tt = t < num_tiles ? t : 0;
+      x[t] = *reinterpret_cast<const float4*>(pa + static_cast<int64_t>(tt) * kDim);
+      v[t] = ml[tt];
+    }
+    const float sk = sink ? sink[head] * kLog2e : -INFINITY;
+    float mx = sk;
+#pragma unroll
+    for (int t = 0; t < kMergeFastTiles; ++t)
+      if (t < num_tiles && v[t].y > 0.f) mx = fmaxf(mx, v[t].x);
+    float L = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (mx != -INFINITY) {
+#pragma unroll
+      for (int t = 0; t < kMergeFastTiles; ++t) {
+        if (t < num_tiles && v[t].y > 0.f) {
+          const float w = fast_exp2(v[t].x - mx);
+          L = fmaf(v[t].y, w, L);
+          acc.x = fmaf(w, x[t].x, acc.x);
+          acc.y = fmaf(w, x[t].y, acc.y);
+          acc.z = fmaf(w, x[t].z, acc.z);
+          acc.w = fmaf(w, x[t].w, acc.w);
+        }
+      }
+      if (sink) L += fast_exp2(sk - mx);
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    T* o = out + qh * kDim + d;
+    o[0] = from_f32<T>(acc.x * inv);
+    o[1] = from_f32<T>(acc.y * inv);
+    o[2] = from_f32<T>(acc.z * inv);
+    o[3] = from_f32<T>(acc.w * inv);
+    return;
+  }
   if (tid < kWave) {
     const float sk = sink ? sink[head] * kLog2e : -INFINITY;
     float mx = -INFINITY;
