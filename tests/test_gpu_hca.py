@@ -75,6 +75,8 @@ HCA_CASES = [
     (1, 2, 96, 64, 1, torch.bfloat16),       # chunk 1: full attention over every token
     (1, 1, 128, 1024, 64, torch.float64),    # largest head_dim; f64 storage
     (1, 1, 8192, 128, 8192, torch.bfloat16), # one chunk: output = mean of V
+    (1, 2, 32768, 64, 64, torch.bfloat16),   # C = 512: merge rows in batches (C > 256)
+    (1, 1, 16384, 40, 4, torch.float16),     # C = 4096: two probability passes of 2048 rows
 ]
 
 
