@@ -436,7 +436,8 @@ def block_bench(steps=200, warmup=20):
     (tiled op, tile 8) and dynamic selection (fused step from cached summaries,
     and from summaries rebuilt every step as the reference does), eager and as
     one HIP graph per step.  BASELINE block (RMSNorm/QKV/SiLU MLP, growing
-    cache): eager, since shapes change as chunks complete."""
+    cache): eager, and as one HIP graph per step whose replays advance the
+    cache (position and chunk count live on the device)."""
     import torch
 
     from csahca_amd import native
@@ -491,7 +492,7 @@ def block_bench(steps=200, warmup=20):
             log(f"block mini mlp{mlp:g} {mode}: {row}")
             del gr
     for mlp in (2.0, 0.0):
-        hb = HybridDecodeBlock(batch=B, heads=H, head_dim=D, capacity=S + warmup + steps, chunk_size=chunk,
+        hb = HybridDecodeBlock(batch=B, heads=H, head_dim=D, capacity=S + 2 * (warmup + steps) + 1, chunk_size=chunk,
                                top_k=k, mlp_ratio=mlp, device=dev, seed=0)
         hb.prefill(kc, vc)
         hbuf = hidden0.clone()
@@ -502,11 +503,20 @@ def block_bench(steps=200, warmup=20):
         for _ in range(warmup):
             one_h()
         ms = timed(one_h, steps)
-        row = {"ms_per_token_eager": round(ms, 5), "tokens_per_s": round(B / (ms / 1e3), 1),
-               "final_length": hb.length}
+        replay, gout = hb.capture(hbuf)
+
+        def one_g():
+            replay()
+            hbuf.copy_(gout)
+
+        for _ in range(warmup):
+            one_g()
+        ms_graph = timed(one_g, steps)
+        row = {"ms_per_token_eager": round(ms, 5), "ms_per_token_graph": round(ms_graph, 5),
+               "tokens_per_s_graph": round(B / (ms_graph / 1e3), 1), "final_length": hb.length}
         out[f"baseline_block_mlp{mlp:g}_growing_cache"] = row
         log(f"block baseline mlp{mlp:g}: {row}")
-        del hb
+        del hb, replay
     del kc, vc, summ
     torch.cuda.synchronize()
     torch.cuda.empty_cache()

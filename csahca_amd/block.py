@@ -94,11 +94,17 @@ class HybridDecodeBlock:
     """RMSNorm -> QKV -> CSA over a growing cache -> out
     projection -> SiLU MLP, weights N(0, 0.02^2).
 
-    The cache is preallocated with ``capacity`` token slots; ``prefill`` fills
-    the first ``S`` and builds the summaries of its complete chunks.  Each
-    ``step`` appends one token's K/V at position ``length``, extends the
-    summaries when that token completes a chunk, and selects the top-k among
-    the complete chunks only (the open chunk has no summary yet)."""
+    The cache is preallocated with ``capacity`` token slots and the chunk
+    summaries with ``capacity // chunk_size`` rows; ``prefill`` fills the first
+    ``S`` tokens and builds the summaries of their complete chunks.  Each
+    ``step`` appends one token's K/V at the next position, builds the summary of
+    the chunk that token completes (if any), and selects the top-k among the
+    complete chunks only (the open chunk has no summary yet).
+
+    The position and the chunk count live in device memory and every tensor
+    keeps its shape, so a step has no host synchronisation: ``capture`` records
+    one step as a HIP graph whose replays advance the cache token by token.
+    ``length`` mirrors the position on the host (for the capacity check)."""
 
     def __init__(self, *, batch: int, heads: int, head_dim: int, capacity: int, chunk_size: int = 64,
                  top_k: int = 8, mlp_ratio: float = 2.0, dtype=torch.bfloat16, device="cuda", seed: int = 0,
@@ -120,8 +126,19 @@ class HybridDecodeBlock:
         self.norm2 = torch.ones(self.hidden_dim, dtype=dtype, device=device)
         self.k_cache = torch.zeros(batch, heads, capacity, head_dim, dtype=dtype, device=device)
         self.v_cache = torch.zeros_like(self.k_cache)
+        self.summary_buf = torch.zeros(batch, heads, capacity // chunk_size, head_dim, dtype=torch.float32,
+                                       device=device)
+        self.pos = torch.zeros(1, dtype=torch.int64, device=device)       # next token position
+        self.nchunks = torch.zeros(1, dtype=torch.int32, device=device)   # complete chunks
+        self.attn = torch.empty(batch, heads, head_dim, dtype=dtype, device=device)
+        self.indices = torch.empty(batch, heads, min(top_k, capacity // chunk_size), dtype=torch.int32,
+                                   device=device)
         self.length = 0
-        self.summary = torch.empty(batch, heads, 0, head_dim, dtype=torch.float32, device=device)
+
+    @property
+    def summary(self) -> torch.Tensor:
+        """Summaries of the complete chunks (a view of the preallocated rows)."""
+        return self.summary_buf[:, :, : self.length // self.chunk_size]
 
     def prefill(self, k: torch.Tensor, v: torch.Tensor) -> None:
         S = k.shape[2]
@@ -131,37 +148,66 @@ class HybridDecodeBlock:
         self.v_cache[:, :, :S].copy_(v)
         self.length = S
         C = S // self.chunk_size
-        self.summary = torch.empty(self.batch, self.heads, C, self.head_dim, dtype=torch.float32,
-                                   device=self.k_cache.device)
         if C:
-            native.csa_chunk_summary(self.k_cache, self.chunk_size, out=self.summary, chunk_begin=0, num_chunks=C)
+            native.csa_chunk_summary(self.k_cache, self.chunk_size, out=self.summary_buf, chunk_begin=0,
+                                     num_chunks=C)
+        self.pos.fill_(S)
+        self.nchunks.fill_(C)
 
-    def _extend_summary(self) -> None:
-        C = self.length // self.chunk_size
-        if C == self.summary.shape[2]:
-            return
-        grown = torch.empty(self.batch, self.heads, C, self.head_dim, dtype=torch.float32, device=self.summary.device)
-        grown[:, :, : self.summary.shape[2]].copy_(self.summary)
-        native.csa_chunk_summary(self.k_cache, self.chunk_size, out=grown, chunk_begin=C - 1, num_chunks=1)
-        self.summary = grown
-
-    def step(self, hidden: torch.Tensor) -> torch.Tensor:
-        if self.length >= self.capacity:
-            raise RuntimeError("cache capacity exhausted")
+    def _step(self, hidden: torch.Tensor) -> torch.Tensor:
         B, H, D = self.batch, self.heads, self.head_dim
         x = rms_norm(hidden, self.norm1)
         qkv = F.linear(x, self.w_qkv).view(B, 3, H, D)
         q = qkv[:, 0].contiguous()
-        self.k_cache[:, :, self.length].copy_(qkv[:, 1])
-        self.v_cache[:, :, self.length].copy_(qkv[:, 2])
-        self.length += 1
-        self._extend_summary()
-        if self.summary.shape[2] == 0:
-            raise RuntimeError("no complete chunk to attend to")
-        attn, _idx = native.csa_decode_step(q, self.k_cache, self.v_cache, self.summary, self.chunk_size, self.top_k)
-        h = hidden + F.linear(attn.reshape(B, self.hidden_dim), self.w_out)
+        self.k_cache.index_copy_(2, self.pos, qkv[:, 1].unsqueeze(2))
+        self.v_cache.index_copy_(2, self.pos, qkv[:, 2].unsqueeze(2))
+        native.csa_chunk_summary_at(self.k_cache, self.summary_buf, self.chunk_size, self.pos)
+        self.pos.add_(1)
+        self.nchunks.copy_(torch.div(self.pos, self.chunk_size, rounding_mode="floor"))
+        native.csa_decode_step_dev(q, self.k_cache, self.v_cache, self.summary_buf, self.nchunks, self.chunk_size,
+                                   self.top_k, out=self.attn, indices=self.indices)
+        h = hidden + F.linear(self.attn.reshape(B, self.hidden_dim), self.w_out)
         if self.use_mlp:
             h = h + F.linear(F.silu(F.linear(rms_norm(h, self.norm2), self.w_up)), self.w_down)
         return h
 
+    def _advance(self) -> None:
+        if self.length >= self.capacity:
+            raise RuntimeError("cache capacity exhausted")
+        if (self.length + 1) // self.chunk_size == 0:
+            raise RuntimeError("no complete chunk to attend to")
+        self.length += 1
+
+    def step(self, hidden: torch.Tensor) -> torch.Tensor:
+        self._advance()
+        return self._step(hidden)
+
     __call__ = step
+
+    def capture(self, hidden: torch.Tensor):
+        """Record one step on the static input ``hidden`` as a HIP graph.
+
+        Returns ``(replay, out)``: each ``replay()`` runs one step (appending the
+        token of the current ``hidden`` contents) and leaves its result in
+        ``out``.  A warm-up step on the capture stream creates that stream's
+        library state first; its position advance is undone, and the K/V slot
+        it wrote is overwritten by the next step."""
+        s = torch.cuda.Stream(device=hidden.device)
+        s.wait_stream(torch.cuda.current_stream(hidden.device))
+        with torch.cuda.stream(s):
+            self._step(hidden)
+            self.pos.sub_(1)
+            self.nchunks.copy_(torch.div(self.pos, self.chunk_size, rounding_mode="floor"))
+        torch.cuda.current_stream(hidden.device).wait_stream(s)
+        torch.cuda.synchronize(hidden.device)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            out = self._step(hidden)
+
+        def replay():
+            self._advance()
+            graph.replay()
+            return out
+
+        replay.graph = graph
+        return replay, out

@@ -252,19 +252,34 @@ __global__ __launch_bounds__(256) void csa_merge_kernel(const float* __restrict_
 // ---------------------------------------------------------------------------
 // Chunk summaries (chunk_mean, hybrid_attention/reference.py:40-45).
 // ---------------------------------------------------------------------------
+// Chunk a summary workgroup computes: chunk_begin + its index in the request,
+// or, with token_pos set (one workgroup per head), the chunk that the token at
+// *token_pos completes; -1 when that token completes no chunk that both the
+// cache and the summary hold (the workgroup then does nothing).
+__device__ __forceinline__ int64_t summary_chunk(const int64_t* token_pos, int64_t chunk_begin, int64_t nreq,
+                                                 int chunk, int64_t seq_len, int64_t summary_chunks) {
+  if (token_pos == nullptr) return chunk_begin + blockIdx.x % nreq;
+  const int64_t pos = *token_pos;
+  if (pos < 0 || (pos + 1) % chunk != 0) return -1;
+  const int64_t c = pos / chunk;
+  return (c < summary_chunks && (c + 1) * chunk <= seq_len) ? c : -1;
+}
+
 template <typename T, int D>
 __global__ __launch_bounds__(64) void csa_summary_vec_kernel(const T* __restrict__ k,
                                                              float* __restrict__ summary,
                                                              int64_t seq_len, int chunk,
                                                              int64_t summary_chunks,
-                                                             int64_t chunk_begin, int64_t nreq) {
+                                                             int64_t chunk_begin, int64_t nreq,
+                                                             const int64_t* __restrict__ token_pos) {
   using L = AttendLayout<T, D>;
   constexpr int VEC = L::VEC, LPR = L::LPR, RPL = L::RPL;
   const int lane = threadIdx.x;
   const int grp = lane / LPR;
   const int col = lane % LPR;
   const int64_t bh = blockIdx.x / nreq;
-  const int64_t c = chunk_begin + blockIdx.x % nreq;
+  const int64_t c = summary_chunk(token_pos, chunk_begin, nreq, chunk, seq_len, summary_chunks);
+  if (c < 0) return;
   const T* __restrict__ base = k + (bh * seq_len + c * chunk) * D + col * VEC;
   float acc[VEC];
 #pragma unroll
@@ -300,9 +315,10 @@ __global__ __launch_bounds__(64) void csa_summary_vec_kernel(const T* __restrict
 template <typename T>
 __global__ __launch_bounds__(64) void csa_summary_generic_kernel(
     const T* __restrict__ k, float* __restrict__ summary, int64_t seq_len, int D, int chunk,
-    int64_t summary_chunks, int64_t chunk_begin, int64_t nreq) {
+    int64_t summary_chunks, int64_t chunk_begin, int64_t nreq, const int64_t* __restrict__ token_pos) {
   const int64_t bh = blockIdx.x / nreq;
-  const int64_t c = chunk_begin + blockIdx.x % nreq;
+  const int64_t c = summary_chunk(token_pos, chunk_begin, nreq, chunk, seq_len, summary_chunks);
+  if (c < 0) return;
   const T* __restrict__ base = k + (bh * seq_len + c * chunk) * D;
   const float fc = static_cast<float>(chunk);
   for (int d = threadIdx.x; d < D; d += kWave) {
@@ -589,20 +605,14 @@ extern "C" int csahca_csa_decode_forward_tiled(const void* q, const void* k_cach
                          workspace_bytes, stream);
 }
 
-extern "C" int csahca_csa_chunk_summary(const void* k_cache, float* summary, int dtype,
-                                        int64_t batch, int64_t heads, int64_t seq_len,
-                                        int64_t head_dim, int64_t chunk_size,
-                                        int64_t summary_chunks, int64_t chunk_begin,
-                                        int64_t num_chunks, void* stream_ptr) {
-  clear_error();
-  CSAHCA_REQUIRE(valid_dtype(dtype), "k_cache must be float32, float64, float16 or bfloat16");
-  CSAHCA_REQUIRE(batch >= 0 && heads >= 0 && seq_len >= 0 && head_dim >= 0, "negative dimension");
-  CSAHCA_REQUIRE(chunk_size > 0 && chunk_size <= INT_MAX, "chunk_size must be positive");
-  CSAHCA_REQUIRE(chunk_begin >= 0 && num_chunks >= 0, "chunk range must be non-negative");
-  CSAHCA_REQUIRE((chunk_begin + num_chunks) * chunk_size <= seq_len,
-                 "requested chunks extend past seq_len (only complete chunks have summaries)");
-  CSAHCA_REQUIRE(summary_chunks >= chunk_begin + num_chunks, "summary has too few chunk rows");
-  CSAHCA_REQUIRE(head_dim <= 1024, "head_dim > 1024 is not supported");
+namespace {
+
+// Launches the summary kernels over num_chunks chunks from chunk_begin, or,
+// with token_pos set (num_chunks = 1), over the chunk *token_pos completes.
+int chunk_summary_launch(const void* k_cache, float* summary, int dtype, int64_t batch, int64_t heads,
+                         int64_t seq_len, int64_t head_dim, int64_t chunk_size, int64_t summary_chunks,
+                         int64_t chunk_begin, int64_t num_chunks, const int64_t* token_pos,
+                         void* stream_ptr) {
   const int64_t bh = batch * heads;
   if (bh == 0 || num_chunks == 0 || head_dim == 0) return CSAHCA_OK;
   CSAHCA_REQUIRE(k_cache && summary, "null tensor pointer");
@@ -620,7 +630,8 @@ extern "C" int csahca_csa_chunk_summary(const void* k_cache, float* summary, int
     return launch("csa_summary_vec_kernel",                                                  \
                   csa_summary_vec_kernel<T, (DD / VEC <= kWave ? DD : VEC)>, grid,           \
                   dim3(kWave), 0, stream, kp, summary, seq_len,                              \
-                  static_cast<int>(chunk_size), summary_chunks, chunk_begin, num_chunks);    \
+                  static_cast<int>(chunk_size), summary_chunks, chunk_begin, num_chunks,     \
+                  token_pos);                                                                \
   }
     CSAHCA_SUM_VEC(64)
     CSAHCA_SUM_VEC(128)
@@ -629,8 +640,49 @@ extern "C" int csahca_csa_chunk_summary(const void* k_cache, float* summary, int
 #undef CSAHCA_SUM_VEC
     return launch("csa_summary_generic_kernel", csa_summary_generic_kernel<T>, grid, dim3(kWave),
                   0, stream, kp, summary, seq_len, static_cast<int>(head_dim),
-                  static_cast<int>(chunk_size), summary_chunks, chunk_begin, num_chunks);
+                  static_cast<int>(chunk_size), summary_chunks, chunk_begin, num_chunks, token_pos);
   });
+}
+
+int check_summary_args(int dtype, int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
+                       int64_t chunk_size) {
+  CSAHCA_REQUIRE(valid_dtype(dtype), "k_cache must be float32, float64, float16 or bfloat16");
+  CSAHCA_REQUIRE(batch >= 0 && heads >= 0 && seq_len >= 0 && head_dim >= 0, "negative dimension");
+  CSAHCA_REQUIRE(chunk_size > 0 && chunk_size <= INT_MAX, "chunk_size must be positive");
+  CSAHCA_REQUIRE(head_dim <= 1024, "head_dim > 1024 is not supported");
+  return CSAHCA_OK;
+}
+
+}  // namespace
+
+extern "C" int csahca_csa_chunk_summary(const void* k_cache, float* summary, int dtype,
+                                        int64_t batch, int64_t heads, int64_t seq_len,
+                                        int64_t head_dim, int64_t chunk_size,
+                                        int64_t summary_chunks, int64_t chunk_begin,
+                                        int64_t num_chunks, void* stream_ptr) {
+  clear_error();
+  const int rc = check_summary_args(dtype, batch, heads, seq_len, head_dim, chunk_size);
+  if (rc != CSAHCA_OK) return rc;
+  CSAHCA_REQUIRE(chunk_begin >= 0 && num_chunks >= 0, "chunk range must be non-negative");
+  CSAHCA_REQUIRE((chunk_begin + num_chunks) * chunk_size <= seq_len,
+                 "requested chunks extend past seq_len (only complete chunks have summaries)");
+  CSAHCA_REQUIRE(summary_chunks >= chunk_begin + num_chunks, "summary has too few chunk rows");
+  return chunk_summary_launch(k_cache, summary, dtype, batch, heads, seq_len, head_dim, chunk_size,
+                              summary_chunks, chunk_begin, num_chunks, nullptr, stream_ptr);
+}
+
+extern "C" int csahca_csa_chunk_summary_at(const void* k_cache, float* summary, int dtype, int64_t batch,
+                                           int64_t heads, int64_t seq_len, int64_t head_dim,
+                                           int64_t chunk_size, int64_t summary_chunks,
+                                           const int64_t* token_pos, void* stream_ptr) {
+  clear_error();
+  const int rc = check_summary_args(dtype, batch, heads, seq_len, head_dim, chunk_size);
+  if (rc != CSAHCA_OK) return rc;
+  CSAHCA_REQUIRE(summary_chunks >= 0, "negative dimension");
+  CSAHCA_REQUIRE(token_pos != nullptr || batch * heads == 0, "null token_pos pointer");
+  if (summary_chunks == 0) return CSAHCA_OK;
+  return chunk_summary_launch(k_cache, summary, dtype, batch, heads, seq_len, head_dim, chunk_size,
+                              summary_chunks, 0, 1, token_pos, stream_ptr);
 }
 
 extern "C" size_t csahca_csa_select_workspace_bytes(int64_t batch, int64_t heads,

@@ -3,10 +3,13 @@
 //   split-KV sparse attention over the selected tokens -> partial merge.
 //
 // Each (b,h) head is served by P workgroups of 4 wavefronts:
-//   A. workgroup p scores chunks [C*p/P, C*(p+1)/P) and publishes their order
-//      keys (fp32 score -> monotone uint32);
+//   A. workgroup p scores summary rows [Cs*p/P, Cs*(p+1)/P) of the head's Cs
+//      rows and publishes the order keys (fp32 score -> monotone uint32) of
+//      those below the chunk count C (C = Cs unless the count is read from
+//      device memory, which lets a captured graph follow a growing cache);
 //   B. every workgroup gathers the head's C keys into LDS and wavefront 0 runs
 //      the top-k (same keys, deterministic algorithm: identical everywhere);
+//      selection slots beyond C hold chunk -1 (skipped);
 //   C. workgroup p attends the selected-token slots [T*p/P, T*(p+1)/P) (T = k *
 //      chunk) -- chunk ids from LDS, K/V rows by 16-byte lane loads -- and folds
 //      its 4 wavefronts' online-softmax states in LDS;
@@ -62,7 +65,9 @@ struct StepParams {
   uint64_t* keys;      // [BH][C] tagged keys
   uint64_t* part;      // [BH][P][D + 2] tagged partials (m, l, acc[D])
   int64_t S;
-  int64_t C;
+  int64_t C;            // chunks in play (when c_dev is null)
+  int64_t Cs;           // summary / key rows per head (C <= Cs)
+  const int32_t* c_dev;  // chunks in play, read on the device (clamped to [0, Cs]); may be null
   int chunk;
   int chunk_shift;
   int topk;
@@ -120,7 +125,10 @@ __global__ __launch_bounds__(kStepThreads) void csa_step_kernel(StepParams a) {
   const int P = a.P;
   const int64_t h = blockIdx.x / P;
   const int p = static_cast<int>(blockIdx.x % P);
-  const int64_t C = a.C;
+  const int64_t Cs = a.Cs;
+  // Chunks in play: the host's count, or the device's (its load overlaps the
+  // summary loads of phase A, which are laid out over the Cs rows).
+  const int64_t C = a.c_dev ? min<int64_t>(max<int32_t>(*a.c_dev, 0), Cs) : a.C;
   const T* __restrict__ q = static_cast<const T*>(a.q) + h * D;
 
   // This launch's tag for the head.  Every thread issues the (same-address)
@@ -135,9 +143,9 @@ __global__ __launch_bounds__(kStepThreads) void csa_step_kernel(StepParams a) {
     float qf4[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) qf4[e] = to_f32(q[col * 4 + e]);
-    const float* __restrict__ sb = a.summary + h * C * D + col * 4;
-    uint64_t* kg = a.keys + h * C;
-    const int64_t c0 = C * p / P, c1 = C * (p + 1) / P;
+    const float* __restrict__ sb = a.summary + h * Cs * D + col * 4;
+    uint64_t* kg = a.keys + h * Cs;
+    const int64_t c0 = Cs * p / P, c1 = Cs * (p + 1) / P;
     constexpr int US = kStepScoreUnroll;
     for (int64_t blk = c0; blk < c1; blk += kStepWaves * SRPL * US) {
       const int64_t base = blk + wave * SRPL * US;
@@ -147,7 +155,7 @@ __global__ __launch_bounds__(kStepThreads) void csa_step_kernel(StepParams a) {
 #pragma unroll
         for (int u = 0; u < US; ++u) {
           const int64_t c = base + grp + SRPL * u;
-          if (c < c1) {
+          if (c < c1 && c < C) {
             const uint32_t key = order_key(sc[u] * a.score_scale);
             if (P > 1)
               put_tagged(kg + c, tag, key);
@@ -161,7 +169,7 @@ __global__ __launch_bounds__(kStepThreads) void csa_step_kernel(StepParams a) {
 
   // ---- B: gather the head's keys, top-k -----------------------------------
   if (P > 1) {
-    const uint64_t* kg = a.keys + h * C;
+    const uint64_t* kg = a.keys + h * Cs;
     for (int64_t i0 = tid; i0 < C; i0 += kStepThreads * B8) {
       uint64_t w[B8];
 #pragma unroll
@@ -184,7 +192,11 @@ __global__ __launch_bounds__(kStepThreads) void csa_step_kernel(StepParams a) {
       sel[r] = i;
       if (write_ids) io[r] = i;
     };
-    wave_topk<TOPK_M>(keys_l, static_cast<int>(C), a.topk, scratch, hist, skey, sidx, lcount, emit);
+    // Fewer chunks in play than selection slots (device count only): the
+    // slots past the count hold -1, which the attention below skips.
+    const int kk = static_cast<int>(min<int64_t>(a.topk, C));
+    if (kk > 0) wave_topk<TOPK_M>(keys_l, static_cast<int>(C), kk, scratch, hist, skey, sidx, lcount, emit);
+    for (int r = kk + lane; r < a.topk; r += kWave) emit(r, -1);
   }
   __syncthreads();
 
@@ -347,13 +359,14 @@ extern "C" size_t csahca_csa_step_workspace_bytes(int64_t batch, int64_t heads, 
   return step_layout(batch * heads, num_chunks, head_dim, k, chunk_size).total;
 }
 
-extern "C" int csahca_csa_decode_step(const void* q, const void* k_cache, const void* v_cache,
-                                      const float* summary, void* out, int32_t* out_indices,
-                                      int dtype, int64_t batch, int64_t heads, int64_t seq_len,
-                                      int64_t head_dim, int64_t num_chunks, int64_t chunk_size,
-                                      int64_t top_k, void* workspace, size_t workspace_bytes,
-                                      void* stream_ptr) {
-  clear_error();
+namespace {
+
+// One decode step over num_chunks summary rows per head; with c_dev set the
+// chunks in play are *c_dev (clamped to [0, num_chunks]), read on the device.
+int decode_step_impl(const void* q, const void* k_cache, const void* v_cache, const float* summary, void* out,
+                     int32_t* out_indices, int dtype, int64_t batch, int64_t heads, int64_t seq_len,
+                     int64_t head_dim, int64_t num_chunks, const int32_t* c_dev, int64_t chunk_size,
+                     int64_t top_k, void* workspace, size_t workspace_bytes, void* stream_ptr) {
   CSAHCA_REQUIRE(valid_dtype(dtype), "q, k_cache and v_cache must be float32, float64, float16 or bfloat16");
   CSAHCA_REQUIRE(batch >= 0 && heads >= 0 && seq_len >= 0 && head_dim >= 0 && num_chunks >= 0,
                  "negative dimension");
@@ -415,6 +428,8 @@ extern "C" int csahca_csa_decode_step(const void* q, const void* k_cache, const 
     pr.part = reinterpret_cast<uint64_t*>(ws + lay.part);
     pr.S = seq_len;
     pr.C = num_chunks;
+    pr.Cs = num_chunks;
+    pr.c_dev = c_dev;
     pr.chunk = static_cast<int>(chunk_size);
     int shift = -1;
     if ((chunk_size & (chunk_size - 1)) == 0) {
@@ -447,6 +462,10 @@ extern "C" int csahca_csa_decode_step(const void* q, const void* k_cache, const 
       }
     });
   }
+  if (c_dev != nullptr)
+    return fail(CSAHCA_ERR_ARGUMENT,
+                "a device chunk count needs the fused step (float32/float16/bfloat16, head_dim 64/128/256, "
+                "16-byte aligned tensors, top_k <= 1024)");
   // General path: score + top-k kernels, then the split-KV decode.
   uint32_t* keys = reinterpret_cast<uint32_t*>(ws + lay.keys);
   if (k > 0) {
@@ -457,6 +476,31 @@ extern "C" int csahca_csa_decode_step(const void* q, const void* k_cache, const 
   return csahca_csa_decode_forward_tiled(q, k_cache, v_cache, out_indices, out, dtype, CSAHCA_I32, batch,
                                          heads, seq_len, head_dim, k, chunk_size, tile, ws + lay.part,
                                          lay.total - lay.part, stream);
+}
+
+}  // namespace
+
+extern "C" int csahca_csa_decode_step(const void* q, const void* k_cache, const void* v_cache,
+                                      const float* summary, void* out, int32_t* out_indices,
+                                      int dtype, int64_t batch, int64_t heads, int64_t seq_len,
+                                      int64_t head_dim, int64_t num_chunks, int64_t chunk_size,
+                                      int64_t top_k, void* workspace, size_t workspace_bytes,
+                                      void* stream_ptr) {
+  clear_error();
+  return decode_step_impl(q, k_cache, v_cache, summary, out, out_indices, dtype, batch, heads, seq_len, head_dim,
+                          num_chunks, nullptr, chunk_size, top_k, workspace, workspace_bytes, stream_ptr);
+}
+
+extern "C" int csahca_csa_decode_step_dev(const void* q, const void* k_cache, const void* v_cache,
+                                          const float* summary, const int32_t* num_chunks_dev, void* out,
+                                          int32_t* out_indices, int dtype, int64_t batch, int64_t heads,
+                                          int64_t seq_len, int64_t head_dim, int64_t max_chunks,
+                                          int64_t chunk_size, int64_t top_k, void* workspace,
+                                          size_t workspace_bytes, void* stream_ptr) {
+  clear_error();
+  CSAHCA_REQUIRE(num_chunks_dev != nullptr, "null num_chunks pointer");
+  return decode_step_impl(q, k_cache, v_cache, summary, out, out_indices, dtype, batch, heads, seq_len, head_dim,
+                          max_chunks, num_chunks_dev, chunk_size, top_k, workspace, workspace_bytes, stream_ptr);
 }
 
 extern "C" int csahca_csa_step_status(const void* workspace, uint32_t* status_out, void* stream_ptr) {

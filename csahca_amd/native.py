@@ -44,6 +44,7 @@ _SIGNATURES = {
     "csahca_csa_decode_forward": (_int, [_vp] * 5 + [_int, _int] + [_i64] * 6 + [_vp, _sz, _vp]),
     "csahca_csa_decode_forward_tiled": (_int, [_vp] * 5 + [_int, _int] + [_i64] * 7 + [_vp, _sz, _vp]),
     "csahca_csa_chunk_summary": (_int, [_vp, _vp, _int] + [_i64] * 8 + [_vp]),
+    "csahca_csa_chunk_summary_at": (_int, [_vp, _vp, _int] + [_i64] * 6 + [_vp, _vp]),
     "csahca_csa_select_workspace_bytes": (_sz, [_i64] * 3),
     "csahca_csa_select_topk": (_int, [_vp, _vp, _vp, _int] + [_i64] * 5 + [_vp, _sz, _vp]),
     "csahca_dsv4_decode_workspace_bytes": (_sz, [_i64] * 5),
@@ -57,6 +58,7 @@ _SIGNATURES = {
                _i64, _vp, _vp, _dbl, _vp, _vp, _sz, _vp]),
     "csahca_csa_step_workspace_bytes": (_sz, [_i64] * 6),
     "csahca_csa_decode_step": (_int, [_vp] * 6 + [_int] + [_i64] * 7 + [_vp, _sz, _vp]),
+    "csahca_csa_decode_step_dev": (_int, [_vp] * 7 + [_int] + [_i64] * 7 + [_vp, _sz, _vp]),
     "csahca_csa_step_status": (_int, [_vp, ctypes.POINTER(ctypes.c_uint32), _vp]),
     "csahca_hca_decode_workspace_bytes": (_sz, [_i64] * 5),
     "csahca_dsv4_pack_tokens": (_int, [_vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp]),
@@ -220,6 +222,29 @@ def csa_chunk_summary(k_cache, chunk_size, *, out=None, chunk_begin: int = 0, nu
     return out
 
 
+def csa_chunk_summary_at(k_cache, summary, chunk_size, token_pos):
+    """Recompute in place the summary of the chunk that the token at
+    ``token_pos`` (a one-element int64 CUDA tensor, read on the device)
+    completes; nothing happens when that token completes no chunk.  The
+    graph-capturable form of the incremental update: ``summary`` is a
+    preallocated ``[B, H, max_chunks, D]`` fp32 tensor and only ever receives
+    complete chunks."""
+    chunk_size = int(chunk_size)
+    _check(k_cache.is_cuda and summary.is_cuda and token_pos.is_cuda, "tensors must be CUDA tensors")
+    _check(k_cache.is_contiguous() and k_cache.dim() == 4, "k_cache must be a contiguous [batch, heads, seq, head_dim]")
+    _check(k_cache.dtype in _FLOATING, f"unsupported dtype {k_cache.dtype}")
+    _check(chunk_size > 0, "chunk_size must be positive")
+    B, H, S, D = k_cache.shape
+    _check(summary.is_contiguous() and summary.dtype == torch.float32 and summary.dim() == 4
+           and tuple(summary.shape[:2]) == (B, H) and summary.shape[3] == D,
+           "summary must be a contiguous fp32 [batch, heads, chunks, head_dim] CUDA tensor")
+    _check(token_pos.dtype == torch.int64 and token_pos.numel() == 1, "token_pos must be a one-element int64 tensor")
+    with torch.cuda.device(k_cache.device):
+        _rc(lib().csahca_csa_chunk_summary_at(_ptr(k_cache), _ptr(summary), _DTYPES[k_cache.dtype], B, H, S, D,
+                                              chunk_size, summary.shape[2], _ptr(token_pos), _stream()))
+    return summary
+
+
 def csa_select_topk(q, summary, top_k):
     """Top-k chunk ids by q . summary / sqrt(D) (select_topk_chunks scoring,
     hybrid_attention/reference.py:51-56).  int32 ``[B, H, min(top_k, C)]``, best
@@ -292,6 +317,43 @@ def csa_decode_step(q, k_cache, v_cache, summary, chunk_size, top_k, tile_size: 
                                          _DTYPES[q.dtype], B, H, S, D, C, chunk_size, top_k, _ptr(ws), ws.numel(),
                                          _stream()))
     return out, idx
+
+
+def csa_decode_step_dev(q, k_cache, v_cache, summary, num_chunks, chunk_size, top_k, *, out=None, indices=None):
+    """csa_decode_step with the chunk count in device memory: ``summary`` holds
+    ``max_chunks`` rows per head and the step selects among the first
+    ``clamp(num_chunks, 0, max_chunks)`` of them (``num_chunks``: one-element
+    int32 CUDA tensor, read on the device).  Index slots past that count are
+    -1.  No host synchronisation and fixed shapes, so a decode loop over a
+    growing cache can be captured in one HIP graph.  ``out`` / ``indices``
+    may be given to write in place.  Returns ``(out, chunk_indices)``."""
+    chunk_size, top_k = int(chunk_size), int(top_k)
+    _csa_checks(q, k_cache, v_cache, torch.empty((q.shape[0], q.shape[1], 0), dtype=torch.int32, device=q.device),
+                chunk_size, tiled=False)
+    _check(summary.is_cuda and summary.is_contiguous() and summary.dtype == torch.float32 and summary.dim() == 4,
+           "summary must be a contiguous fp32 [batch, heads, chunks, head_dim] CUDA tensor")
+    _check(num_chunks.is_cuda and num_chunks.dtype == torch.int32 and num_chunks.numel() == 1,
+           "num_chunks must be a one-element int32 CUDA tensor")
+    B, H, D = q.shape
+    S = k_cache.shape[2]
+    _check(tuple(summary.shape[:2]) == (B, H) and summary.shape[3] == D, "summary shape must match q")
+    Cs = summary.shape[2]
+    _check(top_k >= 0, "top_k must be non-negative")
+    k = min(top_k, Cs)
+    with torch.cuda.device(q.device):
+        if out is None:
+            out = torch.empty_like(q)
+        if indices is None:
+            indices = torch.empty((B, H, k), dtype=torch.int32, device=q.device)
+        _check(out.shape == q.shape and out.dtype == q.dtype and out.is_contiguous(), "out must match q")
+        _check(tuple(indices.shape) == (B, H, k) and indices.dtype == torch.int32 and indices.is_contiguous(),
+               "indices must be a contiguous int32 [batch, heads, min(top_k, max_chunks)] tensor")
+        ws = _step_workspace(lib().csahca_csa_step_workspace_bytes(B, H, Cs, D, top_k, chunk_size), q.device,
+                             (B * H, Cs, D, k, chunk_size))
+        _rc(lib().csahca_csa_decode_step_dev(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(summary), _ptr(num_chunks),
+                                             _ptr(out), _ptr(indices), _DTYPES[q.dtype], B, H, S, D, Cs, chunk_size,
+                                             top_k, _ptr(ws), ws.numel(), _stream()))
+    return out, indices
 
 
 def csa_step_status(device=None) -> dict:

@@ -101,6 +101,18 @@ int csahca_csa_chunk_summary(const void* k_cache, float* summary, int dtype, int
                              int64_t chunk_size, int64_t summary_chunks, int64_t chunk_begin,
                              int64_t num_chunks, void* stream);
 
+/* The incremental summary update with the token position in device memory (no
+ * reference counterpart; for a decode loop captured in a HIP graph, where the
+ * position advances on the device): if the token at *token_pos (int64)
+ * completes chunk c = *token_pos / chunk_size ((*token_pos + 1) % chunk_size
+ * == 0), summary[b,h,c] is recomputed as csahca_csa_chunk_summary does;
+ * otherwise, or when chunk c lies beyond seq_len or summary_chunks, nothing is
+ * written.  Summary rows thus only ever hold complete chunks. */
+int csahca_csa_chunk_summary_at(const void* k_cache, float* summary, int dtype, int64_t batch,
+                                int64_t heads, int64_t seq_len, int64_t head_dim,
+                                int64_t chunk_size, int64_t summary_chunks,
+                                const int64_t* token_pos, void* stream);
+
 /* Workspace for csahca_csa_select_topk: the fp32 chunk scores. */
 size_t csahca_csa_select_workspace_bytes(int64_t batch, int64_t heads, int64_t num_chunks);
 
@@ -130,6 +142,22 @@ int csahca_csa_decode_step(const void* q, const void* k_cache, const void* v_cac
                            int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
                            int64_t num_chunks, int64_t chunk_size, int64_t top_k,
                            void* workspace, size_t workspace_bytes, void* stream);
+
+/* csahca_csa_decode_step with the chunk count in device memory (no reference
+ * counterpart; for a decode loop captured in a HIP graph over a growing
+ * cache): summary holds max_chunks rows per head, and the step selects among
+ * the first C = clamp(*num_chunks, 0, max_chunks) of them.  out_indices holds
+ * min(top_k, max_chunks) slots per head; slots past C hold -1 and add nothing
+ * to the attention (C = 0 gives a zero output).  Workspace as for
+ * csahca_csa_step_workspace_bytes(batch, heads, max_chunks, ...).  Needs the
+ * single-launch path: float32/float16/bfloat16, head_dim 64/128/256, 16-byte
+ * aligned tensors; other shapes return CSAHCA_ERR_ARGUMENT. */
+int csahca_csa_decode_step_dev(const void* q, const void* k_cache, const void* v_cache,
+                               const float* summary, const int32_t* num_chunks, void* out,
+                               int32_t* out_indices, int dtype, int64_t batch, int64_t heads,
+                               int64_t seq_len, int64_t head_dim, int64_t max_chunks,
+                               int64_t chunk_size, int64_t top_k, void* workspace,
+                               size_t workspace_bytes, void* stream);
 
 /* Reads the step workspace's sticky status word (0 = healthy; bit 0 = a
  * workgroup hand-off timed out, so a result may be wrong) into host memory;

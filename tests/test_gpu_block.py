@@ -138,3 +138,94 @@ def test_hybrid_block_steps_match_cpu_across_a_chunk_boundary(mlp_ratio):
     # the summary of the chunk completed during decoding equals a fresh build
     fresh = native.csa_chunk_summary(blk.k_cache[:, :, :256].contiguous(), 64)
     torch.testing.assert_close(blk.summary, fresh, rtol=0, atol=0)
+
+
+# ---------------------------------------------------------------------------
+# Device-side position / chunk count (graph-capturable growing cache)
+# ---------------------------------------------------------------------------
+
+def test_summary_at_writes_only_the_chunk_a_token_completes():
+    _, k, _ = make_static(B=1, H=4, S=512, D=64, seed=11)
+    k = k.to(DEV)
+    fresh = native.csa_chunk_summary(k, 64)
+    summ = torch.full((1, 4, 8, 64), -7.0, device=DEV)
+    pos = torch.zeros(1, dtype=torch.int64, device=DEV)
+    for p in (0, 62, 64, 100, 126):  # completes no chunk
+        pos.fill_(p)
+        native.csa_chunk_summary_at(k, summ, 64, pos)
+    assert torch.all(summ == -7.0)
+    for p, c in ((63, 0), (191, 2), (511, 7)):
+        pos.fill_(p)
+        native.csa_chunk_summary_at(k, summ, 64, pos)
+        torch.testing.assert_close(summ[:, :, c], fresh[:, :, c], rtol=0, atol=0)
+    untouched = [c for c in range(8) if c not in (0, 2, 7)]
+    assert torch.all(summ[:, :, untouched] == -7.0)
+    pos.fill_(575)  # chunk 8: past both the summary rows and the cache
+    native.csa_chunk_summary_at(k, summ, 64, pos)
+    pos.fill_(-1)
+    native.csa_chunk_summary_at(k, summ, 64, pos)
+    assert torch.all(summ[:, :, untouched] == -7.0)
+
+
+def test_decode_step_dev_matches_the_host_count_step():
+    _, k, v = make_static(B=2, H=4, S=4096, D=128, seed=12)
+    q = torch.randn(2, 4, 128, generator=torch.Generator().manual_seed(13)).to(BF).to(DEV)
+    k, v = k.to(DEV), v.to(DEV)
+    summ = native.csa_chunk_summary(k, 64)  # 64 chunks
+    n = torch.tensor([64], dtype=torch.int32, device=DEV)
+    want, want_idx = native.csa_decode_step(q, k, v, summ, 64, 8)
+    got, got_idx = native.csa_decode_step_dev(q, k, v, summ, n, 64, 8)
+    assert torch.equal(got_idx, want_idx) and torch.equal(got, want)
+    # fewer chunks in play than summary rows: the first 40 only
+    n.fill_(40)
+    part, part_idx = native.csa_decode_step(q, k, v, summ[:, :, :40].contiguous(), 64, 8)
+    got, got_idx = native.csa_decode_step_dev(q, k, v, summ, n, 64, 8)
+    assert torch.equal(got_idx, part_idx)
+    assert_close(got, part, atol=1e-3, rtol=1e-3, what="40 of 64 chunks")
+
+
+def test_decode_step_dev_with_fewer_chunks_than_top_k():
+    _, k, v = make_static(B=1, H=4, S=1024, D=64, seed=14)
+    q = torch.randn(1, 4, 64, generator=torch.Generator().manual_seed(15)).to(BF)
+    kd, vd, qd = k.to(DEV), v.to(DEV), q.to(DEV)
+    summ = native.csa_chunk_summary(kd, 64)  # 16 rows
+    n = torch.tensor([3], dtype=torch.int32, device=DEV)
+    got, idx = native.csa_decode_step_dev(qd, kd, vd, summ, n, 64, 8)
+    want_idx, _ = oracle.select_topk(q, oracle.chunk_mean(k[:, :, :192].contiguous(), 64), 8)
+    assert idx.shape == (1, 4, 8)
+    assert np.array_equal(idx[:, :, :3].cpu().numpy(), want_idx) and torch.all(idx[:, :, 3:] == -1)
+    assert_close(got, cpu_csa(q, k, v, want_idx, 64), what="3 chunks")
+    n.fill_(0)
+    got, idx = native.csa_decode_step_dev(qd, kd, vd, summ, n, 64, 8)
+    assert torch.all(idx == -1) and torch.all(got == 0)
+    n.fill_(1000)  # clamped to the 16 summary rows
+    got, idx = native.csa_decode_step_dev(qd, kd, vd, summ, n, 64, 8)
+    full, full_idx = native.csa_decode_step(qd, kd, vd, summ, 64, 8)
+    assert torch.equal(idx, full_idx) and torch.equal(got, full)
+
+
+@pytest.mark.parametrize("mlp_ratio", [0.0, 2.0])
+def test_hybrid_block_graph_replays_match_eager_steps(mlp_ratio):
+    B, H, D, S0, steps = 1, 4, 64, 1000, 100  # tokens 1024 and 1088 complete chunks 15 and 16
+    blocks = [HybridDecodeBlock(batch=B, heads=H, head_dim=D, capacity=1200, chunk_size=64, top_k=4,
+                                mlp_ratio=mlp_ratio, device=DEV, seed=21) for _ in range(2)]
+    g = torch.Generator().manual_seed(22)
+    k0 = torch.randn(B, H, S0, D, generator=g).to(BF).to(DEV)
+    v0 = torch.randn(B, H, S0, D, generator=g).to(BF).to(DEV)
+    hiddens = [torch.randn(B, H * D, generator=g).to(BF).to(DEV) for _ in range(steps)]
+    for blk in blocks:
+        blk.prefill(k0, v0)
+    eager, graphed = blocks
+    hbuf = torch.empty(B, H * D, dtype=BF, device=DEV)
+    hbuf.copy_(hiddens[0])
+    replay, out = graphed.capture(hbuf)
+    for i in range(steps):
+        want = eager(hiddens[i])
+        hbuf.copy_(hiddens[i])
+        got = replay()
+        assert torch.equal(got, want), f"step {i}"
+    assert eager.length == graphed.length == S0 + steps
+    assert int(graphed.pos.item()) == S0 + steps and int(graphed.nchunks.item()) == (S0 + steps) // 64
+    assert torch.equal(graphed.k_cache, eager.k_cache) and torch.equal(graphed.summary_buf, eager.summary_buf)
+    fresh = native.csa_chunk_summary(eager.k_cache[:, :, :1088].contiguous(), 64)
+    torch.testing.assert_close(eager.summary, fresh, rtol=0, atol=0)
