@@ -59,6 +59,9 @@ def parse_args():
     ap.add_argument("--no-block", action="store_true")
     ap.add_argument("--no-large-batch", action="store_true")
     ap.add_argument("--sweep", action="store_true", help="also run the BASELINE config-2 sweep (stderr + json)")
+    ap.add_argument("--dsv4-case", default=None, metavar="cR_nqN_hH",
+                    help="run only this DSV4 case (e.g. c4_nq32_h64), --steps eager calls over 16 rotated caches, "
+                         "print its timing and exit (a short program to profile)")
     ap.add_argument("--sweep-out", type=Path, default=None)
     ap.add_argument("--no-graph", action="store_true",
                     help="time eager launches only (for profiler counter passes, which serialise dispatches)")
@@ -336,6 +339,55 @@ def dsv4_bench(steps=200, copies=64):
     return out
 
 
+def dsv4_case_run(key, calls, copies=16):
+    """One DSV4 case of the dsv4 leg (same inputs), `calls` eager calls over
+    `copies` rotated caches; returns the mean call time from device events."""
+    import re
+
+    import torch
+
+    from csahca_amd import native
+    from csahca_amd.synthetic import make_dsv4_window_case
+
+    m = re.fullmatch(r"c(0|4|128)_nq(\d+)_h(\d+)", key)
+    if not m:
+        raise SystemExit(f"bench.py: --dsv4-case wants cR_nqN_hH with R in 0/4/128, got {key!r}")
+    ratio, nq, H = (int(x) for x in m.groups())
+    if nq > 32 or H > 64:
+        raise SystemExit("bench.py: --dsv4-case covers nq <= 32, H <= 64 (the dsv4 leg's inputs)")
+    dev = torch.device("cuda", 0)
+    c = make_dsv4_window_case(compress_ratio=ratio, num_queries=32, heads=64, seed=ratio, device=dev)
+    caches = [c.cache] + [c.cache.clone() for _ in range(copies - 1)]
+    ecaches = ([c.extra_cache] + [c.extra_cache.clone() for _ in range(copies - 1)]) if ratio else None
+    q = c.q[:nq, :H].contiguous()
+    idx, lens = c.token_indices[:nq].contiguous(), c.topk_lengths[:nq].contiguous()
+    sink = c.attn_sink[:H].contiguous()
+    eidx = c.extra_token_indices[:nq].contiguous() if ratio else None
+    elens = c.extra_topk_lengths[:nq].contiguous() if ratio else None
+    scale = 1.0 / math.sqrt(512)
+
+    def call(j):
+        if ratio:
+            return native.dsv4_decode_forward_tiled(q, caches[j], idx, lens, ecaches[j], eidx, elens, sink,
+                                                    c.page_size, c.extra_page_size, 0, scale)
+        return native.dsv4_decode_forward_tiled(q, caches[j], idx, lens, None, None, None, sink, c.page_size, 1, 0,
+                                                scale)
+
+    for j in range(copies):
+        call(j)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(calls):
+        call(i % copies)
+    end.record()
+    torch.cuda.synchronize()
+    slots = idx.shape[1] + (eidx.shape[1] if ratio else 0)
+    return {"dsv4_case": key, "calls": calls, "ms_per_call_eager": round(start.elapsed_time(end) / calls, 5),
+            "algorithmic_bytes": nq * slots * 584 + nq * H * 1024 * 2 + nq * slots * 4 + H * 4,
+            "flops": 2048 * slots * H * nq}
+
+
 def large_batch_bench(steps=40, copies=2):
     """The fused step where enough heads are in flight to be bandwidth-bound:
     BASELINE config-2 point B32 H8 D128 S131072 chunk 64 top-32 (the sweep's
@@ -572,6 +624,9 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"calibrate_copy": {"bytes_read_per_launch": n, "bytes_written_per_launch": n,
                                              "launches": 8}}), flush=True)
+        return
+    if args.dsv4_case:
+        print(json.dumps(dsv4_case_run(args.dsv4_case, args.steps)), flush=True)
         return
     r = csa_bench(args, copies=args.copies, attend_only=True)
     ms = r["ms_per_step_eager"] if args.no_graph else r["ms_per_step_graph"]

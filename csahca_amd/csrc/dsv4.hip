@@ -334,9 +334,16 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kMfmaHeads = 16;
 constexpr int kMfmaSlots = 32;
-// Row stride of the LDS V tile in bf16: 1056 B = 264 dwords (8 mod 64 banks),
-// so the 16 lanes of a transpose read touch 16 distinct bank pairs.
-constexpr int kVRowStride = kDim + 16;
+// Row stride of the LDS V tile in bf16: 1072 B = 268 dwords (12 mod 64 banks).
+// The 16 lanes of a 16-byte row store (slots 0..15) then start 12 banks apart
+// mod 64 (distinct 4-bank groups), and the 4 row groups of a transpose read
+// (rows r..r+3, 8 dwords each) land on banks [0,8), [12,20), [24,32), [36,44):
+// both conflict-free.
+constexpr int kVRowStride = kDim + 24;
+// Row stride of the per-wave score partials in floats (36 = 4 mod 32): the
+// stores of the 4 lane groups (rows 4 apart) and the 16-byte reads (rows
+// l%16) both spread over all banks.
+constexpr int kSpStride = kMfmaSlots + 4;
 constexpr int kMfmaWaves = 4;
 constexpr int kMfmaThreads = kMfmaWaves * kWave;
 constexpr int kKStepsPerWave = kDim / 32 / kMfmaWaves;  // 4 k-steps of 32 dims
@@ -418,7 +425,7 @@ struct MfmaArgs {
 __global__ __launch_bounds__(kMfmaThreads) void dsv4_mfma_kernel(const bf16* __restrict__ q, Dsv4Args a,
                                                                  MfmaArgs m) {
   __shared__ __align__(16) uint16_t vtile[kMfmaSlots * kVRowStride];     // [slot][dim] bf16 bits
-  __shared__ __align__(16) float sp[kMfmaWaves][kMfmaHeads][kMfmaSlots];  // per-wave score partials
+  __shared__ __align__(16) float sp[kMfmaWaves][kMfmaHeads][kSpStride];   // per-wave score partials
   __shared__ float xch[kMfmaWaves][kMfmaHeads];                           // per-wave head exchange
 
   const int tid = threadIdx.x;
