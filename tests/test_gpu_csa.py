@@ -276,7 +276,7 @@ def test_cuda_graph_replays_match_eager():
 
 FUSED = [
     # B, H, S, D, chunk, k, dtype      (P = workgroups per head follows from B*H)
-    (1, 8, 32768, 128, 64, 8, torch.bfloat16),     # headline: P = 32
+    (1, 8, 32768, 128, 64, 8, torch.bfloat16),     # headline: P = 8
     (1, 8, 32768, 128, 64, 32, torch.bfloat16),
     (2, 8, 8192, 128, 64, 8, torch.bfloat16),
     (8, 8, 8192, 128, 64, 16, torch.bfloat16),     # P = 8
@@ -311,6 +311,46 @@ def test_fused_step_matches_oracle_and_two_pass(B, H, S, D, chunk, k, dtype):
         assert_close(out, ref, atol, rtol, "fused vs oracle")
     two = extension.csa_decode_forward_tiled(qd, kd, vd, idx, chunk, 16)
     assert torch.allclose(out.float(), two.float(), atol=atol, rtol=rtol)
+    assert all(v == 0 for v in native.csa_step_status().values())
+
+
+def test_fused_step_ties_and_planted_selections():
+    B, H, S, D, chunk, k = 1, 8, 32768, 128, 64, 8  # P = 8 workgroups per head exchange keys
+    q = torch.ones(B, H, D, dtype=torch.bfloat16, device=DEV)
+    kc = torch.ones(B, H, S, D, dtype=torch.bfloat16, device=DEV)
+    v = torch.randn(B, H, S, D, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16).to(DEV)
+    _, idx = native.csa_decode_step(q, kc, v, extension.csa_chunk_summary(kc, chunk), chunk, k)
+    assert torch.equal(idx.cpu(), torch.arange(k, dtype=torch.int32).expand(B, H, k))  # all tie: lowest ids
+    kc[:, :, 300 * chunk:301 * chunk] = 2.0  # one winner above 511 tied chunks
+    _, idx = native.csa_decode_step(q, kc, v, extension.csa_chunk_summary(kc, chunk), chunk, k)
+    want = torch.tensor([300] + list(range(k - 1)), dtype=torch.int32).expand(B, H, k)
+    assert torch.equal(idx.cpu(), want)
+    C = S // chunk
+    case = make_synthetic_case(batch=B, heads=H, seq_len=S, head_dim=D, chunk_size=chunk, top_k=k, seed=4)
+    for ids in (scattered_chunks(B, H, C, k), clustered_chunks(B, H, C, k)):
+        kp = plant_chunks(case.q, case.k_cache, ids, chunk, alpha=1.0).to(DEV)
+        _, idx = native.csa_decode_step(case.q.to(DEV), kp, case.v_cache.to(DEV),
+                                        extension.csa_chunk_summary(kp, chunk), chunk, k)
+        assert torch.equal(idx.cpu(), ids)
+    assert all(v == 0 for v in native.csa_step_status().values())
+
+
+def test_fused_step_device_count_matches_oracle():
+    B, H, S, D, chunk, k = 1, 8, 32768, 128, 64, 8
+    case = make_synthetic_case(batch=B, heads=H, seq_len=S, head_dim=D, chunk_size=chunk, top_k=k, seed=6)
+    q, kd, vd = case.q.to(DEV), case.k_cache.to(DEV), case.v_cache.to(DEV)
+    summ = extension.csa_chunk_summary(kd, chunk)
+    summ_ref = oracle.chunk_mean(case.k_cache, chunk)
+    n = torch.zeros(1, dtype=torch.int32, device=DEV)
+    for count in (1, 5, 37, 100, 512):  # few chunks leave most workgroups without local candidates
+        n.fill_(count)
+        out, idx = native.csa_decode_step_dev(q, kd, vd, summ, n, chunk, k)
+        want, scores = oracle.select_topk(case.q, summ_ref[:, :, :count], k)
+        kk = want.shape[-1]
+        assert_indices(idx[:, :, :kk], want, scores)
+        assert torch.all(idx[:, :, kk:] == -1)
+        ref = oracle.csa_attend(case.q, case.k_cache, case.v_cache, idx.cpu(), chunk, prob_dtype=oracle.F32)
+        assert_close(out, ref, 2e-2, 1e-2, f"count {count}")
     assert all(v == 0 for v in native.csa_step_status().values())
 
 
