@@ -4,7 +4,7 @@ roofline of the dominant kernel, the CPU oracle baseline, and DSV4 ms/query.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--sweep] [--no-dsv4]
 
-Workload (BASELINE config 2 at its headline point): one decode step = select the
+Workload (the decode-step benchmark at its headline point): one decode step = select the
 top-8 of 512 chunks from cached fp32 chunk summaries (score + top-k kernels),
 then split-KV sparse attention over the 512 selected tokens of each head plus
 the partial merge.  B=1, H=8, D=128, S=32768, chunk 64, bf16 N(0,1) inputs from
@@ -58,7 +58,8 @@ def parse_args():
     ap.add_argument("--no-hca", action="store_true")
     ap.add_argument("--no-block", action="store_true")
     ap.add_argument("--no-large-batch", action="store_true")
-    ap.add_argument("--sweep", action="store_true", help="also run the BASELINE config-2 sweep (stderr + json)")
+    ap.add_argument("--sweep", action="store_true", help="also run the batch x context x top-k sweep: B {1,8,32} x S {8K,32K,128K} x k {8,32} "
+                         "(rows on stderr; --sweep-out FILE also writes them as JSON)")
     ap.add_argument("--dsv4-case", default=None, metavar="cR_nqN_hH",
                     help="run only this DSV4 case (e.g. c4_nq32_h64), --steps eager calls over 16 rotated caches, "
                          "print its timing and exit (a short program to profile)")
@@ -390,8 +391,7 @@ def dsv4_case_run(key, calls, copies=16):
 
 def large_batch_bench(steps=40, copies=2):
     """The fused step where enough heads are in flight to be bandwidth-bound:
-    BASELINE config-2 point B32 H8 D128 S131072 chunk 64 top-32 (the sweep's
-    largest), two distinct 17 GiB K/V copies alternating (no cache reuse).
+    Sweep point B32 H8 D128 S131072 chunk 64 top-32 (the sweep's largest), two distinct 17 GiB K/V copies alternating (no cache reuse).
     Reports the step time and HBM roofline on the algorithmic bytes (fp32
     summaries + selected K/V rows)."""
     import torch
@@ -480,14 +480,14 @@ def hca_bench(steps=256, copies=4, hca_chunk=256):
 
 
 def block_bench(steps=200, warmup=20):
-    """BASELINE config 3 on the decode blocks of csahca_amd.block, at S=32768,
+    """The decode blocks of csahca_amd.block at S=32768,
     H=8, D=128 (hidden 1024), chunk 64, top-8, bf16, 200 steps after 20 warm-up
     steps, the hidden state fed back each step (the reference harness,
     hybrid_attention/model_inference.py:140-162).  Like that harness it reuses
     one static cache (no rotation).  Reference block: precomputed selection
     (tiled op, tile 8) and dynamic selection (fused step from cached summaries,
     and from summaries rebuilt every step as the reference does), eager and as
-    one HIP graph per step.  BASELINE block (RMSNorm/QKV/SiLU MLP, growing
+    one HIP graph per step.  Hybrid block (RMSNorm/QKV/SiLU MLP, growing
     cache): eager, and as one HIP graph per step whose replays advance the
     cache (position and chunk count live on the device)."""
     import torch
@@ -685,9 +685,9 @@ def main():
         line["dsv4"] = dsv4_bench()
     if args.sweep:
         rows = sweep(args)
-        out = args.sweep_out or (ROOT / "gpurun_out" / "sweep.json")
-        out.parent.mkdir(parents=True, exist_ok=True)
-        out.write_text(json.dumps(rows, indent=1) + "\n")
+        if args.sweep_out is not None:
+            args.sweep_out.parent.mkdir(parents=True, exist_ok=True)
+            args.sweep_out.write_text(json.dumps(rows, indent=1) + "\n")
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)

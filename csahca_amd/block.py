@@ -15,7 +15,7 @@ Two blocks:
     reference's per-step ``chunk_mean`` exactly, rebuilt every step
     (``summary_cache=False``).
 
-* ``HybridDecodeBlock`` -- the BASELINE config-3 block: RMSNorm -> QKV
+* ``HybridDecodeBlock`` -- a hybrid decode block: RMSNorm -> QKV
   projection -> the new token's K/V appended to a growing cache -> the chunk
   summary of a chunk that just completed -> CSA over the complete chunks (fused
   step) -> out projection -> residual -> RMSNorm -> SiLU MLP -> residual.
@@ -91,7 +91,7 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.
 
 
 class HybridDecodeBlock:
-    """RMSNorm -> QKV -> CSA over a growing cache -> out
+    """Hybrid decode block: RMSNorm -> QKV -> CSA over a growing cache -> out
     projection -> SiLU MLP, weights N(0, 0.02^2).
 
     The cache is preallocated with ``capacity`` token slots and the chunk

@@ -149,7 +149,7 @@ def make_dsv4_window_case(*, compress_ratio: int, num_queries: int, heads: int, 
                           page_size: int = 64, window: int = 128, extra_top_k: int = 64,
                           extra_page_size: int | None = None, q_dtype: torch.dtype = torch.bfloat16,
                           seed: int = 0, device: str | torch.device = "cpu") -> Dsv4Case:
-    """A serving-shaped DSV4 decode workload (BASELINE configs 4 and 5).
+    """A serving-shaped DSV4 decode workload (SWA windows over a paged pool, C4/C128 extra slots).
 
     ``context`` latent rows are stored in pages of ``page_size`` whose physical
     order is a seeded random permutation (the page table).  Query ``i`` attends

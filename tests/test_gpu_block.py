@@ -3,7 +3,7 @@
 MiniCSADecodeBlock restates hybrid_attention/model_inference.py:14-76; its
 reference here is the same block on the CPU in torch with identical weights and
 the oracle's CSA (cuda-csa semantics: fp32 probabilities).  HybridDecodeBlock
-is checked step by step against a CPU restatement that
+(the hybrid block over a growing cache) is checked step by step against a CPU restatement that
 rounds exactly where the GPU block stores bf16 (q, the appended K/V, every
 linear output).  Tolerance: |got - ref| <= 2e-2 + 1e-2 |ref| on block outputs.
 """

@@ -1,6 +1,6 @@
 """GPU parity of the CSA kernels against the CPU oracle (and golden vectors).
 
-Tolerances: outputs |got - ref| <= 2e-2 + 1e-2 |ref| for
+Tolerances (the parity bar of this path): outputs |got - ref| <= 2e-2 + 1e-2 |ref| for
 16-bit storage (1e-4 + 1e-4 |ref| for fp32/fp64 storage); selected chunk ids
 bit-exact under the declared tie-break (score desc, chunk id asc), where a
 mismatch is accepted only between chunks whose oracle scores agree to 1e-5

@@ -1,6 +1,6 @@
 """GPU parity of the DSV4 paged-FP8 decode against the CPU oracle and the
-reference's golden vectors.  Tolerance for the FP8-cache modes (BASELINE north
-star): |got - ref| <= 5e-2 + 5e-2 |ref| for 16-bit queries; fp32 queries are
+reference's golden vectors.  Tolerance for the FP8-cache modes (the parity bar
+of this path): |got - ref| <= 5e-2 + 5e-2 |ref| for 16-bit queries; fp32 queries are
 held to 1e-4 + 1e-4 |ref|."""
 import math
 import os

@@ -2,7 +2,7 @@
 CSA/HCA hybrid blend (hybrid_reference, reference.py:95-108) against the CPU
 oracle and the golden vectors.
 
-Tolerance: |got - ref| <= 2e-2 + 1e-2 |ref| for 16-bit
+Tolerance (the parity bar of this path): |got - ref| <= 2e-2 + 1e-2 |ref| for 16-bit
 storage, 1e-4 + 1e-4 |ref| for fp32/fp64 storage.
 """
 import numpy as np
