@@ -99,6 +99,36 @@ def test_dsv4_argument_errors(lib):
     assert rc == 1 and lib.csahca_last_error().decode() == "extra_page_size must be positive"
 
 
+def test_device_state_entry_points_argument_errors(lib):
+    """csahca_csa_decode_step_dev / csahca_csa_chunk_summary_at reject bad
+    arguments before any HIP call (dummy pointers are never dereferenced)."""
+    def step(**o):
+        a = dict(q=1, k=1, v=1, summ=1, n=1, out=1, idx=1, dtype=2, B=1, H=1, S=64, D=128, C=1, chunk=64, top_k=1,
+                 ws=None, wsb=0)
+        a.update(o)
+        return lib.csahca_csa_decode_step_dev(a["q"], a["k"], a["v"], a["summ"], a["n"], a["out"], a["idx"], a["dtype"],
+                                              a["B"], a["H"], a["S"], a["D"], a["C"], a["chunk"], a["top_k"], a["ws"],
+                                              a["wsb"], None)
+
+    assert step(n=None) == 1 and lib.csahca_last_error().decode() == "null num_chunks pointer"
+    assert step(chunk=0) == 1 and lib.csahca_last_error().decode() == "chunk_size must be positive"
+    assert step(C=2) == 1 and lib.csahca_last_error().decode() == "summaries cover more chunks than the cache holds"
+    assert step(top_k=-1) == 1
+    assert step() == 2  # valid arguments, no workspace
+    assert step(B=0) == 0
+
+    def summ_at(**o):
+        a = dict(k=1, summ=1, dtype=2, B=1, H=1, S=64, D=128, chunk=64, C=1, pos=1)
+        a.update(o)
+        return lib.csahca_csa_chunk_summary_at(a["k"], a["summ"], a["dtype"], a["B"], a["H"], a["S"], a["D"],
+                                               a["chunk"], a["C"], a["pos"], None)
+
+    assert summ_at(pos=None) == 1 and lib.csahca_last_error().decode() == "null token_pos pointer"
+    assert summ_at(chunk=0) == 1 and lib.csahca_last_error().decode() == "chunk_size must be positive"
+    assert summ_at(dtype=9) == 1
+    assert summ_at(C=0) == 0  # no summary rows: nothing to write
+
+
 def test_binding_rejects_cpu_tensors_with_reference_messages(lib):
     q = torch.zeros(1, 2, 64, dtype=torch.bfloat16)
     k = torch.zeros(1, 2, 128, 64, dtype=torch.bfloat16)
