@@ -364,3 +364,29 @@ def test_fused_step_repeated_calls_rearm_counters():
     torch.cuda.synchronize()
     assert torch.equal(out, first) and torch.equal(idx2, idx)
     assert all(v == 0 for v in native.csa_step_status().values())
+
+
+def test_largest_sweep_point_properties():
+    """B32 H8 S131072 D128 top-32 (17 GiB of K/V) is too large for the CPU
+    oracle, so parity rests on size-independent properties: planted chunks are
+    selected exactly and in their planted order, the fused step's ids equal the
+    selection kernels', and its output equals the two-pass split-KV route over
+    those ids."""
+    B, H, S, D, chunk, k = 32, 8, 131072, 128, 64, 32
+    g = torch.Generator(device=DEV).manual_seed(123)
+    q = torch.randn(B, H, D, device=DEV, generator=g).to(torch.bfloat16)
+    kc = torch.randn(B, H, S, D, device=DEV, generator=g, dtype=torch.bfloat16)
+    vc = torch.randn(B, H, S, D, device=DEV, generator=g, dtype=torch.bfloat16)
+    ids = scattered_chunks(B, H, S // chunk, k).to(DEV)
+    q_hat = q.float() / q.float().norm(dim=-1, keepdim=True)
+    for j, c in enumerate(ids[0, 0].tolist()):  # the same chunks in every head; bias k - j orders them
+        kc[:, :, c * chunk:(c + 1) * chunk] += ((k - j) * q_hat)[:, :, None, :].to(torch.bfloat16)
+    summ = extension.csa_chunk_summary(kc, chunk)
+    out, idx = native.csa_decode_step(q, kc, vc, summ, chunk, k)
+    assert torch.equal(idx, ids)
+    assert torch.equal(idx, extension.csa_select_topk(q, summ, k))
+    two = extension.csa_decode_forward_tiled(q, kc, vc, idx, chunk, 16)
+    assert_close(out, two.float().cpu().numpy(), 2e-2, 1e-2, "fused vs two-pass at B32 S131072 k32")
+    assert all(v == 0 for v in native.csa_step_status().values())
+    del q, kc, vc, summ, out, two
+    torch.cuda.empty_cache()
