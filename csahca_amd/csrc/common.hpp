@@ -101,6 +101,64 @@ __device__ __forceinline__ void load16<double>(const double* __restrict__ p, flo
   out[1] = static_cast<float>(w.y);
 }
 
+// Widen 16 loaded bytes of T to fp32 (N = 16/sizeof(T) values).
+template <typename T>
+__device__ __forceinline__ void widen16(const uint4 w, float* out);
+template <>
+__device__ __forceinline__ void widen16<bf16>(const uint4 w, float* out) {
+  const uint32_t x[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = __uint_as_float(x[i] << 16);
+    out[2 * i + 1] = __uint_as_float(x[i] & 0xffff0000u);
+  }
+}
+template <>
+__device__ __forceinline__ void widen16<f16>(const uint4 w, float* out) {
+  const uint32_t x[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(x[i] & 0xffffu)));
+    out[2 * i + 1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(x[i] >> 16)));
+  }
+}
+template <>
+__device__ __forceinline__ void widen16<float>(const uint4 w, float* out) {
+  out[0] = __uint_as_float(w.x);
+  out[1] = __uint_as_float(w.y);
+  out[2] = __uint_as_float(w.z);
+  out[3] = __uint_as_float(w.w);
+}
+template <>
+__device__ __forceinline__ void widen16<double>(const uint4 w, float* out) {
+  out[0] = static_cast<float>(__builtin_bit_cast(double, (static_cast<uint64_t>(w.y) << 32) | w.x));
+  out[1] = static_cast<float>(__builtin_bit_cast(double, (static_cast<uint64_t>(w.w) << 32) | w.z));
+}
+
+// One unconditional global load from an address the compiler cannot see
+// through (an empty asm launders it): selects of addresses stay selects, and
+// no load ends up under a per-lane branch, where the wait-count pass would
+// make every load in flight complete at the join and so serialise a batch of
+// loads meant to overlap.
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+template <typename V>
+__device__ __forceinline__ V load_global_raw(const void* p) {
+  uint64_t a = reinterpret_cast<uint64_t>(p);
+  asm volatile("" : "+v"(a));
+  return *reinterpret_cast<const __attribute__((address_space(1))) V*>(a);
+}
+__device__ __forceinline__ int32_t load_global_i32(const void* p) { return load_global_raw<int32_t>(p); }
+__device__ __forceinline__ uint2 load_global_u2(const void* p) {
+  const u32x2_t v = load_global_raw<u32x2_t>(p);
+  return make_uint2(v[0], v[1]);
+}
+__device__ __forceinline__ uint4 load_global_u4(const void* p) {
+  const u32x4_t v = load_global_raw<u32x4_t>(p);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
 // Store N = 16/sizeof(T) values; p 16-byte aligned.
 template <typename T>
 __device__ __forceinline__ void store16(T* __restrict__ p, const float* v) {

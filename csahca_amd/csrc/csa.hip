@@ -41,10 +41,7 @@ __global__ __launch_bounds__(64) void csa_attend_vec_kernel(
   const int t = static_cast<int>(item % num_tiles);
   const int64_t bh = item / num_tiles;
 
-  float qf[VEC];
-  load16<T>(q + bh * D + col * VEC, qf);
-#pragma unroll
-  for (int e = 0; e < VEC; ++e) qf[e] *= qscale;
+  const T* qp = q + bh * D + col * VEC;
   const T* __restrict__ kb = k + bh * seq_len * D + col * VEC;
   const T* __restrict__ vb = v + bh * seq_len * D + col * VEC;
   const IdxT* __restrict__ ib = idx + bh * top_k;
@@ -57,7 +54,8 @@ __global__ __launch_bounds__(64) void csa_attend_vec_kernel(
   };
   WaveSoftmax<T, D> st;
   st.init();
-  for (int base = s0; base < s1; base += RPL * U) attend_block<T, D, U>(st, qf, kb, vb, base, s1, grp, tok_of);
+  for (int base = s0; base < s1; base += RPL * U)
+    attend_block<T, D, U>(st, qp, qscale, kb, vb, base, s1, grp, tok_of);
   fold_row_groups(st);
   const int64_t p = bh * num_tiles + t;
   if (grp == 0) {

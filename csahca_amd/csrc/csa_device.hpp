@@ -302,27 +302,55 @@ struct WaveSoftmax {
 
 // Process rows base + grp + RPL*u (u < U) of the slot range [.., s1): tok_of(s,
 // tok) maps a slot to a token (false = skip).  kb/vb point at this lane's
-// columns of row 0 of the (b,h) cache.
+// columns of row 0 of the (b,h) cache, qp at this lane's 16 bytes of q (scaled
+// here by qscale).  Every row load is unconditional (a skipped slot reads row
+// 0 and is zeroed after the load) and q is loaded after the rows -- the newest
+// load, so one wait covers the batch and no hoisted use of q can make the rows
+// wait -- so the 2U + 1 loads of a lane are one batch in flight.
 template <typename T, int D, int U, typename TokOf>
-__device__ __forceinline__ void attend_block(WaveSoftmax<T, D>& st, const float* qf,
+__device__ __forceinline__ void attend_block(WaveSoftmax<T, D>& st, const T* qp, float qscale,
                                              const T* __restrict__ kb, const T* __restrict__ vb,
                                              int base, int s1, int grp, TokOf tok_of) {
   using L = AttendLayout<T, D>;
   constexpr int VEC = L::VEC, LPR = L::LPR, RPL = L::RPL;
-  float kr[U][VEC], vr[U][VEC];
+  // Tokens first (chunk ids may come from global memory), then every row:
+  // the empty asm takes all token positions, so no row load is scheduled
+  // before the last id is known -- an id wait after a row load would, with
+  // in-order wait counts, also wait for that row.
+  int64_t toks[U];
   bool ok[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
+    // Slots past s1 look up slot s1 - 1 (valid whenever this block runs) and
+    // are dropped afterwards: the id lookup stays outside any branch.
     const int s = base + grp + RPL * u;
     int64_t tok = 0;
-    ok[u] = s < s1 && tok_of(s, tok);
-    if (ok[u]) {
-      load16<T>(kb + tok * D, kr[u]);
-      load16<T>(vb + tok * D, vr[u]);
-    } else {
+    const bool found = tok_of(s < s1 ? s : s1 - 1, tok);
+    ok[u] = s < s1 && found;
+    toks[u] = ok[u] ? tok : 0;
+  }
+  if constexpr (U == 4) {
+    asm volatile("" : "+v"(toks[0]), "+v"(toks[1]), "+v"(toks[2]), "+v"(toks[3]));
+  } else {
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) kr[u][e] = vr[u][e] = 0.f;
-    }
+    for (int u = 0; u < U; ++u) asm volatile("" : "+v"(toks[u]));
+  }
+  uint4 rk[U], rv[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    rk[u] = load_global_u4(kb + toks[u] * D);
+    rv[u] = load_global_u4(vb + toks[u] * D);
+  }
+  float qf[VEC];
+  widen16<T>(load_global_u4(qp), qf);
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) qf[e] *= qscale;
+  float kr[U][VEC], vr[U][VEC];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+    widen16<T>(ok[u] ? rk[u] : z, kr[u]);
+    widen16<T>(ok[u] ? rv[u] : z, vr[u]);
   }
   float sc[U];
 #pragma unroll

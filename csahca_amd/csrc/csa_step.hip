@@ -131,26 +131,57 @@ __global__ __launch_bounds__(kStepThreads) void csa_step_kernel(StepParams a) {
   const int64_t C = a.c_dev ? min<int64_t>(max<int32_t>(*a.c_dev, 0), Cs) : a.C;
   const T* __restrict__ q = static_cast<const T*>(a.q) + h * D;
 
-  // This launch's tag for the head.  Every thread issues the (same-address)
-  // load; it is first consumed when phase A publishes keys, so its latency
-  // overlaps the summary loads.
-  const uint32_t tag =
-      P > 1 ? __hip_atomic_load(&a.epoch[h], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u : 0u;
+  // Loads that depend on nothing are issued together, unconditionally, and
+  // consumed only after the summary rows are requested, so phase A costs one
+  // memory round trip: this launch's tag for the head (epoch + 1; every head
+  // has an epoch word, read even when P = 1), q in the summary lane layout,
+  // and the summary rows.
+  const uint32_t epoch = __hip_atomic_load(&a.epoch[h], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   // ---- A: order keys of this workgroup's chunk range ----------------------
   {
     const int grp = lane / SLPR, col = lane % SLPR;
-    float qf4[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) qf4[e] = to_f32(q[col * 4 + e]);
     const float* __restrict__ sb = a.summary + h * Cs * D + col * 4;
     uint64_t* kg = a.keys + h * Cs;
     const int64_t c0 = Cs * p / P, c1 = Cs * (p + 1) / P;
     constexpr int US = kStepScoreUnroll;
     for (int64_t blk = c0; blk < c1; blk += kStepWaves * SRPL * US) {
       const int64_t base = blk + wave * SRPL * US;
+      uint4 rs[US];  // rows past the range re-read row c0 (their scores are dropped)
+#pragma unroll
+      for (int u = 0; u < US; ++u) {
+        const int64_t c = base + grp + SRPL * u;
+        rs[u] = load_global_u4(sb + (c < c1 ? c : c0) * D);
+      }
+      // q[col*4 .. col*4+3] is requested after the rows (the newest load, so
+      // waiting for it covers them all) and the epoch is consumed only here:
+      // the empty asm keeps the compiler from hoisting its use above the loads.
+      uint4 q4;
+      if constexpr (sizeof(T) == 4) {
+        q4 = load_global_u4(q + col * 4);
+      } else {
+        const uint2 t2 = load_global_u2(q + col * 4);
+        q4 = make_uint4(t2.x, t2.y, 0u, 0u);
+      }
+      uint32_t ep = epoch;
+      asm volatile("" : "+v"(ep));
+      float qf[8];
+      widen16<T>(q4, qf);
       float sc[US];
-      score_block<D, US>(qf4, sb, base, c1, grp, sc);
+#pragma unroll
+      for (int u = 0; u < US; ++u) {
+        float r4[4];
+        widen16<float>(rs[u], r4);
+        float d = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) d = fmaf(qf[e], r4[e], d);
+        sc[u] = d;
+      }
+#pragma unroll
+      for (int off = SLPR / 2; off >= 1; off >>= 1)
+#pragma unroll
+        for (int u = 0; u < US; ++u) sc[u] += xor_lanes(sc[u], off);
+      const uint32_t tag = ep + 1u;
       if (col == 0) {
 #pragma unroll
         for (int u = 0; u < US; ++u) {
@@ -168,6 +199,7 @@ __global__ __launch_bounds__(kStepThreads) void csa_step_kernel(StepParams a) {
   }
 
   // ---- B: gather the head's keys, top-k -----------------------------------
+  const uint32_t tag = epoch + 1u;
   if (P > 1) {
     const uint64_t* kg = a.keys + h * Cs;
     for (int64_t i0 = tid; i0 < C; i0 += kStepThreads * B8) {
@@ -205,10 +237,7 @@ __global__ __launch_bounds__(kStepThreads) void csa_step_kernel(StepParams a) {
   const int s0 = static_cast<int>(static_cast<int64_t>(nslots) * p / P);
   const int s1 = static_cast<int>(static_cast<int64_t>(nslots) * (p + 1) / P);
   const int grp = lane / LPR, col = lane % LPR;
-  float qf[VEC];
-  load16<T>(q + col * VEC, qf);
-#pragma unroll
-  for (int e = 0; e < VEC; ++e) qf[e] *= a.qscale;
+  const T* qp = q + col * VEC;  // loaded inside attend_block, after the K/V rows
   const T* __restrict__ kb = static_cast<const T*>(a.kcache) + h * a.S * D + col * VEC;
   const T* __restrict__ vb = static_cast<const T*>(a.vcache) + h * a.S * D + col * VEC;
   auto get_id = [&](int cs) { return sel[cs]; };
@@ -218,7 +247,7 @@ __global__ __launch_bounds__(kStepThreads) void csa_step_kernel(StepParams a) {
   WaveSoftmax<T, D> st;
   st.init();
   for (int blk = s0; blk < s1; blk += kStepWaves * RPL * U)
-    attend_block<T, D, U>(st, qf, kb, vb, blk + wave * RPL * U, s1, grp, tok_of);
+    attend_block<T, D, U>(st, qp, a.qscale, kb, vb, blk + wave * RPL * U, s1, grp, tok_of);
   fold_row_groups(st);
   float* cw = comb + wave * (D + 2);
   if (lane == 0) {

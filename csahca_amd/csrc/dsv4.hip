@@ -393,29 +393,6 @@ __device__ __forceinline__ uint4 dequant8_bf16(uint2 w, uint32_t sbyte) {
   return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
-// One unconditional global load from an address the compiler cannot see
-// through (an empty asm launders it): selects of addresses stay selects, and
-// no load ends up under a branch, where the wait-count pass would serialise
-// the loads in flight at the join.
-typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-
-template <typename V>
-__device__ __forceinline__ V load_global_raw(const void* p) {
-  uint64_t a = reinterpret_cast<uint64_t>(p);
-  asm volatile("" : "+v"(a));
-  return *reinterpret_cast<const __attribute__((address_space(1))) V*>(a);
-}
-__device__ __forceinline__ int32_t load_global_i32(const void* p) { return load_global_raw<int32_t>(p); }
-__device__ __forceinline__ uint2 load_global_u2(const void* p) {
-  const u32x2_t v = load_global_raw<u32x2_t>(p);
-  return make_uint2(v[0], v[1]);
-}
-__device__ __forceinline__ uint4 load_global_u4(const void* p) {
-  const u32x4_t v = load_global_raw<u32x4_t>(p);
-  return make_uint4(v[0], v[1], v[2], v[3]);
-}
-
 struct MfmaArgs {
   int splits;           // slot-list splits per (query, head group)
   int tiles_per_split;  // 32-slot tiles per split

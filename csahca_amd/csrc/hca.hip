@@ -35,40 +35,6 @@ constexpr int kHcaProbChunk = 2048;  // probabilities staged in LDS per pass
 
 constexpr int kRowBatch = 8;          // rows of K and V in flight per thread
 
-// Widen one 16-byte load of T to fp32.
-template <typename T>
-__device__ __forceinline__ void widen16(const uint4 w, float* out);
-template <>
-__device__ __forceinline__ void widen16<bf16>(const uint4 w, float* out) {
-  const uint32_t x[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    out[2 * i] = __uint_as_float(x[i] << 16);
-    out[2 * i + 1] = __uint_as_float(x[i] & 0xffff0000u);
-  }
-}
-template <>
-__device__ __forceinline__ void widen16<f16>(const uint4 w, float* out) {
-  const uint32_t x[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    out[2 * i] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(x[i] & 0xffffu)));
-    out[2 * i + 1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(x[i] >> 16)));
-  }
-}
-template <>
-__device__ __forceinline__ void widen16<float>(const uint4 w, float* out) {
-  out[0] = __uint_as_float(w.x);
-  out[1] = __uint_as_float(w.y);
-  out[2] = __uint_as_float(w.z);
-  out[3] = __uint_as_float(w.w);
-}
-template <>
-__device__ __forceinline__ void widen16<double>(const uint4 w, float* out) {
-  out[0] = static_cast<float>(__builtin_bit_cast(double, (static_cast<uint64_t>(w.y) << 32) | w.x));
-  out[1] = static_cast<float>(__builtin_bit_cast(double, (static_cast<uint64_t>(w.w) << 32) | w.z));
-}
-
 template <typename T>
 __device__ __forceinline__ float round_to(float x) {
   return to_f32(from_f32<T>(x));
