@@ -419,18 +419,26 @@ __global__ __launch_bounds__(kMfmaThreads) void dsv4_mfma_kernel(const bf16* __r
   const int nh = min(kMfmaHeads, a.heads - h0);
 
   // Q A-operands of this wave's k-steps: head h0 + l16, dims 32 kk + 8 grp .. +7.
-  bf16x8_t qa[kKStepsPerWave];
+  // Prologue loads are unconditional (a head past nh re-reads head h0, a
+  // missing length array reads q) and consumed after all are issued, so the
+  // q operands, the lengths and the first slot indices are one batch.
+  uint4 qw[kKStepsPerWave];
+  const int hq = h0 + min(l16, nh - 1);
 #pragma unroll
   for (int i = 0; i < kKStepsPerWave; ++i) {
     const int d0 = 32 * (wave * kKStepsPerWave + i) + 8 * grp;
-    uint4 w = make_uint4(0u, 0u, 0u, 0u);
-    if (l16 < nh) w = *reinterpret_cast<const uint4*>(q + ((query * a.heads) + h0 + l16) * kDim + d0);
-    qa[i] = __builtin_bit_cast(bf16x8_t, w);
+    qw[i] = load_global_u4(q + ((query * a.heads) + hq) * kDim + d0);
   }
+  const int32_t len_raw = load_global_i32(a.lens ? static_cast<const void*>(a.lens + query) : static_cast<const void*>(q));
+  const int32_t elen_raw =
+      load_global_i32(a.elens ? static_cast<const void*>(a.elens + query) : static_cast<const void*>(q));
+  bf16x8_t qa[kKStepsPerWave];
+#pragma unroll
+  for (int i = 0; i < kKStepsPerWave; ++i)
+    qa[i] = __builtin_bit_cast(bf16x8_t, l16 < nh ? qw[i] : make_uint4(0u, 0u, 0u, 0u));
 
-  const int n_swa = a.lens ? max(0, min(a.lens[query], a.topk_slots)) : a.topk_slots;
-  const int n_extra =
-      a.extra_slots > 0 ? (a.elens ? max(0, min(a.elens[query], a.extra_slots)) : a.extra_slots) : 0;
+  const int n_swa = a.lens ? max(0, min(len_raw, a.topk_slots)) : a.topk_slots;
+  const int n_extra = a.extra_slots > 0 ? (a.elens ? max(0, min(elen_raw, a.extra_slots)) : a.extra_slots) : 0;
   const int total = a.topk_slots + a.extra_slots;
   const int t0 = split * m.tiles_per_split;
   const int t1 = min(t0 + m.tiles_per_split, (total + kMfmaSlots - 1) / kMfmaSlots);
@@ -448,19 +456,27 @@ __global__ __launch_bounds__(kMfmaThreads) void dsv4_mfma_kernel(const bf16* __r
   // index loads are unconditional (clamped positions, results selected after
   // the load): loads under per-lane branches make the compiler wait for every
   // outstanding load at the join, which would serialise the prefetch below.
-  auto slot_loc = [&](int t, int nt) -> int32_t {
+  // Issue (two index loads) and resolve (validity select) are separate steps
+  // so a caller can issue several slots' loads before consuming any.
+  struct SlotIdx {
+    int32_t li, le;
+  };
+  auto slot_issue = [&](int t, int nt) -> SlotIdx {
     const int s = t * kMfmaSlots + l16 + 16 * nt;
     const int32_t* ip = a.topk_slots > 0 ? a.idx + query * a.topk_slots + min(s, a.topk_slots - 1)
                                          : reinterpret_cast<const int32_t*>(dummy);
     const int32_t* ep = a.extra_slots > 0
                             ? a.eidx + query * a.extra_slots + min(max(s - a.topk_slots, 0), a.extra_slots - 1)
                             : reinterpret_cast<const int32_t*>(dummy);
-    const int32_t li = load_global_i32(ip);
-    const int32_t le = load_global_i32(ep);
+    return SlotIdx{load_global_i32(ip), load_global_i32(ep)};
+  };
+  auto slot_resolve = [&](int t, int nt, SlotIdx r) -> int32_t {
+    const int s = t * kMfmaSlots + l16 + 16 * nt;
     const bool in_swa = s < a.topk_slots;
     const bool valid = t < t1 && s < total && (in_swa ? s < n_swa : s - a.topk_slots < n_extra);
-    return valid ? (in_swa ? li : le) : -1;
+    return valid ? (in_swa ? r.li : r.le) : -1;
   };
+  auto slot_loc = [&](int t, int nt) -> int32_t { return slot_resolve(t, nt, slot_issue(t, nt)); };
   // This lane's latent bytes of a tile: for each slot, the wave's 4 k-steps
   // (8 e4m3 bytes in .x/.y, or 16 bytes of bf16 rope) and the scale row.
   struct Rows {
@@ -503,9 +519,16 @@ __global__ __launch_bounds__(kMfmaThreads) void dsv4_mfma_kernel(const bf16* __r
   // Two-stage pipeline: while tile t is processed, the rows of tile t+1 and
   // the slot locations of tile t+2 are in flight (lds_barrier keeps them so).
   Rows cur, nxt;
-  int32_t loc[2] = {slot_loc(t0, 0), slot_loc(t0, 1)};
+  // Prologue: the index loads of tiles t0 and t0+1 go out with the q and
+  // length loads above; the empty asm makes every one of them issue before
+  // any is consumed.
+  SlotIdx i00 = slot_issue(t0, 0), i01 = slot_issue(t0, 1), i10 = slot_issue(t0 + 1, 0),
+          i11 = slot_issue(t0 + 1, 1);
+  asm volatile("" : "+v"(i00.li), "+v"(i00.le), "+v"(i01.li), "+v"(i01.le), "+v"(i10.li), "+v"(i10.le),
+               "+v"(i11.li), "+v"(i11.le));
+  int32_t loc[2] = {slot_resolve(t0, 0, i00), slot_resolve(t0, 1, i01)};
   issue_rows(t0, loc, cur);
-  int32_t loc_n[2] = {slot_loc(t0 + 1, 0), slot_loc(t0 + 1, 1)};
+  int32_t loc_n[2] = {slot_resolve(t0 + 1, 0, i10), slot_resolve(t0 + 1, 1, i11)};
   for (int t = t0; t < t1; ++t) {
     if (t + 1 < t1) issue_rows(t + 1, loc_n, nxt);
     const int32_t loc_nn[2] = {slot_loc(t + 2, 0), slot_loc(t + 2, 1)};

@@ -192,13 +192,16 @@ __global__ __launch_bounds__(kHcaThreads) void hca_merge_kernel(const float* __r
   float a = 0.f;
   if (C <= kMergeFastRows) {
     const int n = static_cast<int>(C);
-    const float sc = tid < n ? sb[tid] : -INFINITY;
+    // Unconditional loads (clamped indices, values dropped after the load):
+    // the score and the V-mean column values are one batch in flight.
+    const float sraw = load_global_raw<float>(sb + (tid < n ? tid : 0));
     float x[kMergeRows];
 #pragma unroll
     for (int i = 0; i < kMergeRows; ++i) {
       const int r = rg + i * kMergeRowGroups;
-      x[i] = col[static_cast<int64_t>(r < n ? r : 0) * D];
+      x[i] = load_global_raw<float>(col + static_cast<int64_t>(r < n ? r : 0) * D);
     }
+    const float sc = tid < n ? sraw : -INFINITY;
     const float M = block_reduce(sc, red, true);
     const float e = (tid < n && M != -INFINITY) ? fast_exp2((sc - M) * kLog2e) : 0.f;
     const float L = block_reduce(e, red, false);
