@@ -159,6 +159,25 @@ __device__ __forceinline__ uint4 load_global_u4(const void* p) {
   return make_uint4(v[0], v[1], v[2], v[3]);
 }
 
+// Four consecutive elements of T at p (aligned to 4 * sizeof(T)) widened to
+// fp32, through unconditional loads of 8, 16 or 2 x 16 bytes.
+template <typename T>
+__device__ __forceinline__ void load4_f32(const T* p, float* out) {
+  float tmp[8];
+  if constexpr (sizeof(T) == 2) {
+    const uint2 t = load_global_u2(p);
+    widen16<T>(make_uint4(t.x, t.y, 0u, 0u), tmp);
+  } else if constexpr (sizeof(T) == 4) {
+    widen16<T>(load_global_u4(p), tmp);
+  } else {
+    const uint4 lo = load_global_u4(p), hi = load_global_u4(p + 2);
+    widen16<T>(lo, tmp);
+    widen16<T>(hi, tmp + 2);
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) out[e] = tmp[e];
+}
+
 // Store N = 16/sizeof(T) values; p 16-byte aligned.
 template <typename T>
 __device__ __forceinline__ void store16(T* __restrict__ p, const float* v) {

@@ -345,11 +345,32 @@ __global__ __launch_bounds__(64) void csa_score_vec_kernel(const T* __restrict__
   const int col = lane % LPR;
   const int64_t bh = blockIdx.x / blocks_per_head;
   const int64_t c0 = (blockIdx.x % blocks_per_head) * R;
-  float qf[4];
+  // One memory round trip: the summary rows are requested unconditionally
+  // (rows past C re-read row c0; their scores are never stored), then q, and
+  // only then is anything consumed.
+  const float* __restrict__ sb = summary + bh * C * D + col * 4;
+  uint4 rs[U];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) qf[e] = to_f32(q[bh * D + col * 4 + e]);
+  for (int u = 0; u < U; ++u) {
+    const int64_t c = c0 + grp + RPL * u;
+    rs[u] = load_global_u4(sb + (c < C ? c : c0) * D);
+  }
+  float qf[4];
+  load4_f32<T>(q + bh * D + col * 4, qf);
   float sc[U];
-  score_block<D, U>(qf, summary + bh * C * D + col * 4, c0, C, grp, sc);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    float r4[4];
+    widen16<float>(rs[u], r4);
+    float d = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) d = fmaf(qf[e], r4[e], d);
+    sc[u] = d;
+  }
+#pragma unroll
+  for (int off = LPR / 2; off >= 1; off >>= 1)
+#pragma unroll
+    for (int u = 0; u < U; ++u) sc[u] += xor_lanes(sc[u], off);
   if (col == 0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -517,7 +538,7 @@ int csa_select_launch(const void* q, const float* summary, int32_t* out_indices,
                       int64_t bh, int64_t C, int64_t D, int64_t k, uint32_t* keys,
                       hipStream_t stream) {
   const float scale = 1.0f / sqrtf(static_cast<float>(D));
-  const bool aligned = reinterpret_cast<uintptr_t>(summary) % 16 == 0;
+  const bool aligned = (reinterpret_cast<uintptr_t>(summary) | reinterpret_cast<uintptr_t>(q)) % 16 == 0;
   int rc = dispatch_dtype(dtype, [&](auto tag) -> int {
     using T = decltype(tag);
     const T* qp = static_cast<const T*>(q);

@@ -402,28 +402,4 @@ __device__ __forceinline__ void fold_row_groups(WaveSoftmax<T, D>& st) {
   }
 }
 
-// Scores of R consecutive fp32 summary rows starting at c0 (rows >= C skipped):
-// lanes own 4 columns; returns the score of row c0 + grp + RPL*u in sc[u] on the
-// lanes with col == 0.
-template <int D, int U>
-__device__ __forceinline__ void score_block(const float* qf4, const float* __restrict__ sb,
-                                            int64_t c0, int64_t C, int grp, float* sc) {
-  constexpr int LPR = D / 4;
-  constexpr int RPL = kWave / LPR;
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int64_t c = c0 + grp + RPL * u;
-    float a[4] = {0.f, 0.f, 0.f, 0.f};
-    if (c < C) load16<float>(sb + c * D, a);
-    float d = 0.f;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) d = fmaf(qf4[e], a[e], d);
-    sc[u] = d;
-  }
-#pragma unroll
-  for (int off = LPR / 2; off >= 1; off >>= 1)
-#pragma unroll
-    for (int u = 0; u < U; ++u) sc[u] += xor_lanes(sc[u], off);
-}
-
 }  // namespace csahca

@@ -92,6 +92,9 @@ __global__ __launch_bounds__(kHcaThreads) void hca_chunk_kernel(const T* __restr
       const T* vcp = v + row0 * D + static_cast<int64_t>(vc) * VEC;
       // kRowBatch rows of K and V are requested before any is consumed, so a
       // thread waits for one HBM round trip per batch rather than per row.
+      // The loads are unconditional (rows past the chunk re-read row r0 and
+      // are zeroed after the load): a load under a per-lane branch would make
+      // the compiler wait for the whole batch before issuing it.
       for (int r0 = rg; r0 < chunk; r0 += kRowBatch * R) {
         if constexpr (kVec) {
           uint4 rk[kRowBatch], rv[kRowBatch];
@@ -99,20 +102,22 @@ __global__ __launch_bounds__(kHcaThreads) void hca_chunk_kernel(const T* __restr
           for (int i = 0; i < kRowBatch; ++i) {
             const int r = r0 + i * R;
             const int64_t off = static_cast<int64_t>(r < chunk ? r : r0) * D;
-            rk[i] = *reinterpret_cast<const uint4*>(kc + off);
-            rv[i] = *reinterpret_cast<const uint4*>(vcp + off);
+            rk[i] = load_global_u4(kc + off);
+            rv[i] = load_global_u4(vcp + off);
           }
+          // Keep the scheduler from interleaving the widening below with the
+          // loads (it would wait for the first rows before requesting the rest).
+          __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
           for (int i = 0; i < kRowBatch; ++i) {
-            if (r0 + i * R < chunk) {
-              float xk[VEC], xv[VEC];
-              widen16<T>(rk[i], xk);
-              widen16<T>(rv[i], xv);
+            const bool ok = r0 + i * R < chunk;
+            float xk[VEC], xv[VEC];
+            widen16<T>(rk[i], xk);
+            widen16<T>(rv[i], xv);
 #pragma unroll
-              for (int e = 0; e < VEC; ++e) {
-                ak[e] += xk[e];
-                av[e] += xv[e];
-              }
+            for (int e = 0; e < VEC; ++e) {
+              ak[e] += ok ? xk[e] : 0.f;
+              av[e] += ok ? xv[e] : 0.f;
             }
           }
         } else {
