@@ -238,7 +238,9 @@ def kernel_bytes(name, r):
 
 def cpu_baseline(seconds: float):
     """Time the oracle's decode step (selection from cached summaries + torch-csa
-    attention, bf16-rounded probabilities) on the host on a bounded sample."""
+    attention, bf16-rounded probabilities) on the host on a bounded sample, with
+    up to 8 threads (the value) and with 1; and the attention alone over a
+    precomputed selection (the reference's attend-only torch-csa mode)."""
     import oracle
     from csahca_amd.synthetic import make_synthetic_case
 
@@ -247,19 +249,29 @@ def cpu_baseline(seconds: float):
     nthreads = max(1, min(oracle.ncores(), 8))  # the attention parallelises over the 8 heads
     t = oracle.DecodeStepTimer(case.q, case.k_cache, case.v_cache, summ, 64, 8)
     t.step(nthreads)
-    n = 0
-    t0 = time.perf_counter()
-    while True:
-        t.step(nthreads)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds and n >= 3:
-            break
-    ms = el * 1e3 / n
+
+    def sample(fn, secs):
+        n = 0
+        t0 = time.perf_counter()
+        while True:
+            fn()
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= secs and n >= 3:
+                return el * 1e3 / n, n, el
+
+    ms, n, el = sample(lambda: t.step(nthreads), seconds)
+    side = max(1.0, seconds / 4)
+    ms1, n1, _ = sample(lambda: t.step(1), side)
+    ms_att, n_att, _ = sample(lambda: t.attend(nthreads), side)
     return {"value": round(ms, 5), "unit": "ms/token", "cores": nthreads, "kind": "port",
             "sample": f"{n} decode steps (B1 H8 S32768 D128 chunk64 k8; top-8 selection from cached fp32 "
                       f"summaries + attention over 512 tokens/head) of the C oracle, {el:.1f} s wall, "
-                      f"{nthreads} OpenMP threads on '{cpu_model()}' ({oracle.ncores()} cores visible)"}
+                      f"{nthreads} OpenMP threads on '{cpu_model()}' ({oracle.ncores()} cores visible)",
+            "one_thread_ms_per_token": round(ms1, 5),
+            "attend_only_ms_per_token": round(ms_att, 5),
+            "side_samples": f"{n1} steps on 1 thread; {n_att} attend-only calls (precomputed selection) on "
+                            f"{nthreads} threads; ~{side:.1f} s each"}
 
 
 # ---------------------------------------------------------------------------
@@ -460,8 +472,9 @@ def hca_bench(steps=256, copies=4, hca_chunk=256):
         reps = max(1, steps // copies)
         ms = time_graph_steps(gr, {}, copies, reps * copies) / (reps * copies)
         with native.profile_launches() as prof:
-            for j in range(copies):
-                fn(j)
+            for _ in range(4):
+                for j in range(copies):
+                    fn(j)
         kern = {n: round(v["avg_us"], 3) for n, v in prof.results.items()}
         row = {"ms_per_token": round(ms, 5), "tokens_per_s": round(B / (ms / 1e3), 1), "kernels_avg_us": kern}
         if name == "hca":

@@ -115,6 +115,54 @@ __device__ __forceinline__ void load_row8(const uint8_t* __restrict__ row,
   }
 }
 
+// One slot's share of a lane as raw words, requested unconditionally by every
+// lane (16-byte aligned rows): the 8 nope bytes at 8*lane (for lanes 56..63
+// these are rope bytes 448..511, inside the row), the lane's 16 rope bytes
+// (nope lanes re-read the first rope block) and the tile's scale byte (lanes
+// 56..63 read the slot's pad byte).  The lane's part is selected after the
+// loads, so a batch of slots is one memory round trip.
+struct RawRow8 {
+  uint2 nope;
+  uint4 rope;
+  uint32_t scale;
+};
+
+__device__ __forceinline__ RawRow8 load_raw_row8(const uint8_t* row, const uint8_t* srow, int lane) {
+  const bool nope = lane < kNope / 8;
+  RawRow8 r;
+  r.nope = load_global_u2(row + 8 * lane);
+  r.rope = load_global_u4(row + kNope + 16 * (nope ? 0 : lane - kNope / 8));
+  r.scale = load_global_raw<uint8_t>(srow + (lane >> 3));
+  return r;
+}
+
+__device__ __forceinline__ void decode_raw_row8(const RawRow8& r, int lane, float* kv) {
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  const float s = ue8m0_to_f32(r.scale);
+  const f32x2_t p0 = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(r.nope.x), false);
+  const f32x2_t p1 = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(r.nope.x), true);
+  const f32x2_t p2 = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(r.nope.y), false);
+  const f32x2_t p3 = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(r.nope.y), true);
+  const float fp8v[8] = {p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+  const uint32_t w[4] = {r.rope.x, r.rope.y, r.rope.z, r.rope.w};
+  const bool nope = lane < kNope / 8;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float lo = __uint_as_float(w[i] << 16), hi = __uint_as_float(w[i] & 0xffff0000u);
+    kv[2 * i] = nope ? fp8v[2 * i] * s : lo;
+    kv[2 * i + 1] = nope ? fp8v[2 * i + 1] * s : hi;
+  }
+}
+
+// Eight consecutive elements of T at p (aligned to 8 * sizeof(T)) widened to
+// fp32, through 1, 2 or 4 unconditional 16-byte loads.
+template <typename T>
+__device__ __forceinline__ void load8_f32(const T* p, float* out) {
+  constexpr int N = Vec16<T>::N;
+#pragma unroll
+  for (int i = 0; i < 8 / N; ++i) widen16<T>(load_global_u4(p + N * i), out + N * i);
+}
+
 struct Dsv4Args {
   CacheView swa;
   CacheView extra;
@@ -183,21 +231,38 @@ __global__ __launch_bounds__(64) void dsv4_tile_kernel(const T* __restrict__ q, 
   const int nh = min(kHeadGroup, a.heads - h0);
 
   float qr[kHeadGroup][8];
+  int n_swa, n_extra;
+  if constexpr (kVec) {
+    // One batch: both lengths (a missing list reads q and is dropped) and the
+    // q rows of the group (heads past the last re-read head h0, then zeroed).
+    const int32_t len_raw = load_global_i32(a.lens ? static_cast<const void*>(a.lens + query)
+                                                   : static_cast<const void*>(q));
+    const int32_t elen_raw = load_global_i32(a.elens ? static_cast<const void*>(a.elens + query)
+                                                     : static_cast<const void*>(q));
 #pragma unroll
-  for (int h = 0; h < kHeadGroup; ++h) {
-    if (h < nh) {
-      const T* qp = q + ((query * a.heads) + h0 + h) * kDim + 8 * lane;
+    for (int h = 0; h < kHeadGroup; ++h)
+      load8_f32<T>(q + ((query * a.heads) + h0 + (h < nh ? h : 0)) * kDim + 8 * lane, qr[h]);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) qr[h][e] = to_f32(qp[e]) * a.qscale;
-    } else {
+    for (int h = 0; h < kHeadGroup; ++h)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) qr[h][e] = 0.f;
+      for (int e = 0; e < 8; ++e) qr[h][e] = h < nh ? qr[h][e] * a.qscale : 0.f;
+    n_swa = a.lens ? max(0, min(len_raw, a.topk_slots)) : a.topk_slots;
+    n_extra = a.extra_slots > 0 ? (a.elens ? max(0, min(elen_raw, a.extra_slots)) : a.extra_slots) : 0;
+  } else {
+#pragma unroll
+    for (int h = 0; h < kHeadGroup; ++h) {
+      if (h < nh) {
+        const T* qp = q + ((query * a.heads) + h0 + h) * kDim + 8 * lane;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qr[h][e] = to_f32(qp[e]) * a.qscale;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qr[h][e] = 0.f;
+      }
     }
+    n_swa = a.lens ? max(0, min(a.lens[query], a.topk_slots)) : a.topk_slots;
+    n_extra = a.extra_slots > 0 ? (a.elens ? max(0, min(a.elens[query], a.extra_slots)) : a.extra_slots) : 0;
   }
-
-  const int n_swa = a.lens ? max(0, min(a.lens[query], a.topk_slots)) : a.topk_slots;
-  const int n_extra =
-      a.extra_slots > 0 ? (a.elens ? max(0, min(a.elens[query], a.extra_slots)) : a.extra_slots) : 0;
   const int total = a.topk_slots + a.extra_slots;
   const int s0 = t * a.tile;
   const int s1 = min(s0 + a.tile, total);
@@ -216,7 +281,20 @@ __global__ __launch_bounds__(64) void dsv4_tile_kernel(const T* __restrict__ q, 
     const int s = g + lane;
     const uint8_t* rp = nullptr;
     const uint8_t* sp = nullptr;
-    if (s < s1) {
+    if constexpr (kVec) {
+      // The slot's index is requested unconditionally (lanes past the tile
+      // re-read its last slot) and the slot dropped after the load.
+      const int sc = s < s1 ? s : s1 - 1;
+      const bool in_swa = sc < a.topk_slots;
+      const int32_t* ip = in_swa ? a.idx + query * a.topk_slots + sc
+                                 : a.eidx + query * a.extra_slots + (sc - a.topk_slots);
+      const int32_t loc = load_global_i32(ip);
+      const bool live = s < s1 && (in_swa ? s < n_swa : s - a.topk_slots < n_extra);
+      const uint8_t* sp_c = nullptr;
+      const uint8_t* rp_c = row_ptr(in_swa ? a.swa : a.extra, loc, &sp_c);
+      rp = live ? rp_c : nullptr;
+      sp = live ? sp_c : nullptr;
+    } else if (s < s1) {
       if (s < a.topk_slots) {
         if (s < n_swa) rp = row_ptr(a.swa, a.idx[query * a.topk_slots + s], &sp);
       } else {
@@ -237,11 +315,26 @@ __global__ __launch_bounds__(64) void dsv4_tile_kernel(const T* __restrict__ q, 
       const uint32_t ok = static_cast<uint32_t>(valid >> b) & ((1u << kSlotBatch) - 1u);
       if (ok == 0u) continue;
       float kv[kSlotBatch][8];
+      if constexpr (kVec) {
+        RawRow8 raw[kSlotBatch];
 #pragma unroll
-      for (int j = 0; j < kSlotBatch; ++j) {
-        const uint8_t* row = reinterpret_cast<const uint8_t*>(readlane64(r_lane, b + j));
-        const uint8_t* srow = reinterpret_cast<const uint8_t*>(readlane64(s_lane, b + j));
-        load_row8<kVec>(row, srow, lane, kv[j]);
+        for (int j = 0; j < kSlotBatch; ++j) {
+          const uint8_t* row = reinterpret_cast<const uint8_t*>(readlane64(r_lane, b + j));
+          const uint8_t* srow = reinterpret_cast<const uint8_t*>(readlane64(s_lane, b + j));
+          raw[j] = load_raw_row8(row, srow, lane);
+        }
+        // No decoding is scheduled between the loads (it would wait for the
+        // first slot before the others are requested).
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < kSlotBatch; ++j) decode_raw_row8(raw[j], lane, kv[j]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < kSlotBatch; ++j) {
+          const uint8_t* row = reinterpret_cast<const uint8_t*>(readlane64(r_lane, b + j));
+          const uint8_t* srow = reinterpret_cast<const uint8_t*>(readlane64(s_lane, b + j));
+          load_row8<kVec>(row, srow, lane, kv[j]);
+        }
       }
       float part[kSlotBatch * kHeadGroup];
 #pragma unroll
@@ -900,7 +993,8 @@ int dsv4_run(const Dsv4Call& c) {
   return dispatch_dtype(c.dtype, [&](auto tag) -> int {
     using T = decltype(tag);
     const T* qp = static_cast<const T*>(c.q);
-    const int rc = vec ? launch("dsv4_tile_kernel", dsv4_tile_kernel<T, true>, grid, dim3(kWave), 0,
+    const bool tvec = vec && reinterpret_cast<uintptr_t>(c.q) % 16 == 0;
+    const int rc = tvec ? launch("dsv4_tile_kernel", dsv4_tile_kernel<T, true>, grid, dim3(kWave), 0,
                                 stream, qp, a)
                        : launch("dsv4_tile_kernel", dsv4_tile_kernel<T, false>, grid, dim3(kWave), 0,
                                 stream, qp, a);

@@ -252,6 +252,14 @@ class DecodeStepTimer:
                                   _ptr(self.idx64, _c_i64p), _ptr(self.out, _c_f64p), nthreads)
         return self.out
 
+    def attend(self, nthreads: int = 1) -> np.ndarray:
+        """torch-csa attention alone over the selection of the last step() (the
+        reference's attend-only mode with precomputed chunk ids)."""
+        lib().orc_csa_attend(_ptr(self.q, _c_f32p), _ptr(self.k, _c_f32p), _ptr(self.v, _c_f32p),
+                             _ptr(self.idx64, _c_i64p), self.B, self.H, self.S, self.D, self.idx64.shape[-1],
+                             self.chunk, self.prob_dtype, _ptr(self.out, _c_f64p), nthreads)
+        return self.out
+
 
 # --------------------------------------------------------------------------
 # DSV4 (hybrid_attention/dsv4_correctness.py, csrc/dsv4_attention.cu)
