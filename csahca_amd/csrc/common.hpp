@@ -10,6 +10,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "csahca.h"
 
 namespace csahca {
@@ -157,6 +159,16 @@ __device__ __forceinline__ uint2 load_global_u2(const void* p) {
 __device__ __forceinline__ uint4 load_global_u4(const void* p) {
   const u32x4_t v = load_global_raw<u32x4_t>(p);
   return make_uint4(v[0], v[1], v[2], v[3]);
+}
+// One element of a storage type (2, 4 or 8 bytes), through an integer load.
+template <typename T>
+__device__ __forceinline__ T load_global_elem(const T* p) {
+  using U = std::conditional_t<sizeof(T) == 2, uint16_t, std::conditional_t<sizeof(T) == 4, uint32_t, uint64_t>>;
+  static_assert(sizeof(T) == sizeof(U), "2, 4 or 8 byte storage types");
+  const U u = load_global_raw<U>(p);
+  T t;
+  __builtin_memcpy(&t, &u, sizeof(T));
+  return t;
 }
 
 // Four consecutive elements of T at p (aligned to 4 * sizeof(T)) widened to

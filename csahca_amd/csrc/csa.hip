@@ -77,7 +77,8 @@ __global__ __launch_bounds__(64) void csa_attend_vec_kernel(
 }
 
 // Generic path: any D <= 64 * J, any storage type.  Lanes stride the columns
-// (coalesced), one row per iteration, wavefront-wide dot reduction.
+// (coalesced), kGenericRows rows per iteration, wavefront-wide dot reductions.
+constexpr int kGenericRows = 4;
 template <typename T, typename IdxT, int J>
 __global__ __launch_bounds__(64) void csa_attend_generic_kernel(
     const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
@@ -89,10 +90,16 @@ __global__ __launch_bounds__(64) void csa_attend_generic_kernel(
   const int t = static_cast<int>(item % num_tiles);
   const int64_t bh = item / num_tiles;
   float qf[J], acc[J];
+  T qr[J];
 #pragma unroll
   for (int j = 0; j < J; ++j) {
     const int d = lane + kWave * j;
-    qf[j] = d < D ? to_f32(q[bh * D + d]) * qscale : 0.f;
+    qr[j] = load_global_elem<T>(q + bh * D + (d < D ? d : 0));  // one batch; columns past D dropped
+  }
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const int d = lane + kWave * j;
+    qf[j] = d < D ? to_f32(qr[j]) * qscale : 0.f;
     acc[j] = 0.f;
   }
   const T* __restrict__ kb = k + bh * seq_len * D;
@@ -103,27 +110,69 @@ __global__ __launch_bounds__(64) void csa_attend_generic_kernel(
   const int s0 = t * tile;
   const int s1 = min(s0 + tile, total);
   float m = -INFINITY, l = 0.f;
-  for (int s = s0; s < s1; ++s) {
-    int64_t tok;
-    if (!slot_token_of(get_id, s, chunk, chunk_shift, seq_len, tok)) continue;
-    const T* kr = kb + tok * D;
-    const T* vr = vb + tok * D;
-    float dot = 0.f;
+  // kGenericRows slots per batch: their chunk ids, then their K and V rows,
+  // are each requested unconditionally as one batch (slots past the tile
+  // re-read its last slot, skipped slots and columns past D re-read row 0 /
+  // column 0; all are dropped after the loads).
+  for (int s = s0; s < s1; s += kGenericRows) {
+    int64_t toks[kGenericRows];
+    bool ok[kGenericRows];
 #pragma unroll
-    for (int j = 0; j < J; ++j) {
-      const int d = lane + kWave * j;
-      if (d < D) dot = fmaf(qf[j], to_f32(kr[d]), dot);
+    for (int u = 0; u < kGenericRows; ++u) {
+      int64_t tk = 0;
+      const bool found = slot_token_of(get_id, s + u < s1 ? s + u : s1 - 1, chunk, chunk_shift, seq_len, tk);
+      ok[u] = s + u < s1 && found;
+      toks[u] = ok[u] ? tk : 0;
     }
-    dot = wave_sum(dot);
-    const float m_new = fmaxf(m, dot);
+#pragma unroll
+    for (int u = 0; u < kGenericRows; ++u) asm volatile("" : "+v"(toks[u]));
+    T kr[kGenericRows][J], vr[kGenericRows][J];
+#pragma unroll
+    for (int u = 0; u < kGenericRows; ++u)
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        const int d = lane + kWave * j;
+        const int64_t off = toks[u] * D + (d < D ? d : 0);
+        kr[u][j] = load_global_elem<T>(kb + off);
+        vr[u][j] = load_global_elem<T>(vb + off);
+      }
+    __builtin_amdgcn_sched_barrier(0);
+    float sc[kGenericRows];
+#pragma unroll
+    for (int u = 0; u < kGenericRows; ++u) {
+      float dot = 0.f;
+#pragma unroll
+      for (int j = 0; j < J; ++j)
+        if (lane + kWave * j < D) dot = fmaf(qf[j], to_f32(kr[u][j]), dot);
+      sc[u] = dot;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1)
+#pragma unroll
+      for (int u = 0; u < kGenericRows; ++u) sc[u] += xor_lanes(sc[u], off);
+    float mb = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < kGenericRows; ++u) {
+      sc[u] = ok[u] ? sc[u] : -INFINITY;
+      mb = fmaxf(mb, sc[u]);
+    }
+    if (mb == -INFINITY) continue;  // no live slot in the batch (uniform)
+    const float m_new = fmaxf(m, mb);
     const float alpha = fast_exp2(m - m_new);
-    const float pr = fast_exp2(dot - m_new);
-    l = l * alpha + pr;
+    float pr[kGenericRows];
+    float psum = 0.f;
+#pragma unroll
+    for (int u = 0; u < kGenericRows; ++u) {
+      pr[u] = fast_exp2(sc[u] - m_new);
+      psum += pr[u];
+    }
+    l = l * alpha + psum;
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-      const int d = lane + kWave * j;
-      const float vv = d < D ? to_f32(vr[d]) : 0.f;
-      acc[j] = fmaf(pr, vv, acc[j] * alpha);
+      float x = acc[j] * alpha;
+#pragma unroll
+      for (int u = 0; u < kGenericRows; ++u) x = fmaf(pr[u], lane + kWave * j < D ? to_f32(vr[u][j]) : 0.f, x);
+      acc[j] = x;
     }
     m = m_new;
   }
