@@ -502,7 +502,8 @@ def block_bench(steps=200, warmup=20):
     and from summaries rebuilt every step as the reference does), eager and as
     one HIP graph per step.  Hybrid block (RMSNorm/QKV/SiLU MLP, growing
     cache): eager, and as one HIP graph per step whose replays advance the
-    cache (position and chunk count live on the device)."""
+    cache (position and chunk count live on the device); with the library's
+    fused decode-step products, and with torch's products for comparison."""
     import torch
 
     from csahca_amd import native
@@ -556,9 +557,9 @@ def block_bench(steps=200, warmup=20):
             out[f"mini_mlp{mlp:g}_{mode}"] = row
             log(f"block mini mlp{mlp:g} {mode}: {row}")
             del gr
-    for mlp in (2.0, 0.0):
+    for mlp, fused in ((2.0, True), (0.0, True), (2.0, False), (0.0, False)):
         hb = HybridDecodeBlock(batch=B, heads=H, head_dim=D, capacity=S + 2 * (warmup + steps) + 1, chunk_size=chunk,
-                               top_k=k, mlp_ratio=mlp, device=dev, seed=0)
+                               top_k=k, mlp_ratio=mlp, device=dev, seed=0, fused=fused)
         hb.prefill(kc, vc)
         hbuf = hidden0.clone()
 
@@ -579,8 +580,9 @@ def block_bench(steps=200, warmup=20):
         ms_graph = timed(one_g, steps)
         row = {"ms_per_token_eager": round(ms, 5), "ms_per_token_graph": round(ms_graph, 5),
                "tokens_per_s_graph": round(B / (ms_graph / 1e3), 1), "final_length": hb.length}
-        out[f"baseline_block_mlp{mlp:g}_growing_cache"] = row
-        log(f"block baseline mlp{mlp:g}: {row}")
+        name = f"baseline_block_mlp{mlp:g}_growing_cache" + ("" if fused else "_torch_products")
+        out[name] = row
+        log(f"block {name}: {row}")
         del hb, replay
     del kc, vc, summ
     torch.cuda.synchronize()

@@ -19,9 +19,14 @@ Two blocks:
   projection -> the new token's K/V appended to a growing cache -> the chunk
   summary of a chunk that just completed -> CSA over the complete chunks (fused
   step) -> out projection -> residual -> RMSNorm -> SiLU MLP -> residual.
+  Where the shapes allow (bf16/f16, batch <= 4, 16-byte aligned rows) its
+  products run as the library's decode-step GEMV kernels with the norms, the
+  cache append, the activation and the residuals fused in: five or six
+  launches per step.  Otherwise, or with ``fused=False``, the products are
+  torch's.
 
-Matrix products use torch (the vendor BLAS); the attention path is the HIP
-library, which raises if it is not built.
+The mini block's products use torch (the vendor BLAS); the attention path is
+the HIP library, which raises if it is not built.
 """
 from __future__ import annotations
 
@@ -108,7 +113,7 @@ class HybridDecodeBlock:
 
     def __init__(self, *, batch: int, heads: int, head_dim: int, capacity: int, chunk_size: int = 64,
                  top_k: int = 8, mlp_ratio: float = 2.0, dtype=torch.bfloat16, device="cuda", seed: int = 0,
-                 init_std: float = 0.02):
+                 init_std: float = 0.02, fused: bool | None = None):
         self.batch, self.heads, self.head_dim = batch, heads, head_dim
         self.hidden_dim = heads * head_dim
         self.chunk_size, self.top_k = chunk_size, top_k
@@ -133,7 +138,15 @@ class HybridDecodeBlock:
         self.attn = torch.empty(batch, heads, head_dim, dtype=dtype, device=device)
         self.indices = torch.empty(batch, heads, min(top_k, capacity // chunk_size), dtype=torch.int32,
                                    device=device)
+        self.q = torch.empty(batch, heads, head_dim, dtype=dtype, device=device)
         self.length = 0
+        widest = max(self.hidden_dim, mlp_dim)
+        can_fuse = (dtype in (torch.bfloat16, torch.float16) and 0 < batch <= 4 and self.hidden_dim % 8 == 0
+                    and mlp_dim % 8 == 0 and widest <= (4096 if batch == 1 else 2048))
+        if fused and not can_fuse:
+            raise ValueError("the fused decode step needs bf16/f16, batch <= 4 and feature sizes "
+                             "that are multiples of 8 (at most 4096, or 2048 for batch > 1)")
+        self.fused = can_fuse if fused is None else bool(fused)
 
     @property
     def summary(self) -> torch.Tensor:
@@ -155,6 +168,29 @@ class HybridDecodeBlock:
         self.nchunks.fill_(C)
 
     def _step(self, hidden: torch.Tensor) -> torch.Tensor:
+        return self._step_fused(hidden) if self.fused else self._step_torch(hidden)
+
+    def _step_fused(self, hidden: torch.Tensor) -> torch.Tensor:
+        """The step as library kernels: RMSNorm + QKV + cache append (and the
+        complete-chunk count), the summary of a completed chunk, the CSA step,
+        out projection + residual, then RMSNorm + up projection + SiLU and down
+        projection + residual; the last one advances the position."""
+        B, D = self.batch, self.hidden_dim
+        if not hidden.is_contiguous() or hidden.data_ptr() % 16:
+            hidden = hidden.contiguous().clone()
+        native.block_qkv(hidden, self.w_qkv, self.q, self.k_cache, self.v_cache, self.pos, norm_weight=self.norm1,
+                         num_chunks=self.nchunks, chunk_size=self.chunk_size)
+        native.csa_chunk_summary_at(self.k_cache, self.summary_buf, self.chunk_size, self.pos)
+        native.csa_decode_step_dev(self.q, self.k_cache, self.v_cache, self.summary_buf, self.nchunks,
+                                   self.chunk_size, self.top_k, out=self.attn, indices=self.indices)
+        h = native.block_linear(self.attn.view(B, D), self.w_out, residual=hidden,
+                                advance_pos=None if self.use_mlp else self.pos)
+        if self.use_mlp:
+            u = native.block_linear(h, self.w_up, norm_weight=self.norm2, activation="silu")
+            h = native.block_linear(u, self.w_down, residual=h, advance_pos=self.pos)
+        return h
+
+    def _step_torch(self, hidden: torch.Tensor) -> torch.Tensor:
         B, H, D = self.batch, self.heads, self.head_dim
         x = rms_norm(hidden, self.norm1)
         qkv = F.linear(x, self.w_qkv).view(B, 3, H, D)

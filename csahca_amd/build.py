@@ -21,7 +21,7 @@ BUILD = PKG / "_build"
 LIB = PKG / "libcsahca.so"
 ARCH = os.environ.get("CSAHCA_OFFLOAD_ARCH", "gfx950")
 
-SOURCES = ["status.cpp", "csa.hip", "csa_step.hip", "dsv4.hip", "dsv4_pack.hip", "hca.hip"]
+SOURCES = ["status.cpp", "csa.hip", "csa_step.hip", "dsv4.hip", "dsv4_pack.hip", "hca.hip", "block.hip"]
 
 COMMON_FLAGS = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",

@@ -63,6 +63,8 @@ _SIGNATURES = {
     "csahca_hca_decode_workspace_bytes": (_sz, [_i64] * 5),
     "csahca_dsv4_pack_tokens": (_int, [_vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp]),
     "csahca_hca_decode_forward": (_int, [_vp, _vp, _vp, _vp, _dbl, _vp, _int] + [_i64] * 5 + [_vp, _sz, _vp]),
+    "csahca_block_linear": (_int, [_vp, _vp, _dbl, _vp, _vp, _int, _vp, _int, _i64, _i64, _i64, _vp, _vp]),
+    "csahca_block_qkv": (_int, [_vp, _vp, _dbl, _vp, _vp, _vp, _vp, _vp, _vp, _int] + [_i64] * 5 + [_vp]),
     "csahca_profile_begin": (_int, []),
     "csahca_profile_end": (_int, []),
     "csahca_profile_result": (_int, [_int, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_i64),
@@ -354,6 +356,82 @@ def csa_decode_step_dev(q, k_cache, v_cache, summary, num_chunks, chunk_size, to
                                              _ptr(out), _ptr(indices), _DTYPES[q.dtype], B, H, S, D, Cs, chunk_size,
                                              top_k, _ptr(ws), ws.numel(), _stream()))
     return out, indices
+
+
+_ACTIVATIONS = {None: 0, "silu": 1}
+_BLOCK_DTYPES = (torch.bfloat16, torch.float16)
+
+
+def block_linear_supported(x: torch.Tensor, weight: torch.Tensor) -> bool:
+    """Shapes and types block_linear takes (others use torch's linear)."""
+    B, K = x.shape
+    return (x.is_cuda and x.dtype in _BLOCK_DTYPES and weight.dtype == x.dtype and x.is_contiguous()
+            and weight.is_contiguous() and 0 < B <= 4 and K % 8 == 0 and K <= (4096 if B == 1 else 2048)
+            and x.data_ptr() % 16 == 0 and weight.data_ptr() % 16 == 0)
+
+
+def block_linear(x, weight, *, norm_weight=None, eps: float = 1e-6, residual=None, activation=None, out=None,
+                 advance_pos=None):
+    """Decode-step product ``act(x' @ weight.T) (+ residual)`` for x [batch <= 4,
+    in_features] (bf16/f16), rounded like the torch ops it replaces: x' = x or
+    RMSNorm(x; norm_weight, eps); activation None or "silu"; residual
+    [batch, out_features].  ``advance_pos`` (int64 CUDA tensor) is incremented
+    by one after the product.  Returns ``out`` [batch, out_features]."""
+    _check(x.is_cuda and weight.is_cuda, "x and weight must be CUDA tensors")
+    _check(x.dim() == 2 and weight.dim() == 2 and weight.shape[1] == x.shape[1],
+           "x must be [batch, in_features] and weight [out_features, in_features]")
+    _check(x.dtype in _BLOCK_DTYPES and weight.dtype == x.dtype, "x and weight must both be bfloat16 or float16")
+    _check(x.is_contiguous() and weight.is_contiguous(), "x and weight must be contiguous")
+    _check(activation in _ACTIVATIONS, "activation must be None or 'silu'")
+    B, K = x.shape
+    N = weight.shape[0]
+    if norm_weight is not None:
+        _check(norm_weight.is_cuda and norm_weight.dtype == x.dtype and norm_weight.is_contiguous()
+               and norm_weight.numel() == K, "norm_weight must be a contiguous [in_features] tensor of x's dtype")
+    if residual is not None:
+        _check(residual.is_cuda and residual.dtype == x.dtype and residual.is_contiguous()
+               and tuple(residual.shape) == (B, N), "residual must be a contiguous [batch, out_features] tensor")
+    if advance_pos is not None:
+        _check(advance_pos.is_cuda and advance_pos.dtype == torch.int64 and advance_pos.numel() == 1,
+               "advance_pos must be a one-element int64 CUDA tensor")
+    with torch.cuda.device(x.device):
+        if out is None:
+            out = torch.empty((B, N), dtype=x.dtype, device=x.device)
+        _check(out.dtype == x.dtype and out.is_contiguous() and tuple(out.shape) == (B, N),
+               "out must be a contiguous [batch, out_features] tensor of x's dtype")
+        _rc(lib().csahca_block_linear(_ptr(x), _ptr(norm_weight), float(eps), _ptr(weight), _ptr(residual),
+                                      _ACTIVATIONS[activation], _ptr(out), _DTYPES[x.dtype], B, N, K,
+                                      _ptr(advance_pos), _stream()))
+    return out
+
+
+def block_qkv(hidden, w_qkv, q, k_cache, v_cache, token_pos, *, norm_weight=None, eps: float = 1e-6,
+              num_chunks=None, chunk_size: int = 64):
+    """QKV projection of a decode step over a growing cache: RMSNorm(hidden)
+    @ w_qkv.T split into q (written to ``q`` [batch, H, D]) and the new token's
+    K and V (written to row ``token_pos`` of ``k_cache`` / ``v_cache``
+    [batch, H, capacity, D]); ``num_chunks`` (int32, optional) receives
+    (token_pos + 1) // chunk_size.  Positions are read on the device."""
+    _check(all(t.is_cuda for t in (hidden, w_qkv, q, k_cache, v_cache, token_pos)), "all tensors must be CUDA tensors")
+    _check(hidden.dtype in _BLOCK_DTYPES and all(t.dtype == hidden.dtype for t in (w_qkv, q, k_cache, v_cache)),
+           "hidden, w_qkv, q and the caches must share a bfloat16 or float16 dtype")
+    _check(all(t.is_contiguous() for t in (hidden, w_qkv, q, k_cache, v_cache)), "tensors must be contiguous")
+    _check(k_cache.dim() == 4 and k_cache.shape == v_cache.shape, "caches must be [batch, heads, capacity, head_dim]")
+    B, H, cap, D = k_cache.shape
+    _check(tuple(hidden.shape) == (B, H * D) and tuple(w_qkv.shape) == (3 * H * D, H * D)
+           and tuple(q.shape) == (B, H, D), "hidden [batch, H*D], w_qkv [3*H*D, H*D], q [batch, H, D]")
+    _check(token_pos.dtype == torch.int64 and token_pos.numel() == 1, "token_pos must be a one-element int64 tensor")
+    if num_chunks is not None:
+        _check(num_chunks.is_cuda and num_chunks.dtype == torch.int32 and num_chunks.numel() == 1,
+               "num_chunks must be a one-element int32 CUDA tensor")
+    if norm_weight is not None:
+        _check(norm_weight.is_cuda and norm_weight.dtype == hidden.dtype and norm_weight.numel() == H * D,
+               "norm_weight must be a [H*D] tensor of hidden's dtype")
+    with torch.cuda.device(hidden.device):
+        _rc(lib().csahca_block_qkv(_ptr(hidden), _ptr(norm_weight), float(eps), _ptr(w_qkv), _ptr(q), _ptr(k_cache),
+                                   _ptr(v_cache), _ptr(token_pos), _ptr(num_chunks), _DTYPES[hidden.dtype], B, H, D,
+                                   cap, int(chunk_size), _stream()))
+    return q
 
 
 def csa_step_status(device=None) -> dict:

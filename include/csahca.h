@@ -248,6 +248,39 @@ int csahca_dsv4_pack_tokens(const void* k_tokens, const int32_t* locs, int64_t n
 /* Launch profiler (measurement aid; no counterpart in the reference)         */
 /* ------------------------------------------------------------------------- */
 
+/* ------------------------------------------------------------------------- */
+/* Decode-block products (no reference counterpart: the reference's decode     */
+/* blocks call torch's nn.Linear, hybrid_attention/model_inference.py:14-76;   */
+/* these replace those calls and the elementwise ops around them in            */
+/* csahca_amd.block).  W is [out_features, in_features] (nn.Linear layout),    */
+/* rows of x are [batch, in_features], batch <= 4, in_features a multiple of 8 */
+/* and <= 4096 (<= 2048 for batch > 1), bfloat16 or float16, x / W /           */
+/* norm_weight 16-byte aligned.                                                */
+/* ------------------------------------------------------------------------- */
+
+enum csahca_activation { CSAHCA_ACT_NONE = 0, CSAHCA_ACT_SILU = 1 };
+
+/* y = act(x' W^T) (+ residual), each step rounded to the storage type as the
+ * torch ops it replaces round: x' = x, or with norm_weight the RMSNorm
+ * x * rsqrt(mean(x^2) + eps) * norm_weight; then the product; then SiLU
+ * (activation), or + residual ([batch, out_features]; not with an
+ * activation).  With advance_pos, *advance_pos (int64, device) is incremented
+ * by one after the product (the last kernel of a decode step). */
+int csahca_block_linear(const void* x, const void* norm_weight, double eps, const void* weight,
+                        const void* residual, int activation, void* y, int dtype, int64_t batch,
+                        int64_t out_features, int64_t in_features, int64_t* advance_pos, void* stream);
+
+/* The QKV projection of a decode step over a growing cache: with
+ * hidden [batch, H*D], qkv = RMSNorm(hidden) w_qkv^T ([batch, 3, H, D] order)
+ * goes to q [batch, H, D] and, at position p = *token_pos (int64, device), to
+ * k_cache / v_cache [batch, H, capacity, D] row p (no K/V row is written when p
+ * lies outside [0, capacity)); *num_chunks (int32, device, optional) is set to
+ * (p + 1) / chunk_size, the complete chunks once the token is in. */
+int csahca_block_qkv(const void* hidden, const void* norm_weight, double eps, const void* w_qkv, void* q,
+                     void* k_cache, void* v_cache, const int64_t* token_pos, int32_t* num_chunks, int dtype,
+                     int64_t batch, int64_t heads, int64_t head_dim, int64_t capacity, int64_t chunk_size,
+                     void* stream);
+
 /* Between begin and end, every kernel this thread launches through the library
  * carries a start/stop HIP event pair (hipExtLaunchKernel), which timestamps the
  * dispatch itself -- the same interval a kernel trace reports.  end waits for

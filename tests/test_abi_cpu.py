@@ -129,6 +129,42 @@ def test_device_state_entry_points_argument_errors(lib):
     assert summ_at(C=0) == 0  # no summary rows: nothing to write
 
 
+def test_block_product_argument_errors(lib):
+    """csahca_block_linear / csahca_block_qkv reject bad arguments before any
+    HIP call (dummy pointers are never dereferenced)."""
+    def lin(**o):
+        a = dict(x=16, norm=None, eps=1e-6, w=16, res=None, act=0, y=16, dtype=2, B=1, N=8, K=64, adv=None)
+        a.update(o)
+        return lib.csahca_block_linear(a["x"], a["norm"], a["eps"], a["w"], a["res"], a["act"], a["y"], a["dtype"],
+                                       a["B"], a["N"], a["K"], a["adv"], None)
+
+    assert lin(dtype=0) == 1 and "bfloat16 and float16" in lib.csahca_last_error().decode()
+    assert lin(B=5) == 1 and "at most 4 token rows" in lib.csahca_last_error().decode()
+    assert lin(K=12) == 1 and "multiple of 8" in lib.csahca_last_error().decode()
+    assert lin(K=4104) == 1
+    assert lin(B=2, K=4096) == 1 and "needs batch 1" in lib.csahca_last_error().decode()
+    assert lin(act=7) == 1 and lib.csahca_last_error().decode() == "unknown activation"
+    assert lin(res=16, act=1) == 1 and "cannot be combined" in lib.csahca_last_error().decode()
+    assert lin(x=8) == 1 and "16-byte aligned" in lib.csahca_last_error().decode()
+    assert lin(w=None) == 1 and lib.csahca_last_error().decode() == "null tensor pointer"
+    assert lin(B=0) == 0 and lin(N=0) == 0  # empty products: nothing to do
+    assert lin(B=0, adv=16) == 1 and "non-empty product" in lib.csahca_last_error().decode()
+    assert lin(K=0) == 1 and lib.csahca_last_error().decode() == "in_features must be positive"
+
+    def qkv(**o):
+        a = dict(h=16, norm=None, eps=1e-6, w=16, q=16, k=16, v=16, pos=16, nch=None, dtype=2, B=1, H=2, D=64,
+                 cap=128, chunk=64)
+        a.update(o)
+        return lib.csahca_block_qkv(a["h"], a["norm"], a["eps"], a["w"], a["q"], a["k"], a["v"], a["pos"], a["nch"],
+                                    a["dtype"], a["B"], a["H"], a["D"], a["cap"], a["chunk"], None)
+
+    assert qkv(pos=None) == 1 and lib.csahca_last_error().decode() == "null token_pos pointer"
+    assert qkv(chunk=0) == 1 and lib.csahca_last_error().decode() == "chunk_size must be positive"
+    assert qkv(D=61) == 1 and "multiple of 8" in lib.csahca_last_error().decode()  # H*D = 122
+    assert qkv(dtype=3) == 1
+    assert qkv(B=0) == 0
+
+
 def test_binding_rejects_cpu_tensors_with_reference_messages(lib):
     q = torch.zeros(1, 2, 64, dtype=torch.bfloat16)
     k = torch.zeros(1, 2, 128, 64, dtype=torch.bfloat16)

@@ -119,11 +119,13 @@ def cpu_hybrid_reference(blk: HybridDecodeBlock, k0, v0, hiddens):
     return outs
 
 
+@pytest.mark.parametrize("fused", [True, False])
 @pytest.mark.parametrize("mlp_ratio", [0.0, 2.0])
-def test_hybrid_block_steps_match_cpu_across_a_chunk_boundary(mlp_ratio):
+def test_hybrid_block_steps_match_cpu_across_a_chunk_boundary(mlp_ratio, fused):
     B, H, D, S0, steps = 1, 4, 64, 250, 10  # the 256th token completes chunk 4 during the run
     blk = HybridDecodeBlock(batch=B, heads=H, head_dim=D, capacity=512, chunk_size=64, top_k=3, mlp_ratio=mlp_ratio,
-                            device=DEV, seed=5)
+                            device=DEV, seed=5, fused=fused)
+    assert blk.fused == fused
     g = torch.Generator().manual_seed(9)
     k0 = torch.randn(B, H, S0, D, generator=g).to(BF)
     v0 = torch.randn(B, H, S0, D, generator=g).to(BF)
@@ -138,6 +140,29 @@ def test_hybrid_block_steps_match_cpu_across_a_chunk_boundary(mlp_ratio):
     # the summary of the chunk completed during decoding equals a fresh build
     fresh = native.csa_chunk_summary(blk.k_cache[:, :, :256].contiguous(), 64)
     torch.testing.assert_close(blk.summary, fresh, rtol=0, atol=0)
+
+
+def test_fused_hybrid_block_batch_two_matches_cpu():
+    B, H, D, S0, steps = 2, 8, 128, 190, 4  # the 192nd token completes chunk 2
+    blk = HybridDecodeBlock(batch=B, heads=H, head_dim=D, capacity=256, chunk_size=64, top_k=2, mlp_ratio=2.0,
+                            device=DEV, seed=11)
+    assert blk.fused
+    g = torch.Generator().manual_seed(12)
+    k0 = torch.randn(B, H, S0, D, generator=g).to(BF)
+    v0 = torch.randn(B, H, S0, D, generator=g).to(BF)
+    hiddens = [torch.randn(B, H * D, generator=g).to(BF) for _ in range(steps)]
+    blk.prefill(k0.to(DEV), v0.to(DEV))
+    want = cpu_hybrid_reference(blk, k0, v0, hiddens)
+    for i, hdn in enumerate(hiddens):
+        assert_close(blk(hdn.to(DEV)), want[i], what=f"step {i}")
+    assert int(blk.pos.item()) == S0 + steps and int(blk.nchunks.item()) == (S0 + steps) // 64
+
+
+def test_hybrid_block_rejects_unfusable_shapes_when_asked_to_fuse():
+    with pytest.raises(ValueError, match="fused decode step"):
+        HybridDecodeBlock(batch=5, heads=2, head_dim=64, capacity=128, device=DEV, fused=True)
+    blk = HybridDecodeBlock(batch=5, heads=2, head_dim=64, capacity=128, device=DEV)
+    assert not blk.fused  # automatic choice falls back to torch products
 
 
 # ---------------------------------------------------------------------------
@@ -204,11 +229,12 @@ def test_decode_step_dev_with_fewer_chunks_than_top_k():
     assert torch.equal(idx, full_idx) and torch.equal(got, full)
 
 
+@pytest.mark.parametrize("fused", [True, False])
 @pytest.mark.parametrize("mlp_ratio", [0.0, 2.0])
-def test_hybrid_block_graph_replays_match_eager_steps(mlp_ratio):
+def test_hybrid_block_graph_replays_match_eager_steps(mlp_ratio, fused):
     B, H, D, S0, steps = 1, 4, 64, 1000, 100  # tokens 1024 and 1088 complete chunks 15 and 16
     blocks = [HybridDecodeBlock(batch=B, heads=H, head_dim=D, capacity=1200, chunk_size=64, top_k=4,
-                                mlp_ratio=mlp_ratio, device=DEV, seed=21) for _ in range(2)]
+                                mlp_ratio=mlp_ratio, device=DEV, seed=21, fused=fused) for _ in range(2)]
     g = torch.Generator().manual_seed(22)
     k0 = torch.randn(B, H, S0, D, generator=g).to(BF).to(DEV)
     v0 = torch.randn(B, H, S0, D, generator=g).to(BF).to(DEV)
