@@ -526,14 +526,17 @@ def block_bench(steps=200, warmup=20):
         return (time.perf_counter() - t0) * 1e3 / n
 
     out = {"config": f"B{B} H{H} D{D} S{S} chunk{chunk} top{k} bf16, {steps} steps + {warmup} warm-up"}
-    for mlp in (2.0, 0.0):
-        blk = MiniCSADecodeBlock(heads=H, head_dim=D, dtype=torch.bfloat16, device=dev, mlp_ratio=mlp, seed=0)
+    for mlp, fused in ((2.0, True), (0.0, True), (2.0, False), (0.0, False)):
+        blk = MiniCSADecodeBlock(heads=H, head_dim=D, dtype=torch.bfloat16, device=dev, mlp_ratio=mlp, seed=0,
+                                 fused=fused)
         q0 = torch.nn.functional.linear(hidden0, blk.w_q).view(B, H, D)
         sel = native.csa_select_topk(q0, summ, k)
         modes = {"precomputed": dict(selection="precomputed", selected_chunks=sel),
                  "dynamic_cached_summary": dict(selection="dynamic", summary=summ)}
         if mlp == 0.0:
             modes["dynamic_recomputed_summary"] = dict(selection="dynamic", summary=None)
+        if not fused:
+            modes = {"precomputed": modes["precomputed"]}
         for mode, kw in modes.items():
             hbuf = hidden0.clone()
 
@@ -554,8 +557,9 @@ def block_bench(steps=200, warmup=20):
             ms_graph = timed(gr.replay, steps)
             row = {"ms_per_token_eager": round(ms_eager, 5), "ms_per_token_graph": round(ms_graph, 5),
                    "tokens_per_s_graph": round(B / (ms_graph / 1e3), 1)}
-            out[f"mini_mlp{mlp:g}_{mode}"] = row
-            log(f"block mini mlp{mlp:g} {mode}: {row}")
+            name = f"mini_mlp{mlp:g}_{mode}" + ("" if fused else "_torch_products")
+            out[name] = row
+            log(f"block {name}: {row}")
             del gr
     for mlp, fused in ((2.0, True), (0.0, True), (2.0, False), (0.0, False)):
         hb = HybridDecodeBlock(batch=B, heads=H, head_dim=D, capacity=S + 2 * (warmup + steps) + 1, chunk_size=chunk,

@@ -25,8 +25,9 @@ Two blocks:
   launches per step.  Otherwise, or with ``fused=False``, the products are
   torch's.
 
-The mini block's products use torch (the vendor BLAS); the attention path is
-the HIP library, which raises if it is not built.
+The mini block likewise runs its products (q, out, GELU MLP and the
+``hidden + 0.01 * out`` tail) as library kernels where the shapes allow.  The
+attention path is always the HIP library, which raises if it is not built.
 """
 from __future__ import annotations
 
@@ -52,14 +53,16 @@ class MiniCSADecodeBlock:
     """The reference benchmark block (hybrid_attention/model_inference.py:14-76)."""
 
     def __init__(self, *, heads: int, head_dim: int, dtype: torch.dtype, device, mlp_ratio: float,
-                 seed: int = 0, init_std: float | None = None):
+                 seed: int = 0, init_std: float | None = None, fused: bool | None = None):
         self.heads, self.head_dim = heads, head_dim
         self.hidden_dim = heads * head_dim
+        self.fused = fused  # None: the library's products whenever a call's shapes allow
         g = torch.Generator().manual_seed(seed)
         kw = dict(std=init_std, generator=g, dtype=dtype, device=device)
         self.w_q = _linear_weight(self.hidden_dim, self.hidden_dim, **kw)
         self.w_out = _linear_weight(self.hidden_dim, self.hidden_dim, **kw)
         mlp_dim = int(self.hidden_dim * mlp_ratio)
+        self.mlp_dim = mlp_dim
         self.use_mlp = mlp_dim > 0
         if self.use_mlp:
             self.w_up = _linear_weight(mlp_dim, self.hidden_dim, **kw)
@@ -76,8 +79,23 @@ class MiniCSADecodeBlock:
             return out
         raise ValueError(f"unknown selection: {selection}")
 
+    def can_fuse(self, hidden: torch.Tensor) -> bool:
+        """Whether the library's decode-step products take this call's shapes."""
+        B = hidden.shape[0]
+        widest = max(self.hidden_dim, self.mlp_dim)
+        return (hidden.is_cuda and hidden.dtype in (torch.bfloat16, torch.float16) and self.w_q.dtype == hidden.dtype
+                and 0 < B <= 4 and self.hidden_dim % 8 == 0 and self.mlp_dim % 8 == 0
+                and widest <= (4096 if B == 1 else 2048))
+
     def forward(self, hidden, k_cache, v_cache, *, selection: str = "precomputed", selected_chunks=None,
                 summary=None, chunk_size: int = 64, top_k: int = 8, tile_size: int = 8):
+        fuse = self.can_fuse(hidden) if self.fused is None else self.fused
+        if fuse:
+            if not self.can_fuse(hidden):
+                raise ValueError("the fused block products need bf16/f16, batch <= 4 and feature sizes that are "
+                                 "multiples of 8 (at most 4096, or 2048 for batch > 1)")
+            return self._forward_fused(hidden, k_cache, v_cache, selection=selection, selected_chunks=selected_chunks,
+                                       summary=summary, chunk_size=chunk_size, top_k=top_k, tile_size=tile_size)
         batch = hidden.shape[0]
         q = F.linear(hidden, self.w_q).view(batch, self.heads, self.head_dim)
         attn = self.attention(q, k_cache, v_cache, selection=selection, selected_chunks=selected_chunks,
@@ -86,6 +104,23 @@ class MiniCSADecodeBlock:
         if self.use_mlp:
             out = out + F.linear(F.gelu(F.linear(hidden, self.w_up)), self.w_down)
         return hidden + 0.01 * out
+
+    def _forward_fused(self, hidden, k_cache, v_cache, **attn_kw):
+        """The same block through the library's decode-step products: q
+        projection, attention, out projection, and for the MLP the GELU up
+        projection and the down projection whose epilogue adds the out
+        projection and forms ``hidden + 0.01 * out``: four or two products,
+        each one launch."""
+        B = hidden.shape[0]
+        if not hidden.is_contiguous() or hidden.data_ptr() % 16:
+            hidden = hidden.contiguous().clone()
+        q = native.block_linear(hidden, self.w_q).view(B, self.heads, self.head_dim)
+        attn = self.attention(q, k_cache, v_cache, **attn_kw).reshape(B, self.hidden_dim)
+        if self.use_mlp:
+            out = native.block_linear(attn, self.w_out)
+            u = native.block_linear(hidden, self.w_up, activation="gelu")
+            return native.block_linear(u, self.w_down, residual=out, base=hidden, alpha=0.01)
+        return native.block_linear(attn, self.w_out, base=hidden, alpha=0.01)
 
     __call__ = forward
 

@@ -8,14 +8,15 @@
 // the neighbouring elementwise work fused in:
 //   prologue  optional RMSNorm of the input rows,
 //             x * rsqrt(mean(x^2) + eps) * g rounded to the storage type;
-//   epilogue  the product rounded to the storage type, then one of
-//             store, + residual (rounded), SiLU (rounded), or the QKV
-//             scatter: q to [B,H,D], k and v appended to [B,H,capacity,D]
-//             caches at the device-side position, and the count of complete
-//             chunks after that token;
+//   epilogue  the product rounded to the storage type, then either
+//             an optional activation (SiLU or exact GELU), an optional
+//             + residual and an optional base + alpha * (.), each rounded;
+//             or the QKV scatter: q to [B,H,D], k and v appended to
+//             [B,H,capacity,D] caches at the device-side position, and the
+//             count of complete chunks after that token;
 //             optionally the device position advanced by one.
-// Rounding points follow the torch ops they replace (F.linear output, the
-// bf16 residual add, F.silu on the rounded product).
+// Rounding points follow the torch ops they replace (F.linear output, F.silu /
+// F.gelu of the rounded product, the bf16 residual add, `hidden + 0.01 * out`).
 //
 // Work split: a wavefront owns kRowsPerWave rows of W; lane l owns the
 // 16-byte column chunks l, l + 64, ... of a row, so a row of K values is
@@ -35,15 +36,18 @@ constexpr int kGemvWaves = 4;
 constexpr int kGemvThreads = kGemvWaves * kWave;
 constexpr int kRowsPerWave = 2;
 
-enum GemvEpilogue : int { kEpiStore = 0, kEpiResidual = 1, kEpiSilu = 2, kEpiQkv = 3 };
+enum GemvEpilogue : int { kEpiGeneral = 0, kEpiQkv = 1 };
 
 struct GemvArgs {
   const void* x;      // [B, K]
   const void* norm;   // [K] RMSNorm weight, or null
   float eps;
   const void* w;      // [N, K]
-  const void* res;    // [B, N] residual (kEpiResidual)
-  void* y;            // [B, N] (kEpiStore, kEpiResidual, kEpiSilu)
+  int act;            // CSAHCA_ACT_*
+  const void* res;    // [B, N] residual, or null
+  const void* base;   // [B, N] base of base + alpha * y, or null
+  float alpha;
+  void* y;            // [B, N] (kEpiGeneral)
   // kEpiQkv: N = 3 H D; output n = (part, head, dim) in that order
   void* q;            // [B, H, D]
   void* kc;           // [B, H, capacity, D]
@@ -99,10 +103,12 @@ __global__ __launch_bounds__(kGemvThreads) void block_gemv_kernel(GemvArgs a) {
   const int ob = oi / RW, orow = oi % RW;
   const int on = n0 + orow;
   const bool store = lane < NV && ob < a.B && on < a.N;
-  float resv = 0.f;
-  if constexpr (EPI == kEpiResidual) {
+  float resv = 0.f, basev = 0.f;
+  if constexpr (EPI == kEpiGeneral) {
+    // (absent operands re-read x[0] and are dropped)
     const int64_t ri = static_cast<int64_t>(ob < a.B ? ob : 0) * a.N + (on < a.N ? on : a.N - 1);
-    resv = to_f32(load_global_elem<T>(static_cast<const T*>(a.res) + ri));
+    resv = to_f32(load_global_elem<T>(a.res ? static_cast<const T*>(a.res) + ri : x));
+    basev = to_f32(load_global_elem<T>(a.base ? static_cast<const T*>(a.base) + ri : x));
   }
   int64_t pos = 0;
   if constexpr (EPI == kEpiQkv) pos = load_global_raw<int64_t>(a.pos);
@@ -187,8 +193,10 @@ __global__ __launch_bounds__(kGemvThreads) void block_gemv_kernel(GemvArgs a) {
       *a.nchunks = static_cast<int32_t>((pos + 1) / a.chunk);
   } else {
     float out = y0;
-    if constexpr (EPI == kEpiResidual) out = round_t<T>(y0 + resv);
-    if constexpr (EPI == kEpiSilu) out = round_t<T>(y0 / (1.f + __expf(-y0)));
+    if (a.act == CSAHCA_ACT_SILU) out = round_t<T>(out / (1.f + __expf(-out)));
+    if (a.act == CSAHCA_ACT_GELU) out = round_t<T>(0.5f * out * (1.f + erff(out * 0.70710678118654752f)));
+    if (a.res != nullptr) out = round_t<T>(out + resv);
+    if (a.base != nullptr) out = round_t<T>(basev + round_t<T>(a.alpha * out));
     if (store) static_cast<T*>(a.y)[static_cast<int64_t>(ob) * a.N + on] = from_f32<T>(out);
   }
   if (a.advance != nullptr && blockIdx.x == 0 && threadIdx.x == 0) *a.advance = *a.advance + 1;
@@ -197,12 +205,9 @@ __global__ __launch_bounds__(kGemvThreads) void block_gemv_kernel(GemvArgs a) {
 template <typename T, int KV, int BB>
 int launch_gemv_epi(int epi, const GemvArgs& a, dim3 grid, hipStream_t stream) {
   const dim3 block(kGemvThreads);
-  switch (epi) {
-    case kEpiStore: return launch("block_gemv_kernel", block_gemv_kernel<T, KV, BB, kEpiStore>, grid, block, 0, stream, a);
-    case kEpiResidual: return launch("block_gemv_kernel", block_gemv_kernel<T, KV, BB, kEpiResidual>, grid, block, 0, stream, a);
-    case kEpiSilu: return launch("block_gemv_kernel", block_gemv_kernel<T, KV, BB, kEpiSilu>, grid, block, 0, stream, a);
-    default: return launch("block_gemv_kernel", block_gemv_kernel<T, KV, BB, kEpiQkv>, grid, block, 0, stream, a);
-  }
+  return epi == kEpiQkv
+             ? launch("block_gemv_kernel", block_gemv_kernel<T, KV, BB, kEpiQkv>, grid, block, 0, stream, a)
+             : launch("block_gemv_kernel", block_gemv_kernel<T, KV, BB, kEpiGeneral>, grid, block, 0, stream, a);
 }
 
 template <typename T, int KV>
@@ -246,14 +251,14 @@ int run_gemv(int dtype, int epi, const GemvArgs& a, hipStream_t stream) {
 using namespace csahca;
 
 extern "C" int csahca_block_linear(const void* x, const void* norm_weight, double eps, const void* weight,
-                                   const void* residual, int activation, void* y, int dtype, int64_t batch,
-                                   int64_t out_features, int64_t in_features, int64_t* advance_pos,
-                                   void* stream) {
+                                   int activation, const void* residual, const void* base, double alpha,
+                                   void* y, int dtype, int64_t batch, int64_t out_features,
+                                   int64_t in_features, int64_t* advance_pos, void* stream) {
   clear_error();
   int rc = check_gemv(dtype, batch, out_features, in_features);
   if (rc != CSAHCA_OK) return rc;
-  CSAHCA_REQUIRE(activation == CSAHCA_ACT_NONE || activation == CSAHCA_ACT_SILU, "unknown activation");
-  CSAHCA_REQUIRE(!(residual && activation != CSAHCA_ACT_NONE), "residual and activation cannot be combined");
+  CSAHCA_REQUIRE(activation == CSAHCA_ACT_NONE || activation == CSAHCA_ACT_SILU || activation == CSAHCA_ACT_GELU,
+                 "unknown activation");
   if ((batch == 0 || out_features == 0) && advance_pos == nullptr) return CSAHCA_OK;
   CSAHCA_REQUIRE(in_features > 0, "in_features must be positive");
   CSAHCA_REQUIRE(batch > 0 && out_features > 0, "advancing the position needs a non-empty product");
@@ -265,14 +270,16 @@ extern "C" int csahca_block_linear(const void* x, const void* norm_weight, doubl
   a.norm = norm_weight;
   a.eps = static_cast<float>(eps);
   a.w = weight;
+  a.act = activation;
   a.res = residual;
+  a.base = base;
+  a.alpha = static_cast<float>(alpha);
   a.y = y;
   a.advance = advance_pos;
   a.B = static_cast<int>(batch);
   a.N = static_cast<int>(out_features);
   a.K = static_cast<int>(in_features);
-  const int epi = residual ? kEpiResidual : (activation == CSAHCA_ACT_SILU ? kEpiSilu : kEpiStore);
-  return run_gemv(dtype, epi, a, static_cast<hipStream_t>(stream));
+  return run_gemv(dtype, kEpiGeneral, a, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int csahca_block_qkv(const void* hidden, const void* norm_weight, double eps, const void* w_qkv,

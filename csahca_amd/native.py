@@ -63,7 +63,8 @@ _SIGNATURES = {
     "csahca_hca_decode_workspace_bytes": (_sz, [_i64] * 5),
     "csahca_dsv4_pack_tokens": (_int, [_vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp]),
     "csahca_hca_decode_forward": (_int, [_vp, _vp, _vp, _vp, _dbl, _vp, _int] + [_i64] * 5 + [_vp, _sz, _vp]),
-    "csahca_block_linear": (_int, [_vp, _vp, _dbl, _vp, _vp, _int, _vp, _int, _i64, _i64, _i64, _vp, _vp]),
+    "csahca_block_linear": (_int, [_vp, _vp, _dbl, _vp, _int, _vp, _vp, _dbl, _vp, _int, _i64, _i64, _i64, _vp,
+                                   _vp]),
     "csahca_block_qkv": (_int, [_vp, _vp, _dbl, _vp, _vp, _vp, _vp, _vp, _vp, _int] + [_i64] * 5 + [_vp]),
     "csahca_profile_begin": (_int, []),
     "csahca_profile_end": (_int, []),
@@ -358,7 +359,7 @@ def csa_decode_step_dev(q, k_cache, v_cache, summary, num_chunks, chunk_size, to
     return out, indices
 
 
-_ACTIVATIONS = {None: 0, "silu": 1}
+_ACTIVATIONS = {None: 0, "silu": 1, "gelu": 2}
 _BLOCK_DTYPES = (torch.bfloat16, torch.float16)
 
 
@@ -370,27 +371,29 @@ def block_linear_supported(x: torch.Tensor, weight: torch.Tensor) -> bool:
             and x.data_ptr() % 16 == 0 and weight.data_ptr() % 16 == 0)
 
 
-def block_linear(x, weight, *, norm_weight=None, eps: float = 1e-6, residual=None, activation=None, out=None,
-                 advance_pos=None):
-    """Decode-step product ``act(x' @ weight.T) (+ residual)`` for x [batch <= 4,
-    in_features] (bf16/f16), rounded like the torch ops it replaces: x' = x or
-    RMSNorm(x; norm_weight, eps); activation None or "silu"; residual
-    [batch, out_features].  ``advance_pos`` (int64 CUDA tensor) is incremented
-    by one after the product.  Returns ``out`` [batch, out_features]."""
+def block_linear(x, weight, *, norm_weight=None, eps: float = 1e-6, activation=None, residual=None, base=None,
+                 alpha: float = 1.0, out=None, advance_pos=None):
+    """Decode-step product ``base + alpha * (act(x' @ weight.T) + residual)`` for
+    x [batch <= 4, in_features] (bf16/f16), rounded like the torch ops it
+    replaces: x' = x or RMSNorm(x; norm_weight, eps); activation None, "silu"
+    or "gelu" (exact); residual and base [batch, out_features], each optional.
+    ``advance_pos`` (int64 CUDA tensor) is incremented by one after the
+    product.  Returns ``out`` [batch, out_features]."""
     _check(x.is_cuda and weight.is_cuda, "x and weight must be CUDA tensors")
     _check(x.dim() == 2 and weight.dim() == 2 and weight.shape[1] == x.shape[1],
            "x must be [batch, in_features] and weight [out_features, in_features]")
     _check(x.dtype in _BLOCK_DTYPES and weight.dtype == x.dtype, "x and weight must both be bfloat16 or float16")
     _check(x.is_contiguous() and weight.is_contiguous(), "x and weight must be contiguous")
-    _check(activation in _ACTIVATIONS, "activation must be None or 'silu'")
+    _check(activation in _ACTIVATIONS, "activation must be None, 'silu' or 'gelu'")
     B, K = x.shape
     N = weight.shape[0]
     if norm_weight is not None:
         _check(norm_weight.is_cuda and norm_weight.dtype == x.dtype and norm_weight.is_contiguous()
                and norm_weight.numel() == K, "norm_weight must be a contiguous [in_features] tensor of x's dtype")
-    if residual is not None:
-        _check(residual.is_cuda and residual.dtype == x.dtype and residual.is_contiguous()
-               and tuple(residual.shape) == (B, N), "residual must be a contiguous [batch, out_features] tensor")
+    for name, t in (("residual", residual), ("base", base)):
+        if t is not None:
+            _check(t.is_cuda and t.dtype == x.dtype and t.is_contiguous() and tuple(t.shape) == (B, N),
+                   f"{name} must be a contiguous [batch, out_features] tensor of x's dtype")
     if advance_pos is not None:
         _check(advance_pos.is_cuda and advance_pos.dtype == torch.int64 and advance_pos.numel() == 1,
                "advance_pos must be a one-element int64 CUDA tensor")
@@ -399,9 +402,9 @@ def block_linear(x, weight, *, norm_weight=None, eps: float = 1e-6, residual=Non
             out = torch.empty((B, N), dtype=x.dtype, device=x.device)
         _check(out.dtype == x.dtype and out.is_contiguous() and tuple(out.shape) == (B, N),
                "out must be a contiguous [batch, out_features] tensor of x's dtype")
-        _rc(lib().csahca_block_linear(_ptr(x), _ptr(norm_weight), float(eps), _ptr(weight), _ptr(residual),
-                                      _ACTIVATIONS[activation], _ptr(out), _DTYPES[x.dtype], B, N, K,
-                                      _ptr(advance_pos), _stream()))
+        _rc(lib().csahca_block_linear(_ptr(x), _ptr(norm_weight), float(eps), _ptr(weight), _ACTIVATIONS[activation],
+                                      _ptr(residual), _ptr(base), float(alpha), _ptr(out), _DTYPES[x.dtype], B, N,
+                                      K, _ptr(advance_pos), _stream()))
     return out
 
 

@@ -258,17 +258,20 @@ int csahca_dsv4_pack_tokens(const void* k_tokens, const int32_t* locs, int64_t n
 /* norm_weight 16-byte aligned.                                                */
 /* ------------------------------------------------------------------------- */
 
-enum csahca_activation { CSAHCA_ACT_NONE = 0, CSAHCA_ACT_SILU = 1 };
+enum csahca_activation { CSAHCA_ACT_NONE = 0, CSAHCA_ACT_SILU = 1, CSAHCA_ACT_GELU = 2 };
 
-/* y = act(x' W^T) (+ residual), each step rounded to the storage type as the
- * torch ops it replaces round: x' = x, or with norm_weight the RMSNorm
- * x * rsqrt(mean(x^2) + eps) * norm_weight; then the product; then SiLU
- * (activation), or + residual ([batch, out_features]; not with an
- * activation).  With advance_pos, *advance_pos (int64, device) is incremented
- * by one after the product (the last kernel of a decode step). */
-int csahca_block_linear(const void* x, const void* norm_weight, double eps, const void* weight,
-                        const void* residual, int activation, void* y, int dtype, int64_t batch,
-                        int64_t out_features, int64_t in_features, int64_t* advance_pos, void* stream);
+/* y = base + alpha * (act(x' W^T) + residual), each step rounded to the
+ * storage type as the torch ops it replaces round: x' = x, or with
+ * norm_weight the RMSNorm x * rsqrt(mean(x^2) + eps) * norm_weight; then the
+ * product; then the activation (SiLU, or exact GELU 0.5 v (1 + erf(v/sqrt 2)));
+ * then + residual if given; then base + alpha * (.) if base is given
+ * (residual and base are [batch, out_features]).  With advance_pos,
+ * *advance_pos (int64, device) is incremented by one after the product (the
+ * last kernel of a decode step). */
+int csahca_block_linear(const void* x, const void* norm_weight, double eps, const void* weight, int activation,
+                        const void* residual, const void* base, double alpha, void* y, int dtype,
+                        int64_t batch, int64_t out_features, int64_t in_features, int64_t* advance_pos,
+                        void* stream);
 
 /* The QKV projection of a decode step over a growing cache: with
  * hidden [batch, H*D], qkv = RMSNorm(hidden) w_qkv^T ([batch, 3, H, D] order)

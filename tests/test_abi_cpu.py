@@ -133,10 +133,11 @@ def test_block_product_argument_errors(lib):
     """csahca_block_linear / csahca_block_qkv reject bad arguments before any
     HIP call (dummy pointers are never dereferenced)."""
     def lin(**o):
-        a = dict(x=16, norm=None, eps=1e-6, w=16, res=None, act=0, y=16, dtype=2, B=1, N=8, K=64, adv=None)
+        a = dict(x=16, norm=None, eps=1e-6, w=16, act=0, res=None, base=None, alpha=1.0, y=16, dtype=2, B=1, N=8,
+                 K=64, adv=None)
         a.update(o)
-        return lib.csahca_block_linear(a["x"], a["norm"], a["eps"], a["w"], a["res"], a["act"], a["y"], a["dtype"],
-                                       a["B"], a["N"], a["K"], a["adv"], None)
+        return lib.csahca_block_linear(a["x"], a["norm"], a["eps"], a["w"], a["act"], a["res"], a["base"], a["alpha"],
+                                       a["y"], a["dtype"], a["B"], a["N"], a["K"], a["adv"], None)
 
     assert lin(dtype=0) == 1 and "bfloat16 and float16" in lib.csahca_last_error().decode()
     assert lin(B=5) == 1 and "at most 4 token rows" in lib.csahca_last_error().decode()
@@ -144,7 +145,6 @@ def test_block_product_argument_errors(lib):
     assert lin(K=4104) == 1
     assert lin(B=2, K=4096) == 1 and "needs batch 1" in lib.csahca_last_error().decode()
     assert lin(act=7) == 1 and lib.csahca_last_error().decode() == "unknown activation"
-    assert lin(res=16, act=1) == 1 and "cannot be combined" in lib.csahca_last_error().decode()
     assert lin(x=8) == 1 and "16-byte aligned" in lib.csahca_last_error().decode()
     assert lin(w=None) == 1 and lib.csahca_last_error().decode() == "null tensor pointer"
     assert lin(B=0) == 0 and lin(N=0) == 0  # empty products: nothing to do

@@ -50,10 +50,11 @@ def make_static(B=1, H=8, S=4096, D=128, seed=0):
     return hidden, k, v
 
 
+@pytest.mark.parametrize("fused", [True, False])
 @pytest.mark.parametrize("mlp_ratio", [0.0, 2.0])
-def test_mini_block_matches_cpu_restatement(mlp_ratio):
+def test_mini_block_matches_cpu_restatement(mlp_ratio, fused):
     hidden, k, v = make_static()
-    blk = MiniCSADecodeBlock(heads=8, head_dim=128, dtype=BF, device=DEV, mlp_ratio=mlp_ratio, seed=1)
+    blk = MiniCSADecodeBlock(heads=8, head_dim=128, dtype=BF, device=DEV, mlp_ratio=mlp_ratio, seed=1, fused=fused)
     # CPU restatement with the same weights
     q = F.linear(hidden, blk.w_q.cpu()).view(1, 8, 128)
     sel = oracle.select_topk_chunks(q, k, 64, 8)
@@ -73,9 +74,10 @@ def test_mini_block_matches_cpu_restatement(mlp_ratio):
     assert_close(got_dyn, want, what="dynamic")
 
 
-def test_mini_block_graph_replays_match_eager():
+@pytest.mark.parametrize("fused", [True, False])
+def test_mini_block_graph_replays_match_eager(fused):
     hidden, k, v = (t.to(DEV) for t in make_static(seed=3))
-    blk = MiniCSADecodeBlock(heads=8, head_dim=128, dtype=BF, device=DEV, mlp_ratio=2.0, seed=2)
+    blk = MiniCSADecodeBlock(heads=8, head_dim=128, dtype=BF, device=DEV, mlp_ratio=2.0, seed=2, fused=fused)
     summ = native.csa_chunk_summary(k, 64)
     eager = blk(hidden, k, v, selection="dynamic", summary=summ)
     s = torch.cuda.Stream()

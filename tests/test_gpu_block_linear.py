@@ -1,7 +1,8 @@
 """GPU parity of the decode-step products (csahca_block_linear,
 csahca_block_qkv) against a float64 CPU restatement that rounds to the storage
 type exactly where the torch ops they replace round: the RMSNorm output, the
-F.linear output, F.silu of the rounded product, and the residual add.
+F.linear output, F.silu / F.gelu of the rounded product, the residual add, and
+`hidden + 0.01 * out`.
 
 Tolerance (the parity bar of this path): |got - ref| <= 2e-2 + 1e-2 |ref|.
 """
@@ -31,15 +32,19 @@ def assert_close(got, ref, what=""):
     assert not bad.any(), f"{what} max_abs={diff.max():.3e} bad={int(bad.sum())}/{bad.size}"
 
 
-def ref_linear(x, w, dtype, *, norm=None, eps=1e-6, residual=None, act=None):
+def ref_linear(x, w, dtype, *, norm=None, eps=1e-6, residual=None, act=None, base=None, alpha=1.0):
     xf = x.double()
     if norm is not None:
         xf = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * norm.double()).to(dtype).double()
     y = (xf @ w.double().T).to(dtype).double()
     if act == "silu":
         y = (y * torch.sigmoid(y)).to(dtype).double()
+    if act == "gelu":
+        y = (0.5 * y * (1.0 + torch.erf(y / 2.0 ** 0.5))).to(dtype).double()
     if residual is not None:
         y = (y + residual.double()).to(dtype).double()
+    if base is not None:
+        y = (base.double() + (alpha * y).to(dtype).double()).to(dtype).double()
     return y
 
 
@@ -62,6 +67,8 @@ CASES = [
     (4, 7, 8, torch.bfloat16, False, False, "silu"),      # one 16-byte chunk per row, 4 rows
     (1, 64, 4096, torch.bfloat16, True, True, None),      # widest K (8 loads per lane per row)
     (2, 130, 2048, torch.float16, False, True, None),     # widest K with batch > 1
+    (1, 2048, 1024, torch.bfloat16, False, False, "gelu"),  # the mini block's up projection
+    (3, 96, 256, torch.float16, True, True, "gelu"),      # activation, then residual
 ]
 
 
@@ -73,6 +80,19 @@ def test_block_linear_matches_rounded_reference(B, N, K, dtype, norm, residual, 
                               residual=None if res is None else res.to(DEV), activation=act)
     assert got.dtype == dtype
     assert_close(got, ref, f"B{B} N{N} K{K} {dtype} norm={norm} res={residual} act={act}")
+
+
+@pytest.mark.parametrize("mlp", [False, True])
+def test_block_linear_scaled_base_matches_the_mini_block_tail(mlp):
+    """`hidden + 0.01 * (out [+ mlp])` (model_inference.py:70-76) as the epilogue
+    of the last product."""
+    dtype = torch.bfloat16
+    x, w, _, out = operands(1, 1024, 2048 if mlp else 1024, dtype, seed=5, norm=False, residual=True)
+    hidden = torch.randn(1, 1024, generator=torch.Generator().manual_seed(6)).to(dtype)
+    ref = ref_linear(x, w, dtype, residual=out if mlp else None, base=hidden, alpha=0.01)
+    got = native.block_linear(x.to(DEV), w.to(DEV), residual=out.to(DEV) if mlp else None, base=hidden.to(DEV),
+                              alpha=0.01)
+    assert_close(got, ref, f"mlp={mlp}")
 
 
 def test_block_linear_rows_are_independent_of_batch():
