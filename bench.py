@@ -562,7 +562,7 @@ def block_bench(steps=200, warmup=20):
             log(f"block {name}: {row}")
             del gr
     for mlp, fused in ((2.0, True), (0.0, True), (2.0, False), (0.0, False)):
-        hb = HybridDecodeBlock(batch=B, heads=H, head_dim=D, capacity=S + 2 * (warmup + steps) + 1, chunk_size=chunk,
+        hb = HybridDecodeBlock(batch=B, heads=H, head_dim=D, capacity=S + 2 * (warmup + steps) + 64, chunk_size=chunk,
                                top_k=k, mlp_ratio=mlp, device=dev, seed=0, fused=fused)
         hb.prefill(kc, vc)
         hbuf = hidden0.clone()
@@ -584,6 +584,23 @@ def block_bench(steps=200, warmup=20):
         ms_graph = timed(one_g, steps)
         row = {"ms_per_token_eager": round(ms, 5), "ms_per_token_graph": round(ms_graph, 5),
                "tokens_per_s_graph": round(B / (ms_graph / 1e3), 1), "final_length": hb.length}
+        if fused:
+            # library kernels of eager steps (start/stop events per dispatch)
+            nprof = 16
+            with native.profile_launches() as prof:
+                for _ in range(nprof):
+                    one_h()
+            row["library_kernels_us_per_step"] = {n_: round(v["avg_us"] * v["launches"] / nprof, 3)
+                                                  for n_, v in prof.results.items()}
+            g = prof.results.get("block_gemv_kernel")
+            if g:
+                wbytes = sum(t.numel() * t.element_size() for t in (hb.w_qkv, hb.w_out)
+                             + ((hb.w_up, hb.w_down) if hb.use_mlp else ()))
+                us = g["avg_us"] * g["launches"] / nprof
+                row["block_gemv"] = {"weight_bytes_per_step": wbytes, "us_per_step": round(us, 3),
+                                     "launches_per_step": g["launches"] // nprof,
+                                     "achieved_gbps": round(wbytes / (us * 1e-6) / 1e9, 1),
+                                     "frac_of_hbm_peak": round(wbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4)}
         name = f"baseline_block_mlp{mlp:g}_growing_cache" + ("" if fused else "_torch_products")
         out[name] = row
         log(f"block {name}: {row}")

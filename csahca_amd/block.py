@@ -21,9 +21,9 @@ Two blocks:
   step) -> out projection -> residual -> RMSNorm -> SiLU MLP -> residual.
   Where the shapes allow (bf16/f16, batch <= 4, 16-byte aligned rows) its
   products run as the library's decode-step GEMV kernels with the norms, the
-  cache append, the activation and the residuals fused in: five or six
-  launches per step.  Otherwise, or with ``fused=False``, the products are
-  torch's.
+  cache append, the activation and the residuals fused in, and the chunk
+  summary built inside the CSA step: four or five launches per step.
+  Otherwise, or with ``fused=False``, the products are torch's.
 
 The mini block likewise runs its products (q, out, GELU MLP and the
 ``hidden + 0.01 * out`` tail) as library kernels where the shapes allow.  The
@@ -207,17 +207,17 @@ class HybridDecodeBlock:
 
     def _step_fused(self, hidden: torch.Tensor) -> torch.Tensor:
         """The step as library kernels: RMSNorm + QKV + cache append (and the
-        complete-chunk count), the summary of a completed chunk, the CSA step,
-        out projection + residual, then RMSNorm + up projection + SiLU and down
-        projection + residual; the last one advances the position."""
+        complete-chunk count), the CSA step (which first builds the summary of a
+        chunk the token completes), out projection + residual, then RMSNorm + up
+        projection + SiLU and down projection + residual; the last one advances
+        the position."""
         B, D = self.batch, self.hidden_dim
         if not hidden.is_contiguous() or hidden.data_ptr() % 16:
             hidden = hidden.contiguous().clone()
         native.block_qkv(hidden, self.w_qkv, self.q, self.k_cache, self.v_cache, self.pos, norm_weight=self.norm1,
                          num_chunks=self.nchunks, chunk_size=self.chunk_size)
-        native.csa_chunk_summary_at(self.k_cache, self.summary_buf, self.chunk_size, self.pos)
-        native.csa_decode_step_dev(self.q, self.k_cache, self.v_cache, self.summary_buf, self.nchunks,
-                                   self.chunk_size, self.top_k, out=self.attn, indices=self.indices)
+        native.csa_decode_step_at(self.q, self.k_cache, self.v_cache, self.summary_buf, self.pos, self.chunk_size,
+                                  self.top_k, out=self.attn, indices=self.indices)
         h = native.block_linear(self.attn.view(B, D), self.w_out, residual=hidden,
                                 advance_pos=None if self.use_mlp else self.pos)
         if self.use_mlp:

@@ -329,28 +329,7 @@ __global__ __launch_bounds__(64) void csa_summary_vec_kernel(const T* __restrict
   if (c < 0) return;
   const T* __restrict__ base = k + (bh * seq_len + c * chunk) * D + col * VEC;
   float acc[VEC];
-#pragma unroll
-  for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
-  int r = grp;
-  for (; r + 3 * RPL < chunk; r += 4 * RPL) {
-    float a[4][VEC];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) load16<T>(base + static_cast<int64_t>(r + u * RPL) * D, a[u]);
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) acc[e] += a[u][e];
-  }
-  for (; r < chunk; r += RPL) {
-    float a[VEC];
-    load16<T>(base + static_cast<int64_t>(r) * D, a);
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) acc[e] += a[e];
-  }
-#pragma unroll
-  for (int off = LPR; off < kWave; off <<= 1)
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) acc[e] += xor_lanes(acc[e], off);
+  wave_chunk_colsum<T, D>(base, chunk, grp, acc);
   if (grp == 0) {
     float* dst = summary + (bh * summary_chunks + c) * D + col * VEC;
     const float fc = static_cast<float>(chunk);

@@ -287,6 +287,40 @@ struct AttendLayout {
   static_assert(LPR >= 1 && LPR <= kWave && (LPR & (LPR - 1)) == 0, "bad row split");
 };
 
+// Column sums of `chunk` consecutive [*, D] rows by one wavefront in the
+// AttendLayout split: lane (grp, col) adds rows grp, grp + RPL, ... of its VEC
+// columns at `base` (row 0, column col * VEC), four rows per batch of loads,
+// then the row groups are folded by a butterfly, so every lane ends with the
+// sums of its columns.  The chunk-summary kernel and the fused decode step both
+// build summaries through this one function, so their rows agree bit for bit.
+template <typename T, int D>
+__device__ __forceinline__ void wave_chunk_colsum(const T* __restrict__ base, int chunk, int grp, float* acc) {
+  using L = AttendLayout<T, D>;
+  constexpr int VEC = L::VEC, LPR = L::LPR, RPL = L::RPL;
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+  int r = grp;
+  for (; r + 3 * RPL < chunk; r += 4 * RPL) {
+    float a[4][VEC];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) load16<T>(base + static_cast<int64_t>(r + u * RPL) * D, a[u]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc[e] += a[u][e];
+  }
+  for (; r < chunk; r += RPL) {
+    float a[VEC];
+    load16<T>(base + static_cast<int64_t>(r) * D, a);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] += a[e];
+  }
+#pragma unroll
+  for (int off = LPR; off < kWave; off <<= 1)
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] += xor_lanes(acc[e], off);
+}
+
 template <typename T, int D>
 struct WaveSoftmax {
   static constexpr int VEC = AttendLayout<T, D>::VEC;

@@ -68,6 +68,10 @@ struct StepParams {
   int64_t C;            // chunks in play (when c_dev is null)
   int64_t Cs;           // summary / key rows per head (C <= Cs)
   const int32_t* c_dev;  // chunks in play, read on the device (clamped to [0, Cs]); may be null
+  const int64_t* pos_dev;  // position of the token just appended, or null: chunks in play are
+                           // min((pos + 1) / chunk, Cs) and the summary row of the chunk the token
+                           // completes is built first (into summary_out)
+  float* summary_out;
   int chunk;
   int chunk_shift;
   int topk;
@@ -127,8 +131,14 @@ __global__ __launch_bounds__(kStepThreads) void csa_step_kernel(StepParams a) {
   const int p = static_cast<int>(blockIdx.x % P);
   const int64_t Cs = a.Cs;
   // Chunks in play: the host's count, or the device's (its load overlaps the
-  // summary loads of phase A, which are laid out over the Cs rows).
-  const int64_t C = a.c_dev ? min<int64_t>(max<int32_t>(*a.c_dev, 0), Cs) : a.C;
+  // summary loads of phase A, which are laid out over the Cs rows), or the
+  // count implied by the device position of the token just appended.
+  int64_t C = a.c_dev ? min<int64_t>(max<int32_t>(*a.c_dev, 0), Cs) : a.C;
+  // Position mode: the count is set in phase A, after its loads are issued
+  // (the position is requested with them); keys stand in as the address of
+  // the unused load otherwise.
+  const int64_t pos_raw =
+      load_global_raw<int64_t>(a.pos_dev ? static_cast<const void*>(a.pos_dev) : static_cast<const void*>(a.keys));
   const T* __restrict__ q = static_cast<const T*>(a.q) + h * D;
 
   // Loads that depend on nothing are issued together, unconditionally, and
@@ -165,6 +175,42 @@ __global__ __launch_bounds__(kStepThreads) void csa_step_kernel(StepParams a) {
       }
       uint32_t ep = epoch;
       asm volatile("" : "+v"(ep));
+      if (a.pos_dev) {
+        // The token at pos was just appended: n = pos + 1 tokens, C complete
+        // chunks.  If it completes chunk C - 1 and this block of rows holds
+        // that row, wavefront 0 builds the row first -- through the summary
+        // kernel's own column-sum routine, so the bits are the summary
+        // kernel's -- and the block's rows are loaded again (once every
+        // `chunk` steps, in one workgroup per head).
+        int64_t n = pos_raw;
+        asm volatile("" : "+v"(n));  // consumed only here, after the loads above
+        n += 1;
+        const int64_t nc = n <= 0 ? 0 : (a.chunk_shift >= 0 ? n >> a.chunk_shift : n / a.chunk);
+        C = min<int64_t>(nc, Cs);
+        const int64_t cn = C - 1;
+        const bool build = n > 0 && nc * a.chunk == n && nc <= Cs && n <= a.S;
+        if (build && cn >= blk && cn < blk + kStepWaves * SRPL * US && cn < c1) {
+          if (wave == 0) {
+            const int g2 = lane / LPR, c2 = lane % LPR;
+            const T* kb0 = static_cast<const T*>(a.kcache) + (h * a.S + cn * a.chunk) * D + c2 * VEC;
+            float acc[VEC];
+            wave_chunk_colsum<T, D>(kb0, a.chunk, g2, acc);
+            if (g2 == 0) {
+              float* dst = a.summary_out + (h * Cs + cn) * D + c2 * VEC;
+              const float fc = static_cast<float>(a.chunk);
+#pragma unroll
+              for (int e = 0; e < VEC; ++e) dst[e] = acc[e] / fc;
+            }
+            __threadfence();
+          }
+          __syncthreads();
+#pragma unroll
+          for (int u = 0; u < US; ++u) {
+            const int64_t c = base + grp + SRPL * u;
+            rs[u] = load_global_u4(sb + (c < c1 ? c : c0) * D);
+          }
+        }
+      }
       float qf[8];
       widen16<T>(q4, qf);
       float sc[US];
@@ -394,8 +440,9 @@ namespace {
 // chunks in play are *c_dev (clamped to [0, num_chunks]), read on the device.
 int decode_step_impl(const void* q, const void* k_cache, const void* v_cache, const float* summary, void* out,
                      int32_t* out_indices, int dtype, int64_t batch, int64_t heads, int64_t seq_len,
-                     int64_t head_dim, int64_t num_chunks, const int32_t* c_dev, int64_t chunk_size,
-                     int64_t top_k, void* workspace, size_t workspace_bytes, void* stream_ptr) {
+                     int64_t head_dim, int64_t num_chunks, const int32_t* c_dev, const int64_t* pos_dev,
+                     int64_t chunk_size, int64_t top_k, void* workspace, size_t workspace_bytes,
+                     void* stream_ptr) {
   CSAHCA_REQUIRE(valid_dtype(dtype), "q, k_cache and v_cache must be float32, float64, float16 or bfloat16");
   CSAHCA_REQUIRE(batch >= 0 && heads >= 0 && seq_len >= 0 && head_dim >= 0 && num_chunks >= 0,
                  "negative dimension");
@@ -459,6 +506,8 @@ int decode_step_impl(const void* q, const void* k_cache, const void* v_cache, co
     pr.C = num_chunks;
     pr.Cs = num_chunks;
     pr.c_dev = c_dev;
+    pr.pos_dev = pos_dev;
+    pr.summary_out = const_cast<float*>(summary);
     pr.chunk = static_cast<int>(chunk_size);
     int shift = -1;
     if ((chunk_size & (chunk_size - 1)) == 0) {
@@ -491,7 +540,7 @@ int decode_step_impl(const void* q, const void* k_cache, const void* v_cache, co
       }
     });
   }
-  if (c_dev != nullptr)
+  if (c_dev != nullptr || pos_dev != nullptr)
     return fail(CSAHCA_ERR_ARGUMENT,
                 "a device chunk count needs the fused step (float32/float16/bfloat16, head_dim 64/128/256, "
                 "16-byte aligned tensors, top_k <= 1024)");
@@ -517,7 +566,7 @@ extern "C" int csahca_csa_decode_step(const void* q, const void* k_cache, const 
                                       void* stream_ptr) {
   clear_error();
   return decode_step_impl(q, k_cache, v_cache, summary, out, out_indices, dtype, batch, heads, seq_len, head_dim,
-                          num_chunks, nullptr, chunk_size, top_k, workspace, workspace_bytes, stream_ptr);
+                          num_chunks, nullptr, nullptr, chunk_size, top_k, workspace, workspace_bytes, stream_ptr);
 }
 
 extern "C" int csahca_csa_decode_step_dev(const void* q, const void* k_cache, const void* v_cache,
@@ -529,7 +578,20 @@ extern "C" int csahca_csa_decode_step_dev(const void* q, const void* k_cache, co
   clear_error();
   CSAHCA_REQUIRE(num_chunks_dev != nullptr, "null num_chunks pointer");
   return decode_step_impl(q, k_cache, v_cache, summary, out, out_indices, dtype, batch, heads, seq_len, head_dim,
-                          max_chunks, num_chunks_dev, chunk_size, top_k, workspace, workspace_bytes, stream_ptr);
+                          max_chunks, num_chunks_dev, nullptr, chunk_size, top_k, workspace, workspace_bytes,
+                          stream_ptr);
+}
+
+extern "C" int csahca_csa_decode_step_at(const void* q, const void* k_cache, const void* v_cache, float* summary,
+                                         const int64_t* token_pos, void* out, int32_t* out_indices, int dtype,
+                                         int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
+                                         int64_t max_chunks, int64_t chunk_size, int64_t top_k, void* workspace,
+                                         size_t workspace_bytes, void* stream_ptr) {
+  clear_error();
+  CSAHCA_REQUIRE(token_pos != nullptr, "null token_pos pointer");
+  return decode_step_impl(q, k_cache, v_cache, summary, out, out_indices, dtype, batch, heads, seq_len, head_dim,
+                          max_chunks, nullptr, token_pos, chunk_size, top_k, workspace, workspace_bytes,
+                          stream_ptr);
 }
 
 extern "C" int csahca_csa_step_status(const void* workspace, uint32_t* status_out, void* stream_ptr) {

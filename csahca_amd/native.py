@@ -59,6 +59,7 @@ _SIGNATURES = {
     "csahca_csa_step_workspace_bytes": (_sz, [_i64] * 6),
     "csahca_csa_decode_step": (_int, [_vp] * 6 + [_int] + [_i64] * 7 + [_vp, _sz, _vp]),
     "csahca_csa_decode_step_dev": (_int, [_vp] * 7 + [_int] + [_i64] * 7 + [_vp, _sz, _vp]),
+    "csahca_csa_decode_step_at": (_int, [_vp] * 7 + [_int] + [_i64] * 7 + [_vp, _sz, _vp]),
     "csahca_csa_step_status": (_int, [_vp, ctypes.POINTER(ctypes.c_uint32), _vp]),
     "csahca_hca_decode_workspace_bytes": (_sz, [_i64] * 5),
     "csahca_dsv4_pack_tokens": (_int, [_vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp]),
@@ -435,6 +436,43 @@ def block_qkv(hidden, w_qkv, q, k_cache, v_cache, token_pos, *, norm_weight=None
                                    _ptr(v_cache), _ptr(token_pos), _ptr(num_chunks), _DTYPES[hidden.dtype], B, H, D,
                                    cap, int(chunk_size), _stream()))
     return q
+
+
+def csa_decode_step_at(q, k_cache, v_cache, summary, token_pos, chunk_size, top_k, *, out=None, indices=None):
+    """The decode step of the token at ``token_pos`` (one-element int64 CUDA
+    tensor, read on the device) just appended to a growing cache: the chunks in
+    play are min((pos + 1) // chunk_size, max_chunks); if the token completes a
+    chunk, its summary row (``summary``: fp32 [batch, heads, max_chunks, D],
+    updated in place) is built first, bit-identical to csa_chunk_summary.  One
+    launch in place of csa_chunk_summary_at + csa_decode_step_dev.  Returns
+    ``(out, chunk_indices)``."""
+    chunk_size, top_k = int(chunk_size), int(top_k)
+    _csa_checks(q, k_cache, v_cache, torch.empty((q.shape[0], q.shape[1], 0), dtype=torch.int32, device=q.device),
+                chunk_size, tiled=False)
+    _check(summary.is_cuda and summary.is_contiguous() and summary.dtype == torch.float32 and summary.dim() == 4,
+           "summary must be a contiguous fp32 [batch, heads, chunks, head_dim] CUDA tensor")
+    _check(token_pos.is_cuda and token_pos.dtype == torch.int64 and token_pos.numel() == 1,
+           "token_pos must be a one-element int64 CUDA tensor")
+    B, H, D = q.shape
+    S = k_cache.shape[2]
+    _check(tuple(summary.shape[:2]) == (B, H) and summary.shape[3] == D, "summary shape must match q")
+    Cs = summary.shape[2]
+    _check(top_k >= 0, "top_k must be non-negative")
+    k = min(top_k, Cs)
+    with torch.cuda.device(q.device):
+        if out is None:
+            out = torch.empty_like(q)
+        if indices is None:
+            indices = torch.empty((B, H, k), dtype=torch.int32, device=q.device)
+        _check(out.shape == q.shape and out.dtype == q.dtype and out.is_contiguous(), "out must match q")
+        _check(tuple(indices.shape) == (B, H, k) and indices.dtype == torch.int32 and indices.is_contiguous(),
+               "indices must be a contiguous int32 [batch, heads, min(top_k, max_chunks)] tensor")
+        ws = _step_workspace(lib().csahca_csa_step_workspace_bytes(B, H, Cs, D, top_k, chunk_size), q.device,
+                             (B * H, Cs, D, k, chunk_size))
+        _rc(lib().csahca_csa_decode_step_at(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(summary), _ptr(token_pos),
+                                            _ptr(out), _ptr(indices), _DTYPES[q.dtype], B, H, S, D, Cs, chunk_size,
+                                            top_k, _ptr(ws), ws.numel(), _stream()))
+    return out, indices
 
 
 def csa_step_status(device=None) -> dict:

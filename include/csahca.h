@@ -159,6 +159,21 @@ int csahca_csa_decode_step_dev(const void* q, const void* k_cache, const void* v
                                int64_t chunk_size, int64_t top_k, void* workspace,
                                size_t workspace_bytes, void* stream);
 
+/* The decode step of the token at p = *token_pos (int64, device) just
+ * appended to a growing cache (no reference counterpart; for a decode loop
+ * captured in a HIP graph): the chunks in play are C = min((p + 1) /
+ * chunk_size, max_chunks).  If the token completes chunk C - 1 ((p + 1) a
+ * multiple of chunk_size, p < seq_len), summary[b,h,C-1] is first rebuilt from
+ * k_cache exactly as csahca_csa_chunk_summary computes it (same bits); then
+ * the step selects among the first C rows as csahca_csa_decode_step_dev does.
+ * One launch replaces csahca_csa_chunk_summary_at + csahca_csa_decode_step_dev.
+ * Same workspace and shape rules as csahca_csa_decode_step_dev. */
+int csahca_csa_decode_step_at(const void* q, const void* k_cache, const void* v_cache, float* summary,
+                              const int64_t* token_pos, void* out, int32_t* out_indices, int dtype,
+                              int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
+                              int64_t max_chunks, int64_t chunk_size, int64_t top_k, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
 /* Reads the step workspace's sticky status word (0 = healthy; bit 0 = a
  * workgroup hand-off timed out, so a result may be wrong) into host memory;
  * synchronises the stream. */

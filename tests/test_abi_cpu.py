@@ -117,6 +117,19 @@ def test_device_state_entry_points_argument_errors(lib):
     assert step() == 2  # valid arguments, no workspace
     assert step(B=0) == 0
 
+    def step_at(**o):
+        a = dict(q=1, k=1, v=1, summ=1, pos=1, out=1, idx=1, dtype=2, B=1, H=1, S=64, D=128, C=1, chunk=64, top_k=1,
+                 ws=None, wsb=0)
+        a.update(o)
+        return lib.csahca_csa_decode_step_at(a["q"], a["k"], a["v"], a["summ"], a["pos"], a["out"], a["idx"],
+                                             a["dtype"], a["B"], a["H"], a["S"], a["D"], a["C"], a["chunk"],
+                                             a["top_k"], a["ws"], a["wsb"], None)
+
+    assert step_at(pos=None) == 1 and lib.csahca_last_error().decode() == "null token_pos pointer"
+    assert step_at(C=2) == 1 and lib.csahca_last_error().decode() == "summaries cover more chunks than the cache holds"
+    assert step_at() == 2  # valid arguments, no workspace
+    assert step_at(B=0) == 0
+
     def summ_at(**o):
         a = dict(k=1, summ=1, dtype=2, B=1, H=1, S=64, D=128, chunk=64, C=1, pos=1)
         a.update(o)

@@ -211,6 +211,36 @@ def test_decode_step_dev_matches_the_host_count_step():
     assert_close(got, part, atol=1e-3, rtol=1e-3, what="40 of 64 chunks")
 
 
+@pytest.mark.parametrize("D,dtype", [(128, BF), (64, torch.float16), (256, torch.float32)])
+def test_decode_step_at_equals_summary_at_then_step_dev(D, dtype):
+    """One launch (summary built inside the step) against the two-launch
+    sequence, bit for bit, token by token across chunk boundaries: the summary
+    rows, the selected ids and the outputs."""
+    B, H, chunk, cap, k = 1, 4, 32, 20 * 32, 3
+    g = torch.Generator().manual_seed(D)
+    kc = torch.randn(B, H, cap, D, generator=g).to(dtype).to(DEV)
+    vc = torch.randn(B, H, cap, D, generator=g).to(dtype).to(DEV)
+    q = torch.randn(B, H, D, generator=g).to(dtype).to(DEV)
+    Cs = cap // chunk
+    s1 = torch.zeros(B, H, Cs, D, dtype=torch.float32, device=DEV)
+    s2 = torch.zeros_like(s1)
+    start = 3 * chunk - 3
+    native.csa_chunk_summary(kc, chunk, out=s1, chunk_begin=0, num_chunks=start // chunk)
+    s2.copy_(s1)
+    pos = torch.zeros(1, dtype=torch.int64, device=DEV)
+    nch = torch.zeros(1, dtype=torch.int32, device=DEV)
+    for p in list(range(start, start + 8)) + [cap - 1]:  # completes chunks 2 and 19
+        pos.fill_(p)
+        native.csa_chunk_summary_at(kc, s1, chunk, pos)
+        nch.fill_((p + 1) // chunk)
+        o1, i1 = native.csa_decode_step_dev(q, kc, vc, s1, nch, chunk, k)
+        o2, i2 = native.csa_decode_step_at(q, kc, vc, s2, pos, chunk, k)
+        assert torch.equal(s1, s2), p
+        assert torch.equal(i1, i2) and torch.equal(o1, o2), p
+    fresh = native.csa_chunk_summary(kc, chunk)
+    assert torch.equal(s2[:, :, :3], fresh[:, :, :3]) and torch.equal(s2[:, :, 19], fresh[:, :, 19])
+
+
 def test_decode_step_dev_with_fewer_chunks_than_top_k():
     _, k, v = make_static(B=1, H=4, S=1024, D=64, seed=14)
     q = torch.randn(1, 4, 64, generator=torch.Generator().manual_seed(15)).to(BF)
