@@ -492,6 +492,9 @@ def hca_bench(steps=256, copies=4, hca_chunk=256):
     return out
 
 
+GRAPH_STEPS = 10  # decode steps per captured graph in the block leg (as a 10-layer step graph holds 10 blocks)
+
+
 def block_bench(steps=200, warmup=20):
     """The decode blocks of csahca_amd.block at S=32768,
     H=8, D=128 (hidden 1024), chunk 64, top-8, bf16, 200 steps after 20 warm-up
@@ -500,10 +503,12 @@ def block_bench(steps=200, warmup=20):
     one static cache (no rotation).  Reference block: precomputed selection
     (tiled op, tile 8) and dynamic selection (fused step from cached summaries,
     and from summaries rebuilt every step as the reference does), eager and as
-    one HIP graph per step.  Hybrid block (RMSNorm/QKV/SiLU MLP, growing
-    cache): eager, and as one HIP graph per step whose replays advance the
+    HIP graphs of GRAPH_STEPS consecutive steps (the result written back in
+    place as the next input).  Hybrid block (RMSNorm/QKV/SiLU MLP, growing
+    cache): eager, and as graphs of GRAPH_STEPS steps whose replays advance the
     cache (position and chunk count live on the device); with the library's
-    fused decode-step products, and with torch's products for comparison."""
+    fused decode-step products, and with torch's products for comparison.
+    Graph figures are per step (replay time / GRAPH_STEPS)."""
     import torch
 
     from csahca_amd import native
@@ -540,8 +545,8 @@ def block_bench(steps=200, warmup=20):
         for mode, kw in modes.items():
             hbuf = hidden0.clone()
 
-            def one():
-                hbuf.copy_(blk(hbuf, kc, vc, chunk_size=chunk, top_k=k, **kw))
+            def one():  # the step's result becomes the next step's input, in place
+                blk(hbuf, kc, vc, chunk_size=chunk, top_k=k, out=hbuf, **kw)
 
             for _ in range(warmup):
                 one()
@@ -553,8 +558,10 @@ def block_bench(steps=200, warmup=20):
             torch.cuda.current_stream().wait_stream(s)
             gr = torch.cuda.CUDAGraph()
             with torch.cuda.graph(gr):
-                one()
-            ms_graph = timed(gr.replay, steps)
+                for _ in range(GRAPH_STEPS):
+                    one()
+            gr.replay()
+            ms_graph = timed(gr.replay, max(1, steps // GRAPH_STEPS)) / GRAPH_STEPS
             row = {"ms_per_token_eager": round(ms_eager, 5), "ms_per_token_graph": round(ms_graph, 5),
                    "tokens_per_s_graph": round(B / (ms_graph / 1e3), 1)}
             name = f"mini_mlp{mlp:g}_{mode}" + ("" if fused else "_torch_products")
@@ -562,26 +569,23 @@ def block_bench(steps=200, warmup=20):
             log(f"block {name}: {row}")
             del gr
     for mlp, fused in ((2.0, True), (0.0, True), (2.0, False), (0.0, False)):
-        hb = HybridDecodeBlock(batch=B, heads=H, head_dim=D, capacity=S + 2 * (warmup + steps) + 64, chunk_size=chunk,
-                               top_k=k, mlp_ratio=mlp, device=dev, seed=0, fused=fused)
+        reps = max(1, steps // GRAPH_STEPS)
+        hb = HybridDecodeBlock(batch=B, heads=H, head_dim=D, chunk_size=chunk, top_k=k, mlp_ratio=mlp, device=dev,
+                               seed=0, fused=fused,
+                               capacity=S + warmup + steps + 16 + 1 + GRAPH_STEPS * (reps + 2) + 64)
         hb.prefill(kc, vc)
         hbuf = hidden0.clone()
 
-        def one_h():
-            hbuf.copy_(hb(hbuf))
+        def one_h():  # the step's result becomes the next step's input, in place
+            hb(hbuf, out=hbuf)
 
         for _ in range(warmup):
             one_h()
         ms = timed(one_h, steps)
-        replay, gout = hb.capture(hbuf)
-
-        def one_g():
-            replay()
-            hbuf.copy_(gout)
-
-        for _ in range(warmup):
-            one_g()
-        ms_graph = timed(one_g, steps)
+        replay, _ = hb.capture(hbuf, steps=GRAPH_STEPS, feedback=True)
+        replay()
+        replay()
+        ms_graph = timed(replay, reps) / GRAPH_STEPS
         row = {"ms_per_token_eager": round(ms, 5), "ms_per_token_graph": round(ms_graph, 5),
                "tokens_per_s_graph": round(B / (ms_graph / 1e3), 1), "final_length": hb.length}
         if fused:

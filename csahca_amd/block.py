@@ -88,14 +88,27 @@ class MiniCSADecodeBlock:
                 and widest <= (4096 if B == 1 else 2048))
 
     def forward(self, hidden, k_cache, v_cache, *, selection: str = "precomputed", selected_chunks=None,
-                summary=None, chunk_size: int = 64, top_k: int = 8, tile_size: int = 8):
+                summary=None, chunk_size: int = 64, top_k: int = 8, tile_size: int = 8, out=None):
+        """One decode step; the result goes to ``out`` when given (it may be
+        ``hidden`` itself: the step's last kernel reads each hidden value
+        before overwriting it)."""
         fuse = self.can_fuse(hidden) if self.fused is None else self.fused
         if fuse:
             if not self.can_fuse(hidden):
                 raise ValueError("the fused block products need bf16/f16, batch <= 4 and feature sizes that are "
                                  "multiples of 8 (at most 4096, or 2048 for batch > 1)")
-            return self._forward_fused(hidden, k_cache, v_cache, selection=selection, selected_chunks=selected_chunks,
-                                       summary=summary, chunk_size=chunk_size, top_k=top_k, tile_size=tile_size)
+            return self._forward_fused(hidden, k_cache, v_cache, out, selection=selection,
+                                       selected_chunks=selected_chunks, summary=summary, chunk_size=chunk_size,
+                                       top_k=top_k, tile_size=tile_size)
+        res = self._forward_torch(hidden, k_cache, v_cache, selection=selection, selected_chunks=selected_chunks,
+                                  summary=summary, chunk_size=chunk_size, top_k=top_k, tile_size=tile_size)
+        if out is None:
+            return res
+        out.copy_(res)
+        return out
+
+    def _forward_torch(self, hidden, k_cache, v_cache, *, selection, selected_chunks, summary, chunk_size, top_k,
+                       tile_size):
         batch = hidden.shape[0]
         q = F.linear(hidden, self.w_q).view(batch, self.heads, self.head_dim)
         attn = self.attention(q, k_cache, v_cache, selection=selection, selected_chunks=selected_chunks,
@@ -105,7 +118,7 @@ class MiniCSADecodeBlock:
             out = out + F.linear(F.gelu(F.linear(hidden, self.w_up)), self.w_down)
         return hidden + 0.01 * out
 
-    def _forward_fused(self, hidden, k_cache, v_cache, **attn_kw):
+    def _forward_fused(self, hidden, k_cache, v_cache, out, **attn_kw):
         """The same block through the library's decode-step products: q
         projection, attention, out projection, and for the MLP the GELU up
         projection and the down projection whose epilogue adds the out
@@ -117,10 +130,10 @@ class MiniCSADecodeBlock:
         q = native.block_linear(hidden, self.w_q).view(B, self.heads, self.head_dim)
         attn = self.attention(q, k_cache, v_cache, **attn_kw).reshape(B, self.hidden_dim)
         if self.use_mlp:
-            out = native.block_linear(attn, self.w_out)
+            o = native.block_linear(attn, self.w_out)
             u = native.block_linear(hidden, self.w_up, activation="gelu")
-            return native.block_linear(u, self.w_down, residual=out, base=hidden, alpha=0.01)
-        return native.block_linear(attn, self.w_out, base=hidden, alpha=0.01)
+            return native.block_linear(u, self.w_down, residual=o, base=hidden, alpha=0.01, out=out)
+        return native.block_linear(attn, self.w_out, base=hidden, alpha=0.01, out=out)
 
     __call__ = forward
 
@@ -202,10 +215,10 @@ class HybridDecodeBlock:
         self.pos.fill_(S)
         self.nchunks.fill_(C)
 
-    def _step(self, hidden: torch.Tensor) -> torch.Tensor:
-        return self._step_fused(hidden) if self.fused else self._step_torch(hidden)
+    def _step(self, hidden: torch.Tensor, out=None) -> torch.Tensor:
+        return self._step_fused(hidden, out) if self.fused else self._step_torch(hidden, out)
 
-    def _step_fused(self, hidden: torch.Tensor) -> torch.Tensor:
+    def _step_fused(self, hidden: torch.Tensor, out=None) -> torch.Tensor:
         """The step as library kernels: RMSNorm + QKV + cache append (and the
         complete-chunk count), the CSA step (which first builds the summary of a
         chunk the token completes), out projection + residual, then RMSNorm + up
@@ -218,14 +231,14 @@ class HybridDecodeBlock:
                          num_chunks=self.nchunks, chunk_size=self.chunk_size)
         native.csa_decode_step_at(self.q, self.k_cache, self.v_cache, self.summary_buf, self.pos, self.chunk_size,
                                   self.top_k, out=self.attn, indices=self.indices)
-        h = native.block_linear(self.attn.view(B, D), self.w_out, residual=hidden,
-                                advance_pos=None if self.use_mlp else self.pos)
-        if self.use_mlp:
-            u = native.block_linear(h, self.w_up, norm_weight=self.norm2, activation="silu")
-            h = native.block_linear(u, self.w_down, residual=h, advance_pos=self.pos)
-        return h
+        if not self.use_mlp:
+            return native.block_linear(self.attn.view(B, D), self.w_out, residual=hidden, advance_pos=self.pos,
+                                       out=out)
+        h = native.block_linear(self.attn.view(B, D), self.w_out, residual=hidden)
+        u = native.block_linear(h, self.w_up, norm_weight=self.norm2, activation="silu")
+        return native.block_linear(u, self.w_down, residual=h, advance_pos=self.pos, out=out)
 
-    def _step_torch(self, hidden: torch.Tensor) -> torch.Tensor:
+    def _step_torch(self, hidden: torch.Tensor, out=None) -> torch.Tensor:
         B, H, D = self.batch, self.heads, self.head_dim
         x = rms_norm(hidden, self.norm1)
         qkv = F.linear(x, self.w_qkv).view(B, 3, H, D)
@@ -240,7 +253,10 @@ class HybridDecodeBlock:
         h = hidden + F.linear(self.attn.reshape(B, self.hidden_dim), self.w_out)
         if self.use_mlp:
             h = h + F.linear(F.silu(F.linear(rms_norm(h, self.norm2), self.w_up)), self.w_down)
-        return h
+        if out is None:
+            return h
+        out.copy_(h)
+        return out
 
     def _advance(self) -> None:
         if self.length >= self.capacity:
@@ -249,20 +265,30 @@ class HybridDecodeBlock:
             raise RuntimeError("no complete chunk to attend to")
         self.length += 1
 
-    def step(self, hidden: torch.Tensor) -> torch.Tensor:
+    def step(self, hidden: torch.Tensor, out=None) -> torch.Tensor:
+        """One decode step; the result goes to ``out`` when given (it may be
+        ``hidden`` itself, which the fused step's last kernel reads before
+        overwriting)."""
         self._advance()
-        return self._step(hidden)
+        return self._step(hidden, out)
 
     __call__ = step
 
-    def capture(self, hidden: torch.Tensor):
-        """Record one step on the static input ``hidden`` as a HIP graph.
+    def capture(self, hidden: torch.Tensor, steps: int = 1, feedback: bool = False):
+        """Record ``steps`` consecutive steps on the static input ``hidden`` as
+        one HIP graph.
 
-        Returns ``(replay, out)``: each ``replay()`` runs one step (appending the
-        token of the current ``hidden`` contents) and leaves its result in
-        ``out``.  A warm-up step on the capture stream creates that stream's
-        library state first; its position advance is undone, and the K/V slot
-        it wrote is overwritten by the next step."""
+        Returns ``(replay, out)``: each ``replay()`` runs the steps (each
+        appending one token) and leaves the last result in ``out``.  With
+        ``feedback`` every step writes its result into ``hidden``, which the
+        next step (and the next replay) consumes, as a decode loop feeds its
+        hidden state back; ``out`` is then ``hidden``.  Without it every step
+        reads the same ``hidden``.  A warm-up step on the capture stream creates
+        that stream's library state first; its position advance is undone, and
+        the K/V slot it wrote is overwritten by the next step."""
+        steps = int(steps)
+        if steps < 1:
+            raise ValueError("steps must be positive")
         s = torch.cuda.Stream(device=hidden.device)
         s.wait_stream(torch.cuda.current_stream(hidden.device))
         with torch.cuda.stream(s):
@@ -273,10 +299,12 @@ class HybridDecodeBlock:
         torch.cuda.synchronize(hidden.device)
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=s):
-            out = self._step(hidden)
+            for _ in range(steps):
+                out = self._step(hidden, hidden if feedback else None)
 
         def replay():
-            self._advance()
+            for _ in range(steps):
+                self._advance()
             graph.replay()
             return out
 

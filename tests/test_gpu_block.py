@@ -287,3 +287,43 @@ def test_hybrid_block_graph_replays_match_eager_steps(mlp_ratio, fused):
     assert torch.equal(graphed.k_cache, eager.k_cache) and torch.equal(graphed.summary_buf, eager.summary_buf)
     fresh = native.csa_chunk_summary(eager.k_cache[:, :, :1088].contiguous(), 64)
     torch.testing.assert_close(eager.summary, fresh, rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_mini_block_in_place_output_equals_returned_output(fused):
+    hidden, k, v = (t.to(DEV) for t in make_static(seed=4))
+    blk = MiniCSADecodeBlock(heads=8, head_dim=128, dtype=BF, device=DEV, mlp_ratio=2.0, seed=3, fused=fused)
+    summ = native.csa_chunk_summary(k, 64)
+    want = blk(hidden, k, v, selection="dynamic", summary=summ)
+    buf = hidden.clone()
+    got = blk(buf, k, v, selection="dynamic", summary=summ, out=buf)
+    assert got.data_ptr() == buf.data_ptr() and torch.equal(buf, want)
+
+
+@pytest.mark.parametrize("fused", [True, False])
+@pytest.mark.parametrize("mlp_ratio", [0.0, 2.0])
+def test_hybrid_block_multi_step_graph_with_feedback_matches_eager(mlp_ratio, fused):
+    """A graph of 5 consecutive steps whose results feed the next step in place
+    equals 5 eager steps with the hidden state fed back, replay after replay,
+    across a chunk boundary."""
+    B, H, D, S0, G, reps = 1, 4, 64, 118, 5, 4  # token 128 completes chunk 1 during replay 1
+    blocks = [HybridDecodeBlock(batch=B, heads=H, head_dim=D, capacity=256, chunk_size=64, top_k=2,
+                                mlp_ratio=mlp_ratio, device=DEV, seed=31, fused=fused) for _ in range(2)]
+    g = torch.Generator().manual_seed(32)
+    k0 = torch.randn(B, H, S0, D, generator=g).to(BF).to(DEV)
+    v0 = torch.randn(B, H, S0, D, generator=g).to(BF).to(DEV)
+    h0 = torch.randn(B, H * D, generator=g).to(BF).to(DEV)
+    for blk in blocks:
+        blk.prefill(k0, v0)
+    eager, graphed = blocks
+    he = h0.clone()
+    hg = h0.clone()
+    replay, out = graphed.capture(hg, steps=G, feedback=True)
+    assert out is hg
+    for r in range(reps):
+        for _ in range(G):
+            eager(he, out=he)
+        replay()
+        assert torch.equal(hg, he), f"replay {r}"
+    assert eager.length == graphed.length == S0 + G * reps
+    assert torch.equal(graphed.k_cache, eager.k_cache) and torch.equal(graphed.summary_buf, eager.summary_buf)
