@@ -296,6 +296,61 @@ __global__ __launch_bounds__(256) void csa_merge_kernel(const float* __restrict_
   }
 }
 
+// Merge of at most kMergeColTiles partials per head, spread over workgroups
+// of (head, kMergeCols output columns): 256 threads = kMergeCols columns x 8
+// tile groups.  Every load -- the thread's tiles of its column, and lane l's
+// (m, l) of tile l -- is one unconditional batch; each wavefront forms the
+// tile weights itself (a wavefront max and sum over the tiles, one tile per
+// lane) and a thread takes its tiles' weights by lane shuffle, so the only
+// barrier is the one that sums the 8 tile groups of a column.
+constexpr int kMergeColTiles = kWave;
+constexpr int kMergeCols = 32;
+constexpr int kMergeGroups = 256 / kMergeCols;  // 8
+
+template <typename T>
+__global__ __launch_bounds__(256) void csa_merge_cols_kernel(const float* __restrict__ part_ml,
+                                                             const float* __restrict__ part_acc,
+                                                             T* __restrict__ out, int D, int num_tiles,
+                                                             int col_blocks) {
+  constexpr int TPG = kMergeColTiles / kMergeGroups;  // tiles per group
+  __shared__ float colsum[256];
+  const int tid = threadIdx.x, lane = tid % kWave;
+  const int64_t bh = blockIdx.x / col_blocks;
+  const int cb = static_cast<int>(blockIdx.x - bh * col_blocks);
+  const int cl = tid % kMergeCols, g = tid / kMergeCols;
+  const int d = cb * kMergeCols + cl;
+  const float* ml = part_ml + 2 * bh * num_tiles;
+  const float* pa = part_acc + bh * num_tiles * static_cast<int64_t>(D) + (d < D ? d : 0);
+  float x[TPG];
+#pragma unroll
+  for (int i = 0; i < TPG; ++i) {
+    const int t = g + kMergeGroups * i;
+    x[i] = load_global_raw<float>(pa + static_cast<int64_t>(t < num_tiles ? t : 0) * D);
+  }
+  const uint2 mlr = load_global_u2(ml + 2 * (lane < num_tiles ? lane : 0));
+  const float mt = __uint_as_float(mlr.x), lt = lane < num_tiles ? __uint_as_float(mlr.y) : 0.f;
+  float M = lt > 0.f ? mt : -INFINITY;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, xor_lanes(M, off));
+  const float w = (lt > 0.f && M != -INFINITY) ? fast_exp2(mt - M) : 0.f;
+  const float L = wave_sum(w * lt);
+  float a = 0.f;
+#pragma unroll
+  for (int i = 0; i < TPG; ++i) {
+    const int t = g + kMergeGroups * i;
+    const float wt = __shfl(w, t < kWave ? t : 0, kWave);
+    a = fmaf(t < num_tiles ? wt : 0.f, x[i], a);
+  }
+  colsum[tid] = a;
+  __syncthreads();
+  if (tid < kMergeCols && d < D) {
+    float o = 0.f;
+#pragma unroll
+    for (int j = 0; j < kMergeGroups; ++j) o += colsum[j * kMergeCols + tid];
+    out[bh * D + d] = from_f32<T>(L > 0.f ? o / L : 0.f);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Chunk summaries (chunk_mean, hybrid_attention/reference.py:40-45).
 // ---------------------------------------------------------------------------
@@ -553,6 +608,12 @@ int csa_decode_impl(const void* q, const void* k, const void* v, const void* idx
                                              static_cast<int>(top_k), static_cast<int>(chunk), tl,
                                              static_cast<int>(tiles), stream);
     if (rc != CSAHCA_OK) return rc;
+    if (tiles <= kMergeColTiles) {
+      const int64_t cbs = ceil_div(D, kMergeCols);
+      return launch("csa_merge_cols_kernel", csa_merge_cols_kernel<T>, dim3(static_cast<uint32_t>(bh * cbs)),
+                    dim3(256), 0, stream, static_cast<const float*>(part_ml), static_cast<const float*>(part_acc),
+                    static_cast<T*>(out), static_cast<int>(D), static_cast<int>(tiles), static_cast<int>(cbs));
+    }
     return launch("csa_merge_kernel", csa_merge_kernel<T>, dim3(static_cast<uint32_t>(bh)), dim3(256), 0,
                   stream, static_cast<const float*>(part_ml), static_cast<const float*>(part_acc),
                   static_cast<T*>(out), static_cast<int>(D), static_cast<int>(tiles));
