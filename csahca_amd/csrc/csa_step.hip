@@ -50,6 +50,7 @@ constexpr int kStepMaxP = 64;
 constexpr int kStepMaxK = 1024;
 constexpr int kStepScoreUnroll = 8;   // summary rows per lane per batch of loads
 constexpr int kStepAttendUnroll = 4;  // K/V row loads per lane per batch
+constexpr int kRegMergeP = 8;         // partials per head merged from registers
 constexpr size_t kStepLds = 64 * 1024;
 constexpr uint32_t kSpinLimit = 1u << 20;
 
@@ -339,9 +340,70 @@ __global__ __launch_bounds__(kStepThreads) void csa_step_kernel(StepParams a) {
     put_tagged(pp + 1, tag, __float_as_uint(Lsum));
   }
   if (p != 0) return;
+  const uint64_t* ph = a.part + h * P * static_cast<int64_t>(D + 2);
+  if (P <= kRegMergeP) {
+    // Few partials: the thread of column d gathers every (m_j, l_j) and its
+    // acc_j[d] itself -- one batch of tagged loads (partials past P re-read
+    // partial 0, columns past D re-read column 0; both dropped) -- and forms
+    // the weights and its column: no LDS and no barrier.  Partials are
+    // combined in the same order and with the same operations as below.
+    const int dd = d < D ? d : 0;
+    uint64_t wm[kRegMergeP], wl[kRegMergeP], wa[kRegMergeP];
+#pragma unroll
+    for (int j = 0; j < kRegMergeP; ++j) {
+      const uint64_t* pj = ph + static_cast<int64_t>(j < P ? j : 0) * (D + 2);
+      wm[j] = get_raw(pj);
+      wl[j] = get_raw(pj + 1);
+      wa[j] = get_raw(pj + 2 + dd);
+    }
+    // Words not yet tagged are re-read all together, one round trip per
+    // round (a word-by-word wait would cost a round trip per late word).
+    for (uint32_t it = 0;; ++it) {
+      bool ready = true;
+#pragma unroll
+      for (int j = 0; j < kRegMergeP; ++j)
+        ready = ready && static_cast<uint32_t>(wm[j] >> 32) == tag && static_cast<uint32_t>(wl[j] >> 32) == tag &&
+                static_cast<uint32_t>(wa[j] >> 32) == tag;
+      if (ready) break;
+      if (it >= kSpinLimit) {
+        __hip_atomic_fetch_or(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+      for (int j = 0; j < kRegMergeP; ++j) {
+        const uint64_t* pj = ph + static_cast<int64_t>(j < P ? j : 0) * (D + 2);
+        wm[j] = get_raw(pj);
+        wl[j] = get_raw(pj + 1);
+        wa[j] = get_raw(pj + 2 + dd);
+      }
+    }
+    float mj[kRegMergeP], lj[kRegMergeP], aj[kRegMergeP];
+#pragma unroll
+    for (int j = 0; j < kRegMergeP; ++j) {
+      mj[j] = __uint_as_float(static_cast<uint32_t>(wm[j]));
+      lj[j] = __uint_as_float(static_cast<uint32_t>(wl[j]));
+      aj[j] = __uint_as_float(static_cast<uint32_t>(wa[j]));
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kRegMergeP; ++j)
+      if (j < P && lj[j] > 0.f) mx = fmaxf(mx, mj[j]);
+    float LL = 0.f, AA = 0.f;
+#pragma unroll
+    for (int j = 0; j < kRegMergeP; ++j) {
+      const float w = (j < P && lj[j] > 0.f && mx != -INFINITY) ? fast_exp2(mj[j] - mx) : 0.f;
+      LL = fmaf(w, lj[j], LL);
+      AA = fmaf(w, aj[j], AA);
+    }
+    if (d < D) out[d] = from_f32<T>(LL > 0.f ? AA / LL : 0.f);
+    // Every workgroup of the head has published, so each read this launch's
+    // epoch long ago: the next launch's tags can start.
+    if (tid == 0) __hip_atomic_store(&a.epoch[h], tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
   // Gather all P partials ((m, l, acc[D]) each) into LDS in one batch of loads
   // spread over the 256 threads, then merge from LDS.
-  const uint64_t* ph = a.part + h * P * static_cast<int64_t>(D + 2);
   float* pb = reinterpret_cast<float*>(keys_l);
   const int nw = P * (D + 2);
   for (int i0 = tid; i0 < nw; i0 += kStepThreads * kGather) {
