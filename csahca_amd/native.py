@@ -364,6 +364,11 @@ _ACTIVATIONS = {None: 0, "silu": 1, "gelu": 2}
 _BLOCK_DTYPES = (torch.bfloat16, torch.float16)
 
 
+def _overlaps(a: torch.Tensor, b: torch.Tensor) -> bool:
+    a0, b0 = a.data_ptr(), b.data_ptr()
+    return a.device == b.device and a0 < b0 + b.numel() * b.element_size() and b0 < a0 + a.numel() * a.element_size()
+
+
 def block_linear_supported(x: torch.Tensor, weight: torch.Tensor) -> bool:
     """Shapes and types block_linear takes (others use torch's linear)."""
     B, K = x.shape
@@ -378,6 +383,7 @@ def block_linear(x, weight, *, norm_weight=None, eps: float = 1e-6, activation=N
     x [batch <= 4, in_features] (bf16/f16), rounded like the torch ops it
     replaces: x' = x or RMSNorm(x; norm_weight, eps); activation None, "silu"
     or "gelu" (exact); residual and base [batch, out_features], each optional.
+    ``out`` may be ``residual`` or ``base`` itself, never ``x``.
     ``advance_pos`` (int64 CUDA tensor) is incremented by one after the
     product.  Returns ``out`` [batch, out_features]."""
     _check(x.is_cuda and weight.is_cuda, "x and weight must be CUDA tensors")
@@ -403,6 +409,7 @@ def block_linear(x, weight, *, norm_weight=None, eps: float = 1e-6, activation=N
             out = torch.empty((B, N), dtype=x.dtype, device=x.device)
         _check(out.dtype == x.dtype and out.is_contiguous() and tuple(out.shape) == (B, N),
                "out must be a contiguous [batch, out_features] tensor of x's dtype")
+        _check(not _overlaps(out, x), "out must not overlap x")
         _rc(lib().csahca_block_linear(_ptr(x), _ptr(norm_weight), float(eps), _ptr(weight), _ACTIVATIONS[activation],
                                       _ptr(residual), _ptr(base), float(alpha), _ptr(out), _DTYPES[x.dtype], B, N,
                                       K, _ptr(advance_pos), _stream()))

@@ -280,9 +280,11 @@ enum csahca_activation { CSAHCA_ACT_NONE = 0, CSAHCA_ACT_SILU = 1, CSAHCA_ACT_GE
  * norm_weight the RMSNorm x * rsqrt(mean(x^2) + eps) * norm_weight; then the
  * product; then the activation (SiLU, or exact GELU 0.5 v (1 + erf(v/sqrt 2)));
  * then + residual if given; then base + alpha * (.) if base is given
- * (residual and base are [batch, out_features]).  With advance_pos,
- * *advance_pos (int64, device) is incremented by one after the product (the
- * last kernel of a decode step). */
+ * (residual and base are [batch, out_features]).  y may be the same buffer as
+ * residual or base (each element is read by the thread that writes it, before
+ * the write) but must not overlap x.  With advance_pos, *advance_pos (int64,
+ * device) is incremented by one after the product (the last kernel of a
+ * decode step). */
 int csahca_block_linear(const void* x, const void* norm_weight, double eps, const void* weight, int activation,
                         const void* residual, const void* base, double alpha, void* y, int dtype,
                         int64_t batch, int64_t out_features, int64_t in_features, int64_t* advance_pos,

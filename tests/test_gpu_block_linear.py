@@ -159,3 +159,14 @@ def test_block_qkv_position_outside_the_cache_writes_no_kv():
         assert torch.equal(kc, k0) and torch.equal(vc, v0)
     ref = ref_linear(hidden.cpu(), w.cpu(), dtype).view(B, 3, H, D)
     assert_close(q, ref[:, 0], "q")
+
+
+def test_block_linear_output_may_alias_residual_but_not_x():
+    x, w, _, res = operands(2, 256, 256, torch.bfloat16, seed=9, norm=False, residual=True)
+    x, w, res = x.to(DEV), w.to(DEV), res.to(DEV)
+    want = native.block_linear(x, w, residual=res)
+    buf = res.clone()
+    got = native.block_linear(x, w, residual=buf, out=buf)
+    assert got.data_ptr() == buf.data_ptr() and torch.equal(buf, want)
+    with pytest.raises(RuntimeError, match="must not overlap x"):
+        native.block_linear(x, w, out=x)
