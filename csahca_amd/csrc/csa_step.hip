@@ -103,7 +103,7 @@ __device__ __forceinline__ uint32_t wait_tagged(const uint64_t* p, uint64_t w, u
   return static_cast<uint32_t>(w);
 }
 
-template <typename T, int D, int TOPK_M>
+template <typename T, int D, int TOPK_M, bool POS>
 __global__ __launch_bounds__(kStepThreads) void csa_step_kernel(StepParams a) {
   using L = AttendLayout<T, D>;
   constexpr int VEC = L::VEC, LPR = L::LPR, RPL = L::RPL;
@@ -134,12 +134,13 @@ __global__ __launch_bounds__(kStepThreads) void csa_step_kernel(StepParams a) {
   // Chunks in play: the host's count, or the device's (its load overlaps the
   // summary loads of phase A, which are laid out over the Cs rows), or the
   // count implied by the device position of the token just appended.
-  int64_t C = a.c_dev ? min<int64_t>(max<int32_t>(*a.c_dev, 0), Cs) : a.C;
+  // (POS: the position mode, a separate instantiation so that the count
+  // modes compile without it.)
+  int64_t C = POS ? Cs : (a.c_dev ? min<int64_t>(max<int32_t>(*a.c_dev, 0), Cs) : a.C);
   // Position mode: the count is set in phase A, after its loads are issued
-  // (the position is requested with them); keys stand in as the address of
-  // the unused load otherwise.
-  const int64_t pos_raw =
-      load_global_raw<int64_t>(a.pos_dev ? static_cast<const void*>(a.pos_dev) : static_cast<const void*>(a.keys));
+  // (the position is requested with them).
+  int64_t pos_raw = 0;
+  if constexpr (POS) pos_raw = load_global_raw<int64_t>(a.pos_dev);
   const T* __restrict__ q = static_cast<const T*>(a.q) + h * D;
 
   // Loads that depend on nothing are issued together, unconditionally, and
@@ -176,7 +177,7 @@ __global__ __launch_bounds__(kStepThreads) void csa_step_kernel(StepParams a) {
       }
       uint32_t ep = epoch;
       asm volatile("" : "+v"(ep));
-      if (a.pos_dev) {
+      if constexpr (POS) {
         // The token at pos was just appended: n = pos + 1 tokens, C complete
         // chunks.  If it completes chunk C - 1 and this block of rows holds
         // that row, wavefront 0 builds the row first -- through the summary
@@ -588,8 +589,11 @@ int decode_step_impl(const void* q, const void* k_cache, const void* v_cache, co
         return fail(CSAHCA_ERR_ARGUMENT, "unreachable");
       } else {
         const int m = topk_regs_for(num_chunks, k);
-#define CSAHCA_STEP_LAUNCH(DD, MM) \
-  return launch("csa_step_kernel", csa_step_kernel<T, DD, MM>, grid, dim3(kStepThreads), lds, stream, pr)
+#define CSAHCA_STEP_LAUNCH(DD, MM)                                                                          \
+  return pos_dev ? launch("csa_step_kernel", csa_step_kernel<T, DD, MM, true>, grid, dim3(kStepThreads), lds, \
+                          stream, pr)                                                                        \
+                 : launch("csa_step_kernel", csa_step_kernel<T, DD, MM, false>, grid, dim3(kStepThreads), lds, \
+                          stream, pr)
 #define CSAHCA_STEP_BY_M(DD)                          \
   if (m == 8) CSAHCA_STEP_LAUNCH(DD, 8);             \
   if (m == 32) CSAHCA_STEP_LAUNCH(DD, 32);           \
