@@ -538,7 +538,7 @@ int decode_step_impl(const void* q, const void* k_cache, const void* v_cache, co
   // Workgroups per head: the smallest P at which every wavefront streams its
   // share of summary rows and of selected K/V rows in ONE batch of loads (a
   // dependent HBM round trip, ~1.5 us, costs more than the cross-workgroup
-  // exchange a larger P adds), capped at ~4 workgroups per CU over the grid.
+  // exchange a larger P adds), capped at ~2 workgroups per CU over the grid.
   int64_t P = env_wgs_per_head();
   if (P == 0 && ncu > 0) {
     const int64_t esz = dtype == CSAHCA_F32 ? 4 : 2;
@@ -546,7 +546,7 @@ int decode_step_impl(const void* q, const void* k_cache, const void* v_cache, co
     const int64_t attend_rows =
         int64_t{kStepWaves} * kStepAttendUnroll * std::max<int64_t>(1, kWave / (head_dim / (16 / esz)));
     P = std::max(ceil_div(num_chunks, score_rows), ceil_div(k * chunk_size, attend_rows));
-    P = std::min<int64_t>(P, std::max<int64_t>(1, (4 * static_cast<int64_t>(ncu)) / std::max<int64_t>(bh, 1)));
+    P = std::min<int64_t>(P, std::max<int64_t>(1, (2 * static_cast<int64_t>(ncu)) / std::max<int64_t>(bh, 1)));
   }
   P = std::min<int64_t>({P, kStepMaxP, ceil_div(num_chunks, 8), ceil_div(k * chunk_size, 16)});
   P = std::max<int64_t>(1, P);
