@@ -76,6 +76,10 @@ _SIGNATURES = {
 EXPORTED = tuple(_SIGNATURES)
 
 
+# ABI revision of include/csahca.h that these signatures follow.
+ABI_VERSION = 1
+
+
 def library_path() -> Path:
     return _LIB_PATH
 
@@ -92,6 +96,9 @@ def lib():
             fn = getattr(handle, name)
             fn.restype = res
             fn.argtypes = args
+        got = handle.csahca_abi_version()
+        if got != ABI_VERSION:
+            raise RuntimeError(f"{_LIB_PATH} has ABI revision {got}, this binding expects {ABI_VERSION}; rebuild it")
         _LIB = handle
     return _LIB
 

@@ -32,7 +32,7 @@ def test_exports_every_header_symbol(lib):
     for s in syms:
         assert hasattr(raw, s), s
     assert set(syms) == set(native.EXPORTED)
-    assert lib.csahca_abi_version() == 1
+    assert lib.csahca_abi_version() == native.ABI_VERSION == 1
 
 
 def test_workspace_sizes(lib):
