@@ -30,6 +30,7 @@
 // set and the kernel still completes).
 // The workspace must be zero before the first launch.
 #include "csa_device.hpp"
+#include "hca_device.hpp"
 
 #include <algorithm>
 #include <climits>
@@ -41,6 +42,9 @@ namespace csahca {
 int csa_select_launch(const void* q, const float* summary, int32_t* out_indices, int dtype,
                       int64_t bh, int64_t C, int64_t D, int64_t k, uint32_t* keys,
                       hipStream_t stream);
+int hca_merge_launch(int dtype, void* workspace, const void* blend_src, double blend_weight, void* out,
+                     int64_t bh, int64_t C, int D, hipStream_t stream);
+size_t hca_workspace_means_offset(int64_t n_scores);
 
 namespace {
 
@@ -104,7 +108,7 @@ __device__ __forceinline__ uint32_t wait_tagged(const uint64_t* p, uint64_t w, u
 }
 
 template <typename T, int D, int TOPK_M, bool POS>
-__global__ __launch_bounds__(kStepThreads) void csa_step_kernel(StepParams a) {
+__device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
   using L = AttendLayout<T, D>;
   constexpr int VEC = L::VEC, LPR = L::LPR, RPL = L::RPL;
   constexpr int SLPR = D / 4, SRPL = kWave / SLPR;  // fp32 summary rows
@@ -128,8 +132,8 @@ __global__ __launch_bounds__(kStepThreads) void csa_step_kernel(StepParams a) {
   const int wave = tid / kWave;
   const int lane = tid % kWave;
   const int P = a.P;
-  const int64_t h = blockIdx.x / P;
-  const int p = static_cast<int>(blockIdx.x % P);
+  const int64_t h = block / P;
+  const int p = static_cast<int>(block % P);
   const int64_t Cs = a.Cs;
   // Chunks in play: the host's count, or the device's (its load overlaps the
   // summary loads of phase A, which are laid out over the Cs rows), or the
@@ -447,6 +451,47 @@ __global__ __launch_bounds__(kStepThreads) void csa_step_kernel(StepParams a) {
   if (tid == 0) __hip_atomic_store(&a.epoch[h], tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+template <typename T, int D, int TOPK_M, bool POS>
+__global__ __launch_bounds__(kStepThreads) void csa_step_kernel(StepParams a) {
+  csa_step_body<T, D, TOPK_M, POS>(a, blockIdx.x);
+}
+
+// The hybrid step: blocks [0, step_blocks) run the decode step above, the rest
+// the HCA chunk pass over per_block consecutive chunk items each.  The two are
+// independent until the HCA merge (a later launch, which also blends), so the
+// latency-bound step runs beside the bandwidth-bound chunk stream.  Step blocks
+// come first: they wait only on each other, and they are dispatched first.
+struct HcaPart {
+  const void* q;
+  const void* k;
+  const void* v;
+  float* scores;
+  float* means;
+  int64_t S;
+  int64_t C;
+  int64_t items;
+  int chunk;
+  int per_block;
+  float scale;
+};
+
+template <typename T, int D, int TOPK_M>
+__global__ __launch_bounds__(kStepThreads) void csa_hybrid_kernel(StepParams a, HcaPart hp, uint32_t step_blocks) {
+  static_assert(kStepThreads == kHcaThreads, "one block size for both parts");
+  if (blockIdx.x < step_blocks) {
+    csa_step_body<T, D, TOPK_M, false>(a, blockIdx.x);
+    return;
+  }
+  const int64_t j0 = static_cast<int64_t>(blockIdx.x - step_blocks) * hp.per_block;
+  for (int i = 0; i < hp.per_block; ++i) {
+    const int64_t item = j0 + i;
+    if (item >= hp.items) return;
+    if (i > 0) __syncthreads();  // the previous item's LDS reads are done
+    hca_chunk_body<T, true>(static_cast<const T*>(hp.q), static_cast<const T*>(hp.k), static_cast<const T*>(hp.v),
+                            hp.scores, hp.means, hp.S, D, hp.chunk, hp.C, hp.scale, item);
+  }
+}
+
 int device_cu_count() {
   static int cached[64] = {0};
   int dev = 0;
@@ -505,7 +550,8 @@ int decode_step_impl(const void* q, const void* k_cache, const void* v_cache, co
                      int32_t* out_indices, int dtype, int64_t batch, int64_t heads, int64_t seq_len,
                      int64_t head_dim, int64_t num_chunks, const int32_t* c_dev, const int64_t* pos_dev,
                      int64_t chunk_size, int64_t top_k, void* workspace, size_t workspace_bytes,
-                     void* stream_ptr) {
+                     void* stream_ptr, HcaPart* hybrid = nullptr, size_t hybrid_lds = 0,
+                     bool* hybrid_launched = nullptr) {
   CSAHCA_REQUIRE(valid_dtype(dtype), "q, k_cache and v_cache must be float32, float64, float16 or bfloat16");
   CSAHCA_REQUIRE(batch >= 0 && heads >= 0 && seq_len >= 0 && head_dim >= 0 && num_chunks >= 0,
                  "negative dimension");
@@ -583,6 +629,27 @@ int decode_step_impl(const void* q, const void* k_cache, const void* v_cache, co
     pr.score_scale = 1.0f / sqrtf(static_cast<float>(head_dim));
     pr.qscale = kLog2e / sqrtf(static_cast<float>(head_dim));
     const dim3 grid(static_cast<uint32_t>(bh * P));
+    if (hybrid != nullptr && head_dim == 128 && pos_dev == nullptr &&
+        (dtype == CSAHCA_BF16 || dtype == CSAHCA_F16)) {
+      const int64_t hblocks = ceil_div(hybrid->items, static_cast<int64_t>(hybrid->per_block));
+      CSAHCA_REQUIRE(bh * P + hblocks <= INT32_MAX, "too many blocks in one call");
+      const dim3 g2(static_cast<uint32_t>(bh * P + hblocks));
+      const size_t lds2 = std::max(lds, hybrid_lds);
+      const uint32_t sb = static_cast<uint32_t>(bh * P);
+      const int m = topk_regs_for(num_chunks, k);
+      *hybrid_launched = true;
+#define CSAHCA_HYBRID_LAUNCH(TT, MM) \
+  return launch("csa_hybrid_kernel", csa_hybrid_kernel<TT, 128, MM>, g2, dim3(kStepThreads), lds2, stream, pr, *hybrid, sb)
+      if (dtype == CSAHCA_BF16) {
+        if (m == 8) CSAHCA_HYBRID_LAUNCH(bf16, 8);
+        if (m == 32) CSAHCA_HYBRID_LAUNCH(bf16, 32);
+        CSAHCA_HYBRID_LAUNCH(bf16, 0);
+      }
+      if (m == 8) CSAHCA_HYBRID_LAUNCH(f16, 8);
+      if (m == 32) CSAHCA_HYBRID_LAUNCH(f16, 32);
+      CSAHCA_HYBRID_LAUNCH(f16, 0);
+#undef CSAHCA_HYBRID_LAUNCH
+    }
     return dispatch_dtype(dtype, [&](auto tag) -> int {
       using T = decltype(tag);
       if constexpr (std::is_same_v<T, double>) {
@@ -669,4 +736,57 @@ extern "C" int csahca_csa_step_status(const void* workspace, uint32_t* status_ou
   e = hipStreamSynchronize(stream);
   if (e != hipSuccess) return fail_hip(e, "csahca_csa_step_status");
   return CSAHCA_OK;
+}
+
+extern "C" int csahca_hybrid_decode_forward(const void* q, const void* k_cache, const void* v_cache,
+                                            const float* summary, void* csa_out, int32_t* csa_indices, void* out,
+                                            int dtype, int64_t batch, int64_t heads, int64_t seq_len,
+                                            int64_t head_dim, int64_t num_chunks, int64_t csa_chunk_size,
+                                            int64_t top_k, int64_t hca_chunk_size, double csa_weight,
+                                            void* step_workspace, size_t step_workspace_bytes, void* hca_workspace,
+                                            size_t hca_workspace_bytes, void* stream_ptr) {
+  clear_error();
+  CSAHCA_REQUIRE(valid_dtype(dtype), "q, k_cache and v_cache must be float32, float64, float16 or bfloat16");
+  CSAHCA_REQUIRE(batch >= 0 && heads >= 0 && seq_len >= 0 && head_dim >= 0, "negative dimension");
+  CSAHCA_REQUIRE(hca_chunk_size > 0 && hca_chunk_size <= INT_MAX, "chunk_size must be positive");
+  CSAHCA_REQUIRE(seq_len % hca_chunk_size == 0, "seq length must be divisible by chunk_size");
+  const int64_t bh = batch * heads;
+  if (bh == 0 || head_dim == 0) return CSAHCA_OK;
+  const int64_t Ch = seq_len / hca_chunk_size;
+  if (Ch == 0) return fail(CSAHCA_ERR_ARGUMENT, "seq length must be at least chunk_size");
+  CSAHCA_REQUIRE(bh * Ch <= INT32_MAX, "too many chunks in one call");
+  CSAHCA_REQUIRE(q && k_cache && v_cache && out && csa_out, "null tensor pointer");
+  const size_t need = csahca_hca_decode_workspace_bytes(batch, heads, seq_len, head_dim, hca_chunk_size);
+  if (hca_workspace == nullptr || hca_workspace_bytes < need)
+    return fail(CSAHCA_ERR_WORKSPACE, "workspace too small for hca decode");
+  // One launch for the step and the HCA chunk pass where the fused step runs
+  // (bf16/f16, head_dim 128, 16-byte aligned K/V); otherwise the two ops in
+  // turn.  Each HCA block takes two chunk items, so that with the step's
+  // register count the whole grid is resident at once.
+  const bool aligned = ((reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache)) % 16) == 0;
+  HcaPart hp{};
+  hp.q = q;
+  hp.k = k_cache;
+  hp.v = v_cache;
+  hp.scores = static_cast<float*>(hca_workspace);
+  hp.means = reinterpret_cast<float*>(static_cast<char*>(hca_workspace) + hca_workspace_means_offset(bh * Ch));
+  hp.S = seq_len;
+  hp.C = Ch;
+  hp.items = bh * Ch;
+  hp.chunk = static_cast<int>(hca_chunk_size);
+  hp.per_block = 2;
+  hp.scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(head_dim)));
+  // LDS of the chunk pass at head_dim 128, 16-byte rows: 16 row groups of K and V column sums.
+  const size_t hca_lds = 2 * static_cast<size_t>(kHcaThreads / (128 / 8)) * 128 * sizeof(float);
+  bool fused = false;
+  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  int rc = decode_step_impl(q, k_cache, v_cache, summary, csa_out, csa_indices, dtype, batch, heads, seq_len,
+                            head_dim, num_chunks, nullptr, nullptr, csa_chunk_size, top_k, step_workspace,
+                            step_workspace_bytes, stream_ptr, (aligned && head_dim == 128) ? &hp : nullptr,
+                            hca_lds, &fused);
+  if (rc != CSAHCA_OK) return rc;
+  if (!fused)
+    return csahca_hca_decode_forward(q, k_cache, v_cache, csa_out, csa_weight, out, dtype, batch, heads, seq_len,
+                                     head_dim, hca_chunk_size, hca_workspace, hca_workspace_bytes, stream_ptr);
+  return hca_merge_launch(dtype, hca_workspace, csa_out, csa_weight, out, bh, Ch, static_cast<int>(head_dim), stream);
 }

@@ -21,7 +21,7 @@
 //                     optional blend with a CSA output.  Spreading a head's
 //                     columns over workgroups keeps each one to a single round
 //                     trip of ~C x 128 bytes even at batch 1.
-#include "common.hpp"
+#include "hca_device.hpp"
 
 #include <algorithm>
 #include <climits>
@@ -30,35 +30,8 @@
 namespace csahca {
 namespace {
 
-constexpr int kHcaThreads = 256;
 constexpr int kHcaProbChunk = 2048;  // probabilities staged in LDS per pass
 
-constexpr int kRowBatch = 8;          // rows of K and V in flight per thread
-
-template <typename T>
-__device__ __forceinline__ float round_to(float x) {
-  return to_f32(from_f32<T>(x));
-}
-
-__device__ __forceinline__ float block_reduce(float v, float* red, bool is_max) {
-  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const float o = xor_lanes(v, off);
-    v = is_max ? fmaxf(v, o) : v + o;
-  }
-  __syncthreads();
-  if (lane == 0) red[wave] = v;
-  __syncthreads();
-  float r = red[0];
-#pragma unroll
-  for (int w = 1; w < kHcaThreads / kWave; ++w) r = is_max ? fmaxf(r, red[w]) : r + red[w];
-  return r;
-}
-
-// Thread layout over one chunk: tpr threads per row (each owning VEC-wide
-// column groups, looping when a row has more than 256 groups), R = 256/tpr
-// rows per pass.  LDS: 2 x R x D fp32 row-group sums, then the block reduce.
 template <typename T, bool kVec>
 __global__ __launch_bounds__(kHcaThreads) void hca_chunk_kernel(const T* __restrict__ q,
                                                               const T* __restrict__ k,
@@ -67,103 +40,7 @@ __global__ __launch_bounds__(kHcaThreads) void hca_chunk_kernel(const T* __restr
                                                               float* __restrict__ means, int64_t S,
                                                               int D, int chunk, int64_t C,
                                                               float scale) {
-  constexpr int VEC = kVec ? Vec16<T>::N : 1;
-  extern __shared__ float lds[];
-  __shared__ float red[kHcaThreads / kWave];
-  const int tid = threadIdx.x;
-  const int64_t item = blockIdx.x;
-  const int64_t bh = item / C;
-  const int64_t c = item - bh * C;
-  const int nvc = D / VEC;
-  const int tpr = min(nvc, kHcaThreads);
-  const int R = kHcaThreads / tpr;
-  const int rg = tid / tpr;
-  const int lc = tid - rg * tpr;
-  float* sk = lds;
-  float* sv = lds + static_cast<size_t>(R) * D;
-  const int64_t row0 = bh * S + c * chunk;
-
-  if (rg < R) {
-    for (int vc = lc; vc < nvc; vc += tpr) {
-      float ak[VEC], av[VEC];
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) ak[e] = av[e] = 0.f;
-      const T* kc = k + row0 * D + static_cast<int64_t>(vc) * VEC;
-      const T* vcp = v + row0 * D + static_cast<int64_t>(vc) * VEC;
-      // kRowBatch rows of K and V are requested before any is consumed, so a
-      // thread waits for one HBM round trip per batch rather than per row.
-      // The loads are unconditional (rows past the chunk re-read row r0 and
-      // are zeroed after the load): a load under a per-lane branch would make
-      // the compiler wait for the whole batch before issuing it.
-      for (int r0 = rg; r0 < chunk; r0 += kRowBatch * R) {
-        if constexpr (kVec) {
-          uint4 rk[kRowBatch], rv[kRowBatch];
-#pragma unroll
-          for (int i = 0; i < kRowBatch; ++i) {
-            const int r = r0 + i * R;
-            const int64_t off = static_cast<int64_t>(r < chunk ? r : r0) * D;
-            rk[i] = load_global_u4(kc + off);
-            rv[i] = load_global_u4(vcp + off);
-          }
-          // Keep the scheduler from interleaving the widening below with the
-          // loads (it would wait for the first rows before requesting the rest).
-          __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-          for (int i = 0; i < kRowBatch; ++i) {
-            const bool ok = r0 + i * R < chunk;
-            float xk[VEC], xv[VEC];
-            widen16<T>(rk[i], xk);
-            widen16<T>(rv[i], xv);
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) {
-              ak[e] += ok ? xk[e] : 0.f;
-              av[e] += ok ? xv[e] : 0.f;
-            }
-          }
-        } else {
-          float xk[kRowBatch], xv[kRowBatch];
-#pragma unroll
-          for (int i = 0; i < kRowBatch; ++i) {
-            const int r = r0 + i * R;
-            const int64_t off = static_cast<int64_t>(r < chunk ? r : r0) * D;
-            xk[i] = to_f32(kc[off]);
-            xv[i] = to_f32(vcp[off]);
-          }
-#pragma unroll
-          for (int i = 0; i < kRowBatch; ++i) {
-            if (r0 + i * R < chunk) {
-              ak[0] += xk[i];
-              av[0] += xv[i];
-            }
-          }
-        }
-      }
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        sk[rg * D + vc * VEC + e] = ak[e];
-        sv[rg * D + vc * VEC + e] = av[e];
-      }
-    }
-  }
-  __syncthreads();
-  // Column means, rounded to the storage type; the score partial q . kmean.
-  const float inv_n = 1.f / static_cast<float>(chunk);
-  const T* qp = q + bh * D;
-  float* out = means + item * static_cast<int64_t>(D);
-  float dot = 0.f;
-  for (int d = tid; d < D; d += kHcaThreads) {
-    float a = 0.f, b = 0.f;
-    for (int g = 0; g < R; ++g) {
-      a += sk[g * D + d];
-      b += sv[g * D + d];
-    }
-    const float km = round_to<T>(a * inv_n);
-    const float vm = round_to<T>(b * inv_n);
-    dot = fmaf(to_f32(qp[d]), km, dot);
-    out[d] = vm;
-  }
-  dot = block_reduce(dot, red, false);
-  if (tid == 0) scores[item] = dot * scale;
+  hca_chunk_body<T, kVec>(q, k, v, scores, means, S, D, chunk, C, scale, blockIdx.x);
 }
 
 // Merge thread layout: 32 columns x 8 row groups; a wavefront reads 2 rows of
@@ -337,3 +214,28 @@ extern "C" int csahca_hca_decode_forward(const void* q, const void* k_cache, con
                   static_cast<float>(blend_weight), static_cast<T*>(out), C, D, col_blocks);
   });
 }
+
+namespace csahca {
+
+// The HCA merge (+ optional blend) from a workspace a chunk pass of shape
+// (bh, C, D) filled; used by the hybrid step, which runs the chunk pass inside
+// its own kernel.
+int hca_merge_launch(int dtype, void* workspace, const void* blend_src, double blend_weight, void* out,
+                     int64_t bh, int64_t C, int D, hipStream_t stream) {
+  const float* scores = static_cast<const float*>(workspace);
+  const float* means =
+      reinterpret_cast<const float*>(static_cast<const char*>(workspace) + hca_means_offset(bh * C));
+  const int col_blocks = (D + kMergeCols - 1) / kMergeCols;
+  CSAHCA_REQUIRE(bh * col_blocks <= INT32_MAX, "too many heads in one call");
+  return dispatch_dtype(dtype, [&](auto tag) -> int {
+    using T = decltype(tag);
+    return launch("hca_merge_kernel", hca_merge_kernel<T>, dim3(static_cast<uint32_t>(bh * col_blocks)),
+                  dim3(kHcaThreads), 0, stream, scores, means, static_cast<const T*>(blend_src),
+                  static_cast<float>(blend_weight), static_cast<T*>(out), C, D, col_blocks);
+  });
+}
+
+// Byte offset of the V means in an HCA workspace holding n chunk scores.
+size_t hca_workspace_means_offset(int64_t n_scores) { return hca_means_offset(n_scores); }
+
+}  // namespace csahca

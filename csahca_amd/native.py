@@ -64,6 +64,8 @@ _SIGNATURES = {
     "csahca_hca_decode_workspace_bytes": (_sz, [_i64] * 5),
     "csahca_dsv4_pack_tokens": (_int, [_vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp]),
     "csahca_hca_decode_forward": (_int, [_vp, _vp, _vp, _vp, _dbl, _vp, _int] + [_i64] * 5 + [_vp, _sz, _vp]),
+    "csahca_hybrid_decode_forward": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _int] + [_i64] * 8 + [_dbl] +
+                                     [_vp, _sz, _vp, _sz, _vp]),
     "csahca_block_linear": (_int, [_vp, _vp, _dbl, _vp, _int, _vp, _vp, _dbl, _vp, _int, _i64, _i64, _i64, _vp,
                                    _vp]),
     "csahca_block_qkv": (_int, [_vp, _vp, _dbl, _vp, _vp, _vp, _vp, _vp, _vp, _int] + [_i64] * 5 + [_vp]),
@@ -537,8 +539,28 @@ def hybrid_decode_forward(q, k_cache, v_cache, *, csa_chunk_size: int, csa_top_k
     ``summary`` is None) blended with HCA at ``csa_weight``."""
     if summary is None:
         summary = csa_chunk_summary(k_cache, csa_chunk_size)
-    csa_out, _idx = csa_decode_step(q, k_cache, v_cache, summary, csa_chunk_size, csa_top_k)
-    return hca_decode_forward(q, k_cache, v_cache, hca_chunk_size, blend=csa_out, csa_weight=csa_weight)
+    csa_chunk_size, csa_top_k, hca_chunk_size = int(csa_chunk_size), int(csa_top_k), int(hca_chunk_size)
+    _csa_checks(q, k_cache, v_cache, torch.empty((q.shape[0], q.shape[1], 0), dtype=torch.int32, device=q.device),
+                csa_chunk_size, tiled=False)
+    _check(summary.is_cuda and summary.is_contiguous() and summary.dtype == torch.float32 and summary.dim() == 4,
+           "summary must be a contiguous fp32 [batch, heads, chunks, head_dim] CUDA tensor")
+    B, H, S, D = k_cache.shape
+    _check(tuple(summary.shape[:2]) == (B, H) and summary.shape[3] == D, "summary shape must match q")
+    C = summary.shape[2]
+    _check(csa_top_k >= 0, "top_k must be non-negative")
+    k = min(csa_top_k, C)
+    with torch.cuda.device(q.device):
+        out = torch.empty_like(q)
+        csa_out = torch.empty_like(q)
+        idx = torch.empty((B, H, k), dtype=torch.int32, device=q.device)
+        sws = _step_workspace(lib().csahca_csa_step_workspace_bytes(B, H, C, D, csa_top_k, csa_chunk_size), q.device,
+                              (B * H, C, D, k, csa_chunk_size))
+        hws = _workspace(lib().csahca_hca_decode_workspace_bytes(B, H, S, D, hca_chunk_size), q.device)
+        _rc(lib().csahca_hybrid_decode_forward(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(summary), _ptr(csa_out),
+                                               _ptr(idx), _ptr(out), _DTYPES[q.dtype], B, H, S, D, C, csa_chunk_size,
+                                               csa_top_k, hca_chunk_size, float(csa_weight), _ptr(sws), sws.numel(),
+                                               _ptr(hws), hws.numel(), _stream()))
+    return out
 
 
 # ---------------------------------------------------------------------------

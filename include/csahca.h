@@ -201,6 +201,23 @@ int csahca_hca_decode_forward(const void* q, const void* k_cache, const void* v_
                               int64_t chunk_size, void* workspace, size_t workspace_bytes,
                               void* stream);
 
+/* Replaces hybrid_reference (hybrid_attention/reference.py:95-108): the CSA
+ * decode step of csahca_csa_decode_step (selection from `summary`, chunk
+ * csa_chunk_size, top_k; its output to csa_out [B,H,D] and its chunk ids to
+ * csa_indices [B,H,min(top_k,num_chunks)]) blended with csahca_hca_decode_forward
+ * at hca_chunk_size: out = round(round(w*csa) + round((1-w)*hca)), w =
+ * csa_weight.  Where the fused step runs (bf16/f16, head_dim 128, 16-byte
+ * aligned tensors) the step and the HCA chunk pass share one launch, the step
+ * in the first blocks; otherwise the two ops run in turn.  step_workspace
+ * follows csahca_csa_decode_step's rules (zeroed once, reused, one stream);
+ * hca_workspace is sized by csahca_hca_decode_workspace_bytes. */
+int csahca_hybrid_decode_forward(const void* q, const void* k_cache, const void* v_cache, const float* summary,
+                                 void* csa_out, int32_t* csa_indices, void* out, int dtype, int64_t batch,
+                                 int64_t heads, int64_t seq_len, int64_t head_dim, int64_t num_chunks,
+                                 int64_t csa_chunk_size, int64_t top_k, int64_t hca_chunk_size, double csa_weight,
+                                 void* step_workspace, size_t step_workspace_bytes, void* hca_workspace,
+                                 size_t hca_workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------- */
 /* DSV4: MQA decode over the paged FP8 latent cache                           */
 /* ------------------------------------------------------------------------- */

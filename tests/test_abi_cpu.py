@@ -142,6 +142,24 @@ def test_device_state_entry_points_argument_errors(lib):
     assert summ_at(C=0) == 0  # no summary rows: nothing to write
 
 
+def test_hybrid_argument_errors(lib):
+    """csahca_hybrid_decode_forward checks its HCA half before anything runs."""
+    def hyb(**o):
+        a = dict(q=1, k=1, v=1, summ=1, csa=1, idx=1, out=1, dtype=2, B=1, H=1, S=512, D=128, C=8, cc=64, top_k=4,
+                 hc=256, w=0.7, sws=None, swsb=0, hws=None, hwsb=0)
+        a.update(o)
+        return lib.csahca_hybrid_decode_forward(a["q"], a["k"], a["v"], a["summ"], a["csa"], a["idx"], a["out"],
+                                                a["dtype"], a["B"], a["H"], a["S"], a["D"], a["C"], a["cc"],
+                                                a["top_k"], a["hc"], a["w"], a["sws"], a["swsb"], a["hws"], a["hwsb"],
+                                                None)
+
+    assert hyb(hc=300) == 1 and lib.csahca_last_error().decode() == "seq length must be divisible by chunk_size"
+    assert hyb(hc=0) == 1 and lib.csahca_last_error().decode() == "chunk_size must be positive"
+    assert hyb(csa=None) == 1 and lib.csahca_last_error().decode() == "null tensor pointer"
+    assert hyb() == 2 and lib.csahca_last_error().decode() == "workspace too small for hca decode"
+    assert hyb(B=0) == 0
+
+
 def test_block_product_argument_errors(lib):
     """csahca_block_linear / csahca_block_qkv reject bad arguments before any
     HIP call (dummy pointers are never dereferenced)."""

@@ -119,6 +119,54 @@ def test_hybrid_weight_one_is_csa_and_zero_is_hca():
                                                     csa_weight=0.0, summary=summ), hca)
 
 
+@pytest.mark.parametrize("B,H,S,D,dtype", [
+    (1, 8, 8192, 128, torch.bfloat16),   # one launch: step blocks + HCA chunk blocks
+    (1, 3, 4352, 128, torch.float16),    # one launch, 51 chunk items: the last HCA block takes one
+    (1, 2, 4096, 128, torch.float32),    # fp32: the two ops in turn
+    (1, 4, 4096, 64, torch.bfloat16),    # head_dim 64: the two ops in turn
+])
+def test_hybrid_equals_the_two_ops_in_turn(B, H, S, D, dtype):
+    """csahca_hybrid_decode_forward gives exactly the bits of the CSA decode
+    step followed by the blended HCA op, fused into one launch or not."""
+    q, k, v = (t.to(DEV) for t in inputs(B, H, S, D, dtype, seed=B * 17 + H + D))
+    summ = native.csa_chunk_summary(k, 64)
+    csa, _ = native.csa_decode_step(q, k, v, summ, 64, 8)
+    want = native.hca_decode_forward(q, k, v, 256 if S % 256 == 0 else 128, blend=csa, csa_weight=0.7)
+    got = native.hybrid_decode_forward(q, k, v, csa_chunk_size=64, csa_top_k=8,
+                                       hca_chunk_size=256 if S % 256 == 0 else 128, summary=summ)
+    assert torch.equal(got, want)
+    assert all(x == 0 for x in native.csa_step_status().values())
+
+
+def test_hybrid_graph_replays_match_eager():
+    """The hybrid launch captured in a HIP graph: every replay (with eager work
+    and synchronisations between replays) equals the eager result."""
+    q, k, v = (t.to(DEV) for t in inputs(1, 8, 8192, 128, torch.bfloat16, seed=13))
+    summ = native.csa_chunk_summary(k, 64)
+
+    def run():
+        return native.hybrid_decode_forward(q, k, v, csa_chunk_size=64, csa_top_k=8, hca_chunk_size=256,
+                                            summary=summ)
+
+    want = run()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        got = run()
+    for i in range(5):
+        got.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), i
+        run()
+        torch.cuda.synchronize()
+
+
 def test_hca_rejects_ragged_sequence_with_reference_message():
     q, k, v = (t.to(DEV) for t in inputs(1, 1, 100, 64, torch.bfloat16, seed=0))
     with pytest.raises(RuntimeError, match="seq length must be divisible by chunk_size"):
