@@ -119,21 +119,25 @@ def test_hybrid_weight_one_is_csa_and_zero_is_hca():
                                                     csa_weight=0.0, summary=summ), hca)
 
 
-@pytest.mark.parametrize("B,H,S,D,dtype", [
-    (1, 8, 8192, 128, torch.bfloat16),   # one launch: step blocks + HCA chunk blocks
-    (1, 3, 4352, 128, torch.float16),    # one launch, 51 chunk items: the last HCA block takes one
-    (1, 2, 4096, 128, torch.float32),    # fp32: the two ops in turn
-    (1, 4, 4096, 64, torch.bfloat16),    # head_dim 64: the two ops in turn
+@pytest.mark.parametrize("B,H,S,D,dtype,top_k", [
+    (1, 8, 8192, 128, torch.bfloat16, 8),    # one launch: step blocks + HCA chunk blocks
+    (1, 8, 32768, 128, torch.bfloat16, 8),   # the headline shape
+    (4, 8, 8192, 128, torch.bfloat16, 32),   # 32 heads, top-32
+    (1, 2, 65536, 128, torch.bfloat16, 8),   # 1024 summary rows (the 32-keys-per-lane top-k)
+    (1, 3, 4352, 128, torch.float16, 8),     # one launch, 51 chunk items: the last HCA block takes one
+    (1, 2, 4096, 128, torch.float32, 8),     # fp32: the two ops in turn
+    (1, 4, 4096, 64, torch.bfloat16, 8),     # head_dim 64: the two ops in turn
 ])
-def test_hybrid_equals_the_two_ops_in_turn(B, H, S, D, dtype):
+def test_hybrid_equals_the_two_ops_in_turn(B, H, S, D, dtype, top_k):
     """csahca_hybrid_decode_forward gives exactly the bits of the CSA decode
     step followed by the blended HCA op, fused into one launch or not."""
     q, k, v = (t.to(DEV) for t in inputs(B, H, S, D, dtype, seed=B * 17 + H + D))
     summ = native.csa_chunk_summary(k, 64)
-    csa, _ = native.csa_decode_step(q, k, v, summ, 64, 8)
-    want = native.hca_decode_forward(q, k, v, 256 if S % 256 == 0 else 128, blend=csa, csa_weight=0.7)
-    got = native.hybrid_decode_forward(q, k, v, csa_chunk_size=64, csa_top_k=8,
-                                       hca_chunk_size=256 if S % 256 == 0 else 128, summary=summ)
+    csa, _ = native.csa_decode_step(q, k, v, summ, 64, top_k)
+    hc = 256 if S % 256 == 0 else 128
+    want = native.hca_decode_forward(q, k, v, hc, blend=csa, csa_weight=0.7)
+    got = native.hybrid_decode_forward(q, k, v, csa_chunk_size=64, csa_top_k=top_k, hca_chunk_size=hc,
+                                       summary=summ)
     assert torch.equal(got, want)
     assert all(x == 0 for x in native.csa_step_status().values())
 
