@@ -728,6 +728,11 @@ def main():
         if args.sweep_out is not None:
             args.sweep_out.parent.mkdir(parents=True, exist_ok=True)
             args.sweep_out.write_text(json.dumps(rows, indent=1) + "\n")
+    bad = {str(k): v for k, v in native.csa_step_status().items() if v}
+    if bad:
+        print(f"bench.py: a decode-step exchange timed out (status words {bad}); results are invalid",
+              file=sys.stderr)
+        sys.exit(3)
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)

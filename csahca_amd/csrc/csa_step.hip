@@ -26,16 +26,22 @@
 // own.  The tag is this launch's number for the head (epoch[h] + 1, read at
 // entry; the merging workgroup publishes it as the new epoch when done), so a
 // reader accepts a word only once it belongs to the current launch and needs no
-// separate ordering; every wait is bounded (on time-out a sticky status bit is
-// set and the kernel still completes).
-// The workspace must be zero before the first launch.
+// separate ordering.  Every wait is bounded.  On time-out a sticky status bit
+// is set, the head's output is NaN and its epoch becomes kPoisonEpoch: a
+// partner that had not started could otherwise publish words a later launch
+// would take for its own, so every later launch on a poisoned head skips its
+// waits and writes NaN, until the workspace is zero-filled again.
+// The workspace must be zero before the first launch and whenever the problem
+// shape (B*H, chunks, head_dim, top_k, chunk) changes.
 #include "csa_device.hpp"
 #include "hca_device.hpp"
 
 #include <algorithm>
 #include <climits>
 #include <cstdlib>
+#include <mutex>
 #include <type_traits>
+#include <vector>
 
 namespace csahca {
 
@@ -57,6 +63,15 @@ constexpr int kStepAttendUnroll = 4;  // K/V row loads per lane per batch
 constexpr int kRegMergeP = 8;         // partials per head merged from registers
 constexpr size_t kStepLds = 64 * 1024;
 constexpr uint32_t kSpinLimit = 1u << 20;
+constexpr uint32_t kPoisonEpoch = 0xffffffffu;  // a head whose exchange timed out (see above)
+
+// This launch's tag for a head whose epoch word reads `epoch` (never the
+// poison value; after 2^32 - 2 launches the sequence restarts at 1, and every
+// exchanged word is rewritten by each launch, so no stale word carries it).
+__device__ __forceinline__ uint32_t launch_tag(uint32_t epoch) {
+  const uint32_t t = epoch + 1u;
+  return t == kPoisonEpoch ? 1u : t;
+}
 
 struct StepParams {
   const void* q;
@@ -67,8 +82,10 @@ struct StepParams {
   int32_t* idx_out;
   uint32_t* status;
   uint32_t* epoch;     // [BH]
-  uint64_t* keys;      // [BH][C] tagged keys
-  uint64_t* part;      // [BH][P][D + 2] tagged partials (m, l, acc[D])
+  uint64_t* keys;      // head h's tagged keys at h * key_stride
+  uint64_t* part;      // head h's tagged partials (m, l, acc[D]) at h * part_stride + p * (D + 2)
+  int64_t key_stride;
+  int64_t part_stride;
   int64_t S;
   int64_t C;            // chunks in play (when c_dev is null)
   int64_t Cs;           // summary / key rows per head (C <= Cs)
@@ -93,14 +110,19 @@ __device__ __forceinline__ uint64_t get_raw(const uint64_t* p) {
   return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Wait (bounded) until *p carries `tag`; returns its value bits.
-__device__ __forceinline__ uint32_t wait_tagged(const uint64_t* p, uint64_t w, uint32_t tag, uint32_t* status) {
+// Wait (bounded) until *p carries `tag`; returns its value bits.  On time-out
+// the sticky status bit is set and `bad` is raised: the caller poisons what it
+// computes from the word (the head's output becomes NaN and the head is
+// poisoned), so a lost partner never yields a plausible-looking result.
+__device__ __forceinline__ uint32_t wait_tagged(const uint64_t* p, uint64_t w, uint32_t tag, uint32_t* status,
+                                                bool& bad) {
   uint32_t it = 0;
   while (static_cast<uint32_t>(w >> 32) != tag) {
     __builtin_amdgcn_s_sleep(1);
     w = get_raw(p);
     if (++it > kSpinLimit) {
       __hip_atomic_fetch_or(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      bad = true;
       break;
     }
   }
@@ -119,8 +141,8 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
   // LDS: top-k scratch | hist[256] | skey[k] | sidx[k] | sel[k] | count | comb |
   //      keys[max(C, P*(D+2))] (the head's keys, later the gathered partials)
   extern __shared__ uint64_t smem64[];
-  uint32_t* scratch = reinterpret_cast<uint32_t*>(smem64);
-  uint32_t* hist = scratch + kTopkScratchWords;
+  uint32_t* tk_scratch = reinterpret_cast<uint32_t*>(smem64);
+  uint32_t* hist = tk_scratch + kTopkScratchWords;
   uint32_t* skey = hist + 256;
   int32_t* sidx = reinterpret_cast<int32_t*>(skey + a.topk);
   int32_t* sel = sidx + a.topk;
@@ -158,7 +180,7 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
   {
     const int grp = lane / SLPR, col = lane % SLPR;
     const float* __restrict__ sb = a.summary + h * Cs * D + col * 4;
-    uint64_t* kg = a.keys + h * Cs;
+    uint64_t* kg = a.keys + h * a.key_stride;
     const int64_t c0 = Cs * p / P, c1 = Cs * (p + 1) / P;
     constexpr int US = kStepScoreUnroll;
     for (int64_t blk = c0; blk < c1; blk += kStepWaves * SRPL * US) {
@@ -233,7 +255,7 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
       for (int off = SLPR / 2; off >= 1; off >>= 1)
 #pragma unroll
         for (int u = 0; u < US; ++u) sc[u] += xor_lanes(sc[u], off);
-      const uint32_t tag = ep + 1u;
+      const uint32_t tag = launch_tag(ep);
       if (col == 0) {
 #pragma unroll
         for (int u = 0; u < US; ++u) {
@@ -251,9 +273,12 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
   }
 
   // ---- B: gather the head's keys, top-k -----------------------------------
-  const uint32_t tag = epoch + 1u;
-  if (P > 1) {
-    const uint64_t* kg = a.keys + h * Cs;
+  const uint32_t tag = launch_tag(epoch);
+  // This thread timed out on a partner's word (or the head is poisoned: then
+  // nothing is awaited and the output is NaN).
+  bool bad = epoch == kPoisonEpoch;
+  if (P > 1 && !bad) {
+    const uint64_t* kg = a.keys + h * a.key_stride;
     for (int64_t i0 = tid; i0 < C; i0 += kStepThreads * B8) {
       uint64_t w[B8];
 #pragma unroll
@@ -264,7 +289,7 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
 #pragma unroll
       for (int j = 0; j < B8; ++j) {
         const int64_t i = i0 + j * kStepThreads;
-        if (i < C) keys_l[i] = wait_tagged(kg + i, w[j], tag, a.status);
+        if (i < C) keys_l[i] = wait_tagged(kg + i, w[j], tag, a.status, bad);
       }
     }
   }
@@ -279,7 +304,7 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
     // Fewer chunks in play than selection slots (device count only): the
     // slots past the count hold -1, which the attention below skips.
     const int kk = static_cast<int>(min<int64_t>(a.topk, C));
-    if (kk > 0) wave_topk<TOPK_M>(keys_l, static_cast<int>(C), kk, scratch, hist, skey, sidx, lcount, emit);
+    if (kk > 0) wave_topk<TOPK_M>(keys_l, static_cast<int>(C), kk, tk_scratch, hist, skey, sidx, lcount, emit);
     for (int r = kk + lane; r < a.topk; r += kWave) emit(r, -1);
   }
   __syncthreads();
@@ -302,9 +327,12 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
     attend_block<T, D, U>(st, qp, a.qscale, kb, vb, blk + wave * RPL * U, s1, grp, tok_of);
   fold_row_groups(st);
   float* cw = comb + wave * (D + 2);
+  // A wavefront in which any lane timed out on a key marks its state with a
+  // NaN weight, which poisons the head's output below.
+  const bool wave_bad = __any(bad);
   if (lane == 0) {
     cw[0] = st.m;
-    cw[1] = st.l;
+    cw[1] = wave_bad ? __builtin_nanf("") : st.l;
   }
   if (grp == 0) {
 #pragma unroll
@@ -312,9 +340,13 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
   }
   __syncthreads();
   float M = -INFINITY;
+  bool poisoned = false;
 #pragma unroll
-  for (int w = 0; w < kStepWaves; ++w)
-    if (comb[w * (D + 2) + 1] > 0.f) M = fmaxf(M, comb[w * (D + 2)]);
+  for (int w = 0; w < kStepWaves; ++w) {
+    const float lw = comb[w * (D + 2) + 1];
+    poisoned = poisoned || lw != lw;
+    if (lw > 0.f) M = fmaxf(M, comb[w * (D + 2)]);
+  }
   float Lsum = 0.f, A = 0.f;
   const int d = tid;
   if (M != -INFINITY) {
@@ -328,9 +360,10 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
       }
     }
   }
+  if (poisoned) Lsum = __builtin_nanf("");
   T* __restrict__ out = static_cast<T*>(a.out) + h * D;
   if (P == 1) {
-    if (d < D) out[d] = from_f32<T>(Lsum > 0.f ? A / Lsum : 0.f);
+    if (d < D) out[d] = from_f32<T>(poisoned ? Lsum : (Lsum > 0.f ? A / Lsum : 0.f));
     return;
   }
 
@@ -338,14 +371,14 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
   // Workgroup 0 gathers the P tagged partials directly, each word re-read
   // until it carries this launch's tag: no arrival counter, so no atomic round
   // trip between the last partial and the merge.
-  uint64_t* pp = a.part + (h * P + p) * static_cast<int64_t>(D + 2);
+  uint64_t* pp = a.part + h * a.part_stride + p * static_cast<int64_t>(D + 2);
   if (d < D) put_tagged(pp + 2 + d, tag, __float_as_uint(A));
   if (tid == 0) {
     put_tagged(pp, tag, __float_as_uint(M));
     put_tagged(pp + 1, tag, __float_as_uint(Lsum));
   }
   if (p != 0) return;
-  const uint64_t* ph = a.part + h * P * static_cast<int64_t>(D + 2);
+  const uint64_t* ph = a.part + h * a.part_stride;
   if (P <= kRegMergeP) {
     // Few partials: the thread of column d gathers every (m_j, l_j) and its
     // acc_j[d] itself -- one batch of tagged loads (partials past P re-read
@@ -369,9 +402,10 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
       for (int j = 0; j < kRegMergeP; ++j)
         ready = ready && static_cast<uint32_t>(wm[j] >> 32) == tag && static_cast<uint32_t>(wl[j] >> 32) == tag &&
                 static_cast<uint32_t>(wa[j] >> 32) == tag;
-      if (ready) break;
+      if (ready || bad) break;
       if (it >= kSpinLimit) {
         __hip_atomic_fetch_or(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        bad = true;
         break;
       }
       __builtin_amdgcn_s_sleep(1);
@@ -392,8 +426,10 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
     }
     float mx = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < kRegMergeP; ++j)
+    for (int j = 0; j < kRegMergeP; ++j) {
       if (j < P && lj[j] > 0.f) mx = fmaxf(mx, mj[j]);
+      bad = bad || (j < P && lj[j] != lj[j]);  // a poisoned partial
+    }
     float LL = 0.f, AA = 0.f;
 #pragma unroll
     for (int j = 0; j < kRegMergeP; ++j) {
@@ -401,17 +437,19 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
       LL = fmaf(w, lj[j], LL);
       AA = fmaf(w, aj[j], AA);
     }
-    if (d < D) out[d] = from_f32<T>(LL > 0.f ? AA / LL : 0.f);
+    if (d < D) out[d] = from_f32<T>(bad ? __builtin_nanf("") : (LL > 0.f ? AA / LL : 0.f));
     // Every workgroup of the head has published, so each read this launch's
-    // epoch long ago: the next launch's tags can start.
-    if (tid == 0) __hip_atomic_store(&a.epoch[h], tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // epoch long ago: the next launch's tags can start.  After a time-out (or
+    // on a poisoned head) the head is poisoned.
+    if (tid == 0)
+      __hip_atomic_store(&a.epoch[h], bad ? kPoisonEpoch : tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
   // Gather all P partials ((m, l, acc[D]) each) into LDS in one batch of loads
   // spread over the 256 threads, then merge from LDS.
   float* pb = reinterpret_cast<float*>(keys_l);
   const int nw = P * (D + 2);
-  for (int i0 = tid; i0 < nw; i0 += kStepThreads * kGather) {
+  for (int i0 = bad ? nw : tid; i0 < nw; i0 += kStepThreads * kGather) {
     uint64_t w[kGather];
 #pragma unroll
     for (int j = 0; j < kGather; ++j) {
@@ -421,12 +459,17 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
 #pragma unroll
     for (int j = 0; j < kGather; ++j) {
       const int i = i0 + j * kStepThreads;
-      if (i < nw) pb[i] = __uint_as_float(wait_tagged(ph + i, w[j], tag, a.status));
+      if (i < nw) {
+        bool late = false;
+        const uint32_t v = wait_tagged(ph + i, w[j], tag, a.status, late);
+        pb[i] = late ? __builtin_nanf("") : __uint_as_float(v);  // a lost word poisons what uses it
+      }
     }
   }
   __syncthreads();
   // Wavefront 0: one partial per lane -> weights 2^(m_j - M) (0 for empty
-  // partials) and the total L; then every column is a branch-free dot product.
+  // partials) and the total L (NaN if any partial is poisoned); then every
+  // column is a branch-free dot product.
   float* wts = comb;  // P weights, then L at [kStepMaxP]
   if (wave == 0) {
     const float mj = lane < P ? pb[lane * (D + 2)] : -INFINITY;
@@ -437,18 +480,21 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
     const float w = (lj > 0.f && mx != -INFINITY) ? fast_exp2(mj - mx) : 0.f;
     if (lane < P) wts[lane] = w;
     const float Lt = wave_sum(w * lj);
-    if (lane == 0) wts[kStepMaxP] = Lt;
+    const bool any_bad = __any(bad || mj != mj || lj != lj);
+    if (lane == 0) wts[kStepMaxP] = any_bad ? __builtin_nanf("") : Lt;
   }
   __syncthreads();
+  const float LL = wts[kStepMaxP];
   if (d < D) {
     float AA = 0.f;
 #pragma unroll 8
     for (int j = 0; j < P; ++j) AA = fmaf(wts[j], pb[j * (D + 2) + 2 + d], AA);
-    const float LL = wts[kStepMaxP];
-    out[d] = from_f32<T>(LL > 0.f ? AA / LL : 0.f);
+    out[d] = from_f32<T>(LL != LL ? LL : (LL > 0.f ? AA / LL : 0.f));
   }
   __syncthreads();
-  if (tid == 0) __hip_atomic_store(&a.epoch[h], tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // A lost or poisoned partial poisons the head (see the register merge above).
+  if (tid == 0)
+    __hip_atomic_store(&a.epoch[h], LL != LL ? kPoisonEpoch : tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <typename T, int D, int TOPK_M, bool POS>
@@ -523,11 +569,90 @@ StepLayout step_layout(int64_t bh, int64_t C, int64_t D, int64_t k, int64_t chun
   return L;
 }
 
-// CSAHCA_STEP_WGS_PER_HEAD=n (> 0) overrides the workgroups per head (read per call).
+// CSAHCA_STEP_WGS_PER_HEAD=n (> 0) overrides the workgroups per head (read per
+// call; still bounded by the residency rule of decode_step_impl).
 int64_t env_wgs_per_head() {
   const char* s = std::getenv("CSAHCA_STEP_WGS_PER_HEAD");
   return s ? std::max<int64_t>(0, std::atoll(s)) : 0;
 }
+
+using StepKernelFn = void (*)(StepParams);
+using HybridKernelFn = void (*)(StepParams, HcaPart, uint32_t);
+
+// The instantiation of the step kernel a call launches (m: top-k register rows).
+template <typename T>
+StepKernelFn step_kernel_for(int64_t head_dim, int m, bool pos) {
+#define CSAHCA_PICK(DD)                                                                            \
+  if (m == 8) return pos ? csa_step_kernel<T, DD, 8, true> : csa_step_kernel<T, DD, 8, false>;    \
+  if (m == 32) return pos ? csa_step_kernel<T, DD, 32, true> : csa_step_kernel<T, DD, 32, false>; \
+  return pos ? csa_step_kernel<T, DD, 0, true> : csa_step_kernel<T, DD, 0, false>;
+  if (head_dim == 64) { CSAHCA_PICK(64) }
+  if (head_dim == 128) { CSAHCA_PICK(128) }
+  CSAHCA_PICK(256)
+#undef CSAHCA_PICK
+}
+
+StepKernelFn step_kernel_for_dtype(int dtype, int64_t head_dim, int m, bool pos) {
+  switch (dtype) {
+    case CSAHCA_BF16: return step_kernel_for<bf16>(head_dim, m, pos);
+    case CSAHCA_F16: return step_kernel_for<f16>(head_dim, m, pos);
+    case CSAHCA_F32: return step_kernel_for<float>(head_dim, m, pos);
+    default: return nullptr;
+  }
+}
+
+HybridKernelFn hybrid_kernel_for(int dtype, int m) {
+  if (dtype == CSAHCA_BF16)
+    return m == 8 ? csa_hybrid_kernel<bf16, 128, 8> : m == 32 ? csa_hybrid_kernel<bf16, 128, 32>
+                                                               : csa_hybrid_kernel<bf16, 128, 0>;
+  return m == 8 ? csa_hybrid_kernel<f16, 128, 8> : m == 32 ? csa_hybrid_kernel<f16, 128, 32>
+                                                            : csa_hybrid_kernel<f16, 128, 0>;
+}
+
+// Workgroups of kernel `fn` (kStepThreads threads, `lds` bytes of dynamic LDS)
+// that one CU holds at once, from the occupancy API; cached per device, kernel
+// and LDS size.  0 if the query fails.
+int resident_per_cu(const void* fn, size_t lds) {
+  struct Entry {
+    int dev;
+    const void* fn;
+    size_t lds;
+    int n;
+  };
+  static std::mutex mu;
+  static std::vector<Entry> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  {
+    std::lock_guard<std::mutex> g(mu);
+    for (const Entry& e : cache)
+      if (e.dev == dev && e.fn == fn && e.lds == lds) return e.n;
+  }
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kStepThreads, lds) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  std::lock_guard<std::mutex> g(mu);
+  if (cache.size() < 4096) cache.push_back({dev, fn, lds, n});
+  return n;
+}
+
+// Where a step launch keeps its exchange state: carved from the caller's
+// workspace (strides 0: the call's chunk count and P * (head_dim + 2)), or a
+// fixed per-head layout that does not depend on the call's shape.
+struct StepRegions {
+  uint32_t* status;
+  uint32_t* epoch;
+  uint64_t* keys;
+  uint64_t* part;
+  int64_t key_stride;   // words per head; 0 = the call's chunk count
+  int64_t part_stride;  // words per head; 0 = P * (head_dim + 2)
+  int64_t max_p;        // most workgroups per head the partial region holds
+};
 
 }  // namespace
 }  // namespace csahca
@@ -551,7 +676,7 @@ int decode_step_impl(const void* q, const void* k_cache, const void* v_cache, co
                      int64_t head_dim, int64_t num_chunks, const int32_t* c_dev, const int64_t* pos_dev,
                      int64_t chunk_size, int64_t top_k, void* workspace, size_t workspace_bytes,
                      void* stream_ptr, HcaPart* hybrid = nullptr, size_t hybrid_lds = 0,
-                     bool* hybrid_launched = nullptr) {
+                     bool* hybrid_launched = nullptr, const StepRegions* fixed = nullptr) {
   CSAHCA_REQUIRE(valid_dtype(dtype), "q, k_cache and v_cache must be float32, float64, float16 or bfloat16");
   CSAHCA_REQUIRE(batch >= 0 && heads >= 0 && seq_len >= 0 && head_dim >= 0 && num_chunks >= 0,
                  "negative dimension");
@@ -567,10 +692,19 @@ int decode_step_impl(const void* q, const void* k_cache, const void* v_cache, co
   if (bh == 0 || head_dim == 0) return CSAHCA_OK;
   CSAHCA_REQUIRE(q && out && summary && (k == 0 || (k_cache && v_cache && out_indices)),
                  "null tensor pointer");
-  const StepLayout lay = step_layout(bh, num_chunks, head_dim, k, chunk_size);
-  if (workspace == nullptr || workspace_bytes < lay.total)
-    return fail(CSAHCA_ERR_WORKSPACE, "workspace too small for csa decode step");
+  StepLayout lay{};
   char* ws = static_cast<char*>(workspace);
+  StepRegions rg{};
+  if (fixed == nullptr) {
+    lay = step_layout(bh, num_chunks, head_dim, k, chunk_size);
+    if (workspace == nullptr || workspace_bytes < lay.total)
+      return fail(CSAHCA_ERR_WORKSPACE, "workspace too small for csa decode step");
+    rg = StepRegions{reinterpret_cast<uint32_t*>(ws), reinterpret_cast<uint32_t*>(ws + lay.epoch),
+                     reinterpret_cast<uint64_t*>(ws + lay.keys), reinterpret_cast<uint64_t*>(ws + lay.part), 0, 0,
+                     kStepMaxP};
+  } else {
+    rg = *fixed;
+  }
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
 
   const int ncu = device_cu_count();
@@ -594,11 +728,34 @@ int decode_step_impl(const void* q, const void* k_cache, const void* v_cache, co
     P = std::max(ceil_div(num_chunks, score_rows), ceil_div(k * chunk_size, attend_rows));
     P = std::min<int64_t>(P, std::max<int64_t>(1, (2 * static_cast<int64_t>(ncu)) / std::max<int64_t>(bh, 1)));
   }
-  P = std::min<int64_t>({P, kStepMaxP, ceil_div(num_chunks, 8), ceil_div(k * chunk_size, 16)});
+  P = std::min<int64_t>({P, rg.max_p, ceil_div(num_chunks, 8), ceil_div(k * chunk_size, 16)});
   P = std::max<int64_t>(1, P);
   // keys region: the head's C keys, later (P > 1) the P gathered partials
-  const size_t lds = lds_base + static_cast<size_t>(std::max<int64_t>(num_chunks, P > 1 ? P * (head_dim + 2) : 0)) * 4;
+  auto lds_for = [&](int64_t np) {
+    return lds_base + static_cast<size_t>(std::max<int64_t>(num_chunks, np > 1 ? np * (head_dim + 2) : 0)) * 4;
+  };
+  size_t lds = lds_for(P);
   if (k > 0 && k <= kStepMaxK && fused_dtype && fused_dim && aligned && ncu > 0 && lds <= kStepLds) {
+    const int m = topk_regs_for(num_chunks, k);
+    const bool hyb = hybrid != nullptr && head_dim == 128 && pos_dev == nullptr &&
+                     (dtype == CSAHCA_BF16 || dtype == CSAHCA_F16);
+    const HybridKernelFn hfn = hyb ? hybrid_kernel_for(dtype, m) : nullptr;
+    const StepKernelFn sfn = hyb ? nullptr : step_kernel_for_dtype(dtype, head_dim, m, pos_dev != nullptr);
+    const void* fn = hyb ? reinterpret_cast<const void*>(hfn) : reinterpret_cast<const void*>(sfn);
+    auto launch_lds = [&] { return hyb ? std::max(lds, hybrid_lds) : lds; };
+    // The P workgroups of a head wait on each other, so with P > 1 every step
+    // workgroup of the grid must fit on the device at once (measured for the
+    // instantiation launched, with its LDS); the step blocks of the hybrid
+    // kernel come first in its grid.  Where they would not fit, P shrinks,
+    // down to 1 (no exchange at all).
+    if (P > 1) {
+      const int64_t cap = static_cast<int64_t>(resident_per_cu(fn, launch_lds())) * ncu;
+      if (bh * P > cap) {
+        P = cap / bh;
+        if (P < 2) P = 1;
+        lds = lds_for(P);
+      }
+    }
     CSAHCA_REQUIRE(bh * P <= INT32_MAX, "too many heads in one call");
     StepParams pr;
     pr.q = q;
@@ -607,10 +764,12 @@ int decode_step_impl(const void* q, const void* k_cache, const void* v_cache, co
     pr.vcache = v_cache;
     pr.out = out;
     pr.idx_out = out_indices;
-    pr.status = reinterpret_cast<uint32_t*>(ws);
-    pr.epoch = reinterpret_cast<uint32_t*>(ws + lay.epoch);
-    pr.keys = reinterpret_cast<uint64_t*>(ws + lay.keys);
-    pr.part = reinterpret_cast<uint64_t*>(ws + lay.part);
+    pr.status = rg.status;
+    pr.epoch = rg.epoch;
+    pr.keys = rg.keys;
+    pr.part = rg.part;
+    pr.key_stride = rg.key_stride > 0 ? rg.key_stride : num_chunks;
+    pr.part_stride = rg.part_stride > 0 ? rg.part_stride : P * (head_dim + 2);
     pr.S = seq_len;
     pr.C = num_chunks;
     pr.Cs = num_chunks;
@@ -628,51 +787,20 @@ int decode_step_impl(const void* q, const void* k_cache, const void* v_cache, co
     pr.P = static_cast<int>(P);
     pr.score_scale = 1.0f / sqrtf(static_cast<float>(head_dim));
     pr.qscale = kLog2e / sqrtf(static_cast<float>(head_dim));
-    const dim3 grid(static_cast<uint32_t>(bh * P));
-    if (hybrid != nullptr && head_dim == 128 && pos_dev == nullptr &&
-        (dtype == CSAHCA_BF16 || dtype == CSAHCA_F16)) {
+    if (hyb) {
       const int64_t hblocks = ceil_div(hybrid->items, static_cast<int64_t>(hybrid->per_block));
       CSAHCA_REQUIRE(bh * P + hblocks <= INT32_MAX, "too many blocks in one call");
-      const dim3 g2(static_cast<uint32_t>(bh * P + hblocks));
-      const size_t lds2 = std::max(lds, hybrid_lds);
-      const uint32_t sb = static_cast<uint32_t>(bh * P);
-      const int m = topk_regs_for(num_chunks, k);
       *hybrid_launched = true;
-#define CSAHCA_HYBRID_LAUNCH(TT, MM) \
-  return launch("csa_hybrid_kernel", csa_hybrid_kernel<TT, 128, MM>, g2, dim3(kStepThreads), lds2, stream, pr, *hybrid, sb)
-      if (dtype == CSAHCA_BF16) {
-        if (m == 8) CSAHCA_HYBRID_LAUNCH(bf16, 8);
-        if (m == 32) CSAHCA_HYBRID_LAUNCH(bf16, 32);
-        CSAHCA_HYBRID_LAUNCH(bf16, 0);
-      }
-      if (m == 8) CSAHCA_HYBRID_LAUNCH(f16, 8);
-      if (m == 32) CSAHCA_HYBRID_LAUNCH(f16, 32);
-      CSAHCA_HYBRID_LAUNCH(f16, 0);
-#undef CSAHCA_HYBRID_LAUNCH
+      return launch("csa_hybrid_kernel", hfn, dim3(static_cast<uint32_t>(bh * P + hblocks)), dim3(kStepThreads),
+                    launch_lds(), stream, pr, *hybrid, static_cast<uint32_t>(bh * P));
     }
-    return dispatch_dtype(dtype, [&](auto tag) -> int {
-      using T = decltype(tag);
-      if constexpr (std::is_same_v<T, double>) {
-        return fail(CSAHCA_ERR_ARGUMENT, "unreachable");
-      } else {
-        const int m = topk_regs_for(num_chunks, k);
-#define CSAHCA_STEP_LAUNCH(DD, MM)                                                                          \
-  return pos_dev ? launch("csa_step_kernel", csa_step_kernel<T, DD, MM, true>, grid, dim3(kStepThreads), lds, \
-                          stream, pr)                                                                        \
-                 : launch("csa_step_kernel", csa_step_kernel<T, DD, MM, false>, grid, dim3(kStepThreads), lds, \
-                          stream, pr)
-#define CSAHCA_STEP_BY_M(DD)                          \
-  if (m == 8) CSAHCA_STEP_LAUNCH(DD, 8);             \
-  if (m == 32) CSAHCA_STEP_LAUNCH(DD, 32);           \
-  CSAHCA_STEP_LAUNCH(DD, 0);
-        if (head_dim == 64) { CSAHCA_STEP_BY_M(64) }
-        if (head_dim == 128) { CSAHCA_STEP_BY_M(128) }
-        CSAHCA_STEP_BY_M(256)
-#undef CSAHCA_STEP_BY_M
-#undef CSAHCA_STEP_LAUNCH
-      }
-    });
+    return launch("csa_step_kernel", sfn, dim3(static_cast<uint32_t>(bh * P)), dim3(kStepThreads), lds, stream,
+                  pr);
   }
+  if (fixed != nullptr)
+    return fail(CSAHCA_ERR_ARGUMENT,
+                "the allocation-free step takes float32/float16/bfloat16, head_dim 64/128/256, 16-byte aligned "
+                "tensors and 0 < top_k <= 1024");
   if (c_dev != nullptr || pos_dev != nullptr)
     return fail(CSAHCA_ERR_ARGUMENT,
                 "a device chunk count needs the fused step (float32/float16/bfloat16, head_dim 64/128/256, "
@@ -790,3 +918,4 @@ extern "C" int csahca_hybrid_decode_forward(const void* q, const void* k_cache, 
                                      head_dim, hca_chunk_size, hca_workspace, hca_workspace_bytes, stream_ptr);
   return hca_merge_launch(dtype, hca_workspace, csa_out, csa_weight, out, bh, Ch, static_cast<int>(head_dim), stream);
 }
+

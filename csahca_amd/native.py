@@ -286,18 +286,33 @@ _STEP_WS: dict = {}
 
 
 def _step_workspace(nbytes: int, device, signature: tuple) -> torch.Tensor:
-    """Step workspace kept per (device, stream).  The fused step keeps per-head
-    launch epochs and tagged exchange words in it, laid out by the problem shape, so
-    it is zero-filled (a fill kernel) whenever it is created or the shape changes."""
-    key = (device.index, _stream())
-    ent = _STEP_WS.get(key)
-    if ent is None or ent[0].numel() < nbytes:
-        ent = [torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device), signature]
-        _STEP_WS[key] = ent
-    elif ent[1] != signature:
-        ent[0].zero_()
-        ent[1] = signature
-    return ent[0]
+    """Step workspace for one (device, stream, problem shape).
+
+    The fused step keeps per-head launch epochs and tagged exchange words in it,
+    laid out by the shape (B*H, chunks, head_dim, top_k, chunk), so each shape
+    gets a buffer of its own, zero-filled once (a fill kernel, on the calling
+    stream) and then reused by every call of that shape on that stream -- eager
+    calls and replays of graphs captured on it alike.  Buffers live until
+    release_step_workspaces(): a captured graph keeps their addresses."""
+    key = (device.index, _stream(), signature)
+    ws = _STEP_WS.get(key)
+    if ws is None:
+        ws = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+        _STEP_WS[key] = ws
+    return ws
+
+
+def step_workspace_ready(device, stream, signature: tuple) -> bool:
+    """Whether a step workspace exists for (device, stream, shape signature)."""
+    d = torch.device(device)
+    index = d.index if d.index is not None else torch.cuda.current_device()
+    return (index, int(stream), tuple(signature)) in _STEP_WS
+
+
+def release_step_workspaces() -> None:
+    """Drop every cached step workspace (only when no captured graph that used
+    one will be replayed again)."""
+    _STEP_WS.clear()
 
 
 def csa_decode_step(q, k_cache, v_cache, summary, chunk_size, top_k, tile_size: int = 0):
@@ -492,9 +507,11 @@ def csa_decode_step_at(q, k_cache, v_cache, summary, token_pos, chunk_size, top_
 
 
 def csa_step_status(device=None) -> dict:
-    """Sticky status words of this process's step workspaces (0 = healthy)."""
+    """Sticky status words of this process's step workspaces (0 = healthy; bit 0:
+    an exchange wait timed out, the affected heads returned NaN and stay poisoned
+    until their workspace is released).  Synchronises the calling stream."""
     out = {}
-    for key, (ws, _sig) in _STEP_WS.items():
+    for key, ws in _STEP_WS.items():
         if device is not None and key[0] != torch.device(device).index:
             continue
         val = ctypes.c_uint32(0)
@@ -536,8 +553,12 @@ def hybrid_decode_forward(q, k_cache, v_cache, *, csa_chunk_size: int, csa_top_k
                           csa_weight: float = 0.7, summary=None):
     """hybrid_reference (hybrid_attention/reference.py:95-108) on the GPU: the
     CSA decode step (selection from the chunk summaries of K, built here when
-    ``summary`` is None) blended with HCA at ``csa_weight``."""
+    ``summary`` is None) blended with HCA at ``csa_weight``.  Building the
+    summary here needs whole chunks, as chunk_mean does (reference.py:40-42)."""
     if summary is None:
+        _check(int(csa_chunk_size) > 0, "chunk_size must be positive")
+        _check(k_cache.dim() == 4 and k_cache.shape[2] % int(csa_chunk_size) == 0,
+               "seq length must be divisible by chunk_size")
         summary = csa_chunk_summary(k_cache, csa_chunk_size)
     csa_chunk_size, csa_top_k, hca_chunk_size = int(csa_chunk_size), int(csa_top_k), int(hca_chunk_size)
     _csa_checks(q, k_cache, v_cache, torch.empty((q.shape[0], q.shape[1], 0), dtype=torch.int32, device=q.device),

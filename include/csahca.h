@@ -7,7 +7,10 @@
  * hybrid_attention/extension.py:13-197).  Every entry point takes plain device
  * pointers, sizes and a HIP stream, returns a status code, and never allocates:
  * scratch space comes from the caller through `workspace` (size from the
- * matching *_workspace_bytes function; contents need no initialisation).
+ * matching *_workspace_bytes function).  Workspace contents need no
+ * initialisation, except for the decode-step entry points (csahca_csa_decode_step,
+ * _dev, _at, csahca_hybrid_decode_forward's step_workspace): those keep state
+ * between calls and need a zero-filled workspace (see csahca_csa_decode_step).
  * No HIP or torch type appears in a signature: `stream` is a hipStream_t passed
  * as void* (NULL = the null stream).
  *
@@ -134,9 +137,18 @@ size_t csahca_csa_step_workspace_bytes(int64_t batch, int64_t heads, int64_t num
  * min(top_k, num_chunks) chunks from summary [batch, heads, num_chunks,
  * head_dim] exactly as csahca_csa_select_topk (ids to out_indices), then writes
  * the sparse attention over their tokens to out, as csahca_csa_decode_forward.
- * num_chunks * chunk_size <= seq_len.  The workspace must be zero-filled before
- * its first use; every completed call leaves it reusable.  One workspace must
- * not be shared by calls that can run concurrently (e.g. on two streams). */
+ * num_chunks * chunk_size <= seq_len.  The workspace carries per-head launch
+ * epochs and tagged exchange words from call to call: it must be zero-filled
+ * before its first use, and zero-filled again (or replaced by another) whenever
+ * (batch * heads, num_chunks, head_dim, min(top_k, num_chunks), chunk_size)
+ * changes.  Every completed call leaves it reusable for the next call of the
+ * same shape, including replays of a graph that captured such a call.  One
+ * workspace must not be shared by calls that can run concurrently (e.g. on two
+ * streams).  The workgroups of one head wait on each other, so the library
+ * sizes the launch from the kernel's occupancy to be resident at once on an
+ * otherwise idle device.  Should a wait still time out, the head's output is
+ * NaN, csahca_csa_step_status reports it, and the head stays poisoned (NaN)
+ * until the workspace is zero-filled again. */
 int csahca_csa_decode_step(const void* q, const void* k_cache, const void* v_cache,
                            const float* summary, void* out, int32_t* out_indices, int dtype,
                            int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
@@ -175,8 +187,9 @@ int csahca_csa_decode_step_at(const void* q, const void* k_cache, const void* v_
                               size_t workspace_bytes, void* stream);
 
 /* Reads the step workspace's sticky status word (0 = healthy; bit 0 = a
- * workgroup hand-off timed out, so a result may be wrong) into host memory;
- * synchronises the stream. */
+ * workgroup hand-off timed out: the affected heads returned NaN and stay
+ * poisoned until the workspace is zero-filled) into host memory; synchronises
+ * the stream. */
 int csahca_csa_step_status(const void* workspace, uint32_t* status_out, void* stream);
 
 /* ------------------------------------------------------------------------- */

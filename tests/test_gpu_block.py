@@ -85,14 +85,20 @@ def test_mini_block_graph_replays_match_eager(fused):
     with torch.cuda.stream(s):
         blk(hidden, k, v, selection="dynamic", summary=summ)  # warm the stream's workspace
     torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    with torch.cuda.graph(g, stream=s):
         out = blk(hidden, k, v, selection="dynamic", summary=summ)
     for _ in range(3):
-        g.replay()
+        with torch.cuda.stream(s):
+            g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
-        blk(hidden, k, v, selection="dynamic", summary=summ)  # eager work between replays
+        with torch.cuda.stream(s):  # eager work on the capture stream between replays
+            again = blk(hidden, k, v, selection="dynamic", summary=summ)
+        torch.cuda.synchronize()
+        assert torch.equal(again, eager)
+    assert all(x == 0 for x in native.csa_step_status().values())
 
 
 def cpu_hybrid_reference(blk: HybridDecodeBlock, k0, v0, hiddens):

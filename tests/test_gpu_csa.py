@@ -251,27 +251,50 @@ def test_large_offsets_beyond_2_to_32_elements():
 
 
 def test_cuda_graph_replays_match_eager():
+    """A step captured on stream s shares s's workspace for its shape with eager
+    calls on s, so launch epochs carry across replays and interleaved eager calls;
+    eager calls of smaller and larger shapes on s (workspaces of their own) leave
+    the captured graph intact.  Every replay and every eager call must equal its
+    eager reference bit for bit, with the status word clean."""
     case = make_synthetic_case(batch=1, heads=8, seq_len=32768, head_dim=128, chunk_size=64, top_k=8, seed=0)
     q, k, v = case.q.to(DEV), case.k_cache.to(DEV), case.v_cache.to(DEV)
     summ = extension.csa_chunk_summary(k, 64)
+    g = torch.Generator().manual_seed(11)
+    qs, ks, vs = (torch.randn(*shape, generator=g).to(torch.bfloat16).to(DEV)
+                  for shape in ((1, 4, 128), (1, 4, 8192, 128), (1, 4, 8192, 128)))
+    ql, kl, vl = (torch.randn(*shape, generator=g).to(torch.bfloat16).to(DEV)
+                  for shape in ((4, 8, 128), (4, 8, 16384, 128), (4, 8, 16384, 128)))
+    summ_s, summ_l = extension.csa_chunk_summary(ks, 64), extension.csa_chunk_summary(kl, 64)
     eager_out, eager_idx = native.csa_decode_step(q, k, v, summ, 64, 8)
+    small_out, small_idx = native.csa_decode_step(qs, ks, vs, summ_s, 64, 8)
+    large_out, large_idx = native.csa_decode_step(ql, kl, vl, summ_l, 64, 8)
     torch.cuda.synchronize()
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        native.csa_decode_step(q, k, v, summ, 64, 8)  # warm up allocations on the side stream
+        native.csa_decode_step(q, k, v, summ, 64, 8)  # creates s's workspace for this shape
+    assert native.step_workspace_ready(DEV, s.cuda_stream, (8, 512, 128, 8, 64))
     torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with torch.cuda.graph(graph, stream=s):
         gout, gidx = native.csa_decode_step(q, k, v, summ, 64, 8)
-    for _ in range(3):
-        gout.zero_()
-        graph.replay()
+    for r in range(4):
+        with torch.cuda.stream(s):
+            gout.zero_()
+            graph.replay()
         torch.cuda.synchronize()
-        assert torch.equal(gidx, eager_idx)
-        assert torch.equal(gout, eager_out)
-        native.csa_decode_step(q, k, v, summ, 64, 8)  # eager work between replays
+        assert torch.equal(gidx, eager_idx), r
+        assert torch.equal(gout, eager_out), r
+        with torch.cuda.stream(s):  # eager work on the capture stream between replays
+            o, i = native.csa_decode_step(q, k, v, summ, 64, 8)
+            so, si = native.csa_decode_step(qs, ks, vs, summ_s, 64, 8)
+            lo, li = native.csa_decode_step(ql, kl, vl, summ_l, 64, 8)
         torch.cuda.synchronize()
+        assert torch.equal(o, eager_out) and torch.equal(i, eager_idx), r
+        assert torch.equal(so, small_out) and torch.equal(si, small_idx), r
+        assert torch.equal(lo, large_out) and torch.equal(li, large_idx), r
+    assert all(v == 0 for v in native.csa_step_status().values())
 
 
 FUSED = [
@@ -363,6 +386,26 @@ def test_fused_step_repeated_calls_rearm_counters():
         out, idx2 = native.csa_decode_step(q, k, v, summ, 64, 8)
     torch.cuda.synchronize()
     assert torch.equal(out, first) and torch.equal(idx2, idx)
+    assert all(v == 0 for v in native.csa_step_status().values())
+
+
+def test_workgroups_per_head_override_is_bounded_by_residency(monkeypatch):
+    """CSAHCA_STEP_WGS_PER_HEAD=64 at B32 H8 asks for 16384 workgroups that wait
+    on each other, far more than the device holds at once; the library shrinks P
+    to what the kernel's occupancy allows, and the result matches the default
+    launch (same ids; outputs within fp32 reordering)."""
+    B, H, S, D, chunk, k = 32, 8, 8192, 128, 64, 8
+    g = torch.Generator().manual_seed(29)
+    q, kc, vc = (torch.randn(*sh, generator=g).to(torch.bfloat16).to(DEV)
+                 for sh in ((B, H, D), (B, H, S, D), (B, H, S, D)))
+    summ = extension.csa_chunk_summary(kc, chunk)
+    want, want_idx = native.csa_decode_step(q, kc, vc, summ, chunk, k)
+    monkeypatch.setenv("CSAHCA_STEP_WGS_PER_HEAD", "64")
+    for _ in range(3):
+        got, idx = native.csa_decode_step(q, kc, vc, summ, chunk, k)
+    torch.cuda.synchronize()
+    assert torch.equal(idx, want_idx)
+    assert torch.allclose(got.float(), want.float(), atol=2e-2, rtol=1e-2)
     assert all(v == 0 for v in native.csa_step_status().values())
 
 

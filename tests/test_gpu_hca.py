@@ -156,19 +156,24 @@ def test_hybrid_graph_replays_match_eager():
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        run()
+        run()  # creates s's step workspace for this shape
+    assert native.step_workspace_ready(DEV, s.cuda_stream, (8, 128, 128, 8, 64))
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with torch.cuda.graph(graph, stream=s):
         got = run()
     for i in range(5):
-        got.zero_()
-        graph.replay()
+        with torch.cuda.stream(s):
+            got.zero_()
+            graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(got, want), i
-        run()
+        with torch.cuda.stream(s):  # eager work on the capture stream, same workspace
+            again = run()
         torch.cuda.synchronize()
+        assert torch.equal(again, want), i
+    assert all(x == 0 for x in native.csa_step_status().values())
 
 
 def test_hca_rejects_ragged_sequence_with_reference_message():
