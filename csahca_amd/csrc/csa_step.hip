@@ -919,3 +919,88 @@ extern "C" int csahca_hybrid_decode_forward(const void* q, const void* k_cache, 
   return hca_merge_launch(dtype, hca_workspace, csa_out, csa_weight, out, bh, Ch, static_cast<int>(head_dim), stream);
 }
 
+// ---------------------------------------------------------------------------
+// Allocation-free decode step (csahca_csa_decode_step_noalloc).
+//
+// The exchange state lives in `scratch`, a static device array: one copy per
+// device, zero when the library's code object is loaded on that device, held
+// until the process ends.  Its layout does not depend on the call's shape:
+// head slot h (h < kFixedHeads) always has its epoch word, kFixedChunks key
+// words and kFixedP * (kFixedDim + 2) partial words at the same place, and
+// every launch over slot h advances that slot's epoch by one.  Every word left
+// in slot h by an earlier call therefore carries an older tag than the
+// current launch's, whatever shapes earlier calls had, so nothing is cleared
+// between calls.  Calls that overlap on one device (two streams) race on it.
+namespace {
+constexpr int64_t kFixedHeads = 256;    // batch * heads
+constexpr int64_t kFixedChunks = 2048;  // summary rows per head
+constexpr int64_t kFixedDim = 256;      // head_dim
+constexpr int64_t kFixedP = 32;         // workgroups per head
+constexpr int64_t kFixedHeaderWords = 32;                // 256 B: the status word
+constexpr int64_t kFixedEpochWords = kFixedHeads / 2;    // one u32 epoch per head slot
+constexpr int64_t kFixedKeyWords = kFixedChunks;         // per head slot
+constexpr int64_t kFixedPartWords = kFixedP * (kFixedDim + 2);  // per head slot
+constexpr int64_t kFixedWords =
+    kFixedHeaderWords + kFixedEpochWords + kFixedHeads * (kFixedKeyWords + kFixedPartWords);  // 21.1 MB
+constexpr int kMaxDevices = 64;
+}  // namespace
+
+static __device__ __align__(256) uint64_t scratch[kFixedWords];
+
+namespace {
+std::mutex g_scratch_mu;
+uint64_t* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the current device's `scratch` (hipGetSymbolAddress once
+// per device, with that device current).  The array's name in host code is a
+// stand-in, not a device address: only this pointer goes to kernels.
+int scratch_regions(StepRegions* rg) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail_hip(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(CSAHCA_ERR_ARGUMENT, "device ordinal out of range");
+  uint64_t* base = nullptr;
+  {
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    base = g_scratch_ptr[dev];
+    if (base == nullptr) {
+      void* p = nullptr;
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return fail_hip(e, "hipGetSymbolAddress(scratch)");
+      base = static_cast<uint64_t*>(p);
+      g_scratch_ptr[dev] = base;
+    }
+  }
+  rg->status = reinterpret_cast<uint32_t*>(base);
+  rg->epoch = reinterpret_cast<uint32_t*>(base + kFixedHeaderWords);
+  rg->keys = base + kFixedHeaderWords + kFixedEpochWords;
+  rg->part = rg->keys + kFixedHeads * kFixedKeyWords;
+  rg->key_stride = kFixedKeyWords;
+  rg->part_stride = kFixedPartWords;
+  rg->max_p = kFixedP;
+  return CSAHCA_OK;
+}
+}  // namespace
+
+extern "C" int csahca_csa_decode_step_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                                              const float* summary, void* out, int32_t* out_indices, int dtype,
+                                              int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
+                                              int64_t num_chunks, int64_t chunk_size, int64_t top_k,
+                                              void* stream_ptr) {
+  clear_error();
+  CSAHCA_REQUIRE(batch >= 0 && heads >= 0 && seq_len >= 0 && head_dim >= 0 && num_chunks >= 0,
+                 "negative dimension");
+  CSAHCA_REQUIRE(batch * heads <= kFixedHeads,
+                 "csahca_csa_decode_step_noalloc: batch * heads exceeds 256, the static scratch limit");
+  CSAHCA_REQUIRE(num_chunks <= kFixedChunks,
+                 "csahca_csa_decode_step_noalloc: num_chunks exceeds 2048, the static scratch limit");
+  CSAHCA_REQUIRE(head_dim <= kFixedDim, "csahca_csa_decode_step_noalloc: head_dim exceeds 256");
+  CSAHCA_REQUIRE(batch * heads == 0 || head_dim == 0 || (top_k > 0 && num_chunks > 0),
+                 "csahca_csa_decode_step_noalloc needs top_k > 0 and at least one chunk");
+  StepRegions rg{};
+  const int rc = scratch_regions(&rg);
+  if (rc != CSAHCA_OK) return rc;
+  return decode_step_impl(q, k_cache, v_cache, summary, out, out_indices, dtype, batch, heads, seq_len, head_dim,
+                          num_chunks, nullptr, nullptr, chunk_size, top_k, nullptr, 0, stream_ptr, nullptr, 0,
+                          nullptr, &rg);
+}

@@ -61,6 +61,7 @@ _SIGNATURES = {
     "csahca_csa_decode_step_dev": (_int, [_vp] * 7 + [_int] + [_i64] * 7 + [_vp, _sz, _vp]),
     "csahca_csa_decode_step_at": (_int, [_vp] * 7 + [_int] + [_i64] * 7 + [_vp, _sz, _vp]),
     "csahca_csa_step_status": (_int, [_vp, ctypes.POINTER(ctypes.c_uint32), _vp]),
+    "csahca_csa_decode_step_noalloc": (_int, [_vp] * 6 + [_int] + [_i64] * 7 + [_vp]),
     "csahca_hca_decode_workspace_bytes": (_sz, [_i64] * 5),
     "csahca_dsv4_pack_tokens": (_int, [_vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp]),
     "csahca_hca_decode_forward": (_int, [_vp, _vp, _vp, _vp, _dbl, _vp, _int] + [_i64] * 5 + [_vp, _sz, _vp]),
@@ -345,6 +346,39 @@ def csa_decode_step(q, k_cache, v_cache, summary, chunk_size, top_k, tile_size: 
                                          _DTYPES[q.dtype], B, H, S, D, C, chunk_size, top_k, _ptr(ws), ws.numel(),
                                          _stream()))
     return out, idx
+
+
+NOALLOC_MAX_HEADS = 256      # batch * heads
+NOALLOC_MAX_CHUNKS = 2048    # summary rows per head
+NOALLOC_MAX_HEAD_DIM = 256
+
+
+def csa_decode_step_noalloc(q, k_cache, v_cache, summary, chunk_size, top_k, *, out, indices):
+    """csa_decode_step through the library's allocation-free entry point: the
+    exchange state lives in a static per-device array, so neither the library
+    nor this wrapper allocates anything (``out`` like q, ``indices`` int32
+    [B, H, min(top_k, C)] are the caller's).  For callers that cannot allocate
+    (graph capture, tight serving loops).  Limits: B*H <= 256, C <= 2048,
+    head_dim 64/128/256, bf16/f16/f32, 0 < top_k <= 1024.  Calls that overlap
+    on one device race on the shared array.  Returns ``(out, indices)``."""
+    chunk_size, top_k = int(chunk_size), int(top_k)
+    _check(all(t.is_cuda for t in (q, k_cache, v_cache, summary, out, indices)), "all tensors must be CUDA tensors")
+    _check(all(t.is_contiguous() for t in (q, k_cache, v_cache, summary, out, indices)), "tensors must be contiguous")
+    _check(q.dim() == 3 and k_cache.dim() == 4 and k_cache.shape == v_cache.shape, "q [B, H, D], caches [B, H, S, D]")
+    B, H, S, D = k_cache.shape
+    _check(tuple(q.shape) == (B, H, D) and q.dtype == k_cache.dtype == v_cache.dtype, "q must match the caches")
+    _check(q.dtype in _DTYPES, f"unsupported dtype {q.dtype}")
+    _check(summary.dtype == torch.float32 and summary.dim() == 4 and tuple(summary.shape[:2]) == (B, H)
+           and summary.shape[3] == D, "summary must be fp32 [batch, heads, chunks, head_dim]")
+    C = summary.shape[2]
+    _check(out.shape == q.shape and out.dtype == q.dtype, "out must match q")
+    _check(tuple(indices.shape) == (B, H, min(top_k, C)) and indices.dtype == torch.int32,
+           "indices must be int32 [batch, heads, min(top_k, chunks)]")
+    with torch.cuda.device(q.device):
+        _rc(lib().csahca_csa_decode_step_noalloc(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(summary), _ptr(out),
+                                                 _ptr(indices), _DTYPES[q.dtype], B, H, S, D, C, chunk_size, top_k,
+                                                 _stream()))
+    return out, indices
 
 
 def csa_decode_step_dev(q, k_cache, v_cache, summary, num_chunks, chunk_size, top_k, *, out=None, indices=None):

@@ -192,6 +192,23 @@ int csahca_csa_decode_step_at(const void* q, const void* k_cache, const void* v_
  * the stream. */
 int csahca_csa_step_status(const void* workspace, uint32_t* status_out, void* stream);
 
+/* csahca_csa_decode_step without a workspace.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid allocation).
+ * The exchange state lives in a static device array of the library (21.1 MB
+ * per device, zero when the library's code object loads on that device, held
+ * until the process ends); nothing is allocated and nothing needs clearing
+ * between calls, whatever their shapes.  Limits: batch * heads <= 256,
+ * num_chunks <= 2048, head_dim 64/128/256, float32/float16/bfloat16, 16-byte
+ * aligned tensors, 0 < top_k <= 1024; other shapes return CSAHCA_ERR_ARGUMENT.
+ * Results equal csahca_csa_decode_step's bit for bit.  Every call on a device
+ * shares that device's array, so calls that can overlap on one device (two
+ * streams) race and must be serialised by the caller. */
+int csahca_csa_decode_step_noalloc(const void* q, const void* k_cache, const void* v_cache,
+                                   const float* summary, void* out, int32_t* out_indices, int dtype,
+                                   int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
+                                   int64_t num_chunks, int64_t chunk_size, int64_t top_k, void* stream);
+
 /* ------------------------------------------------------------------------- */
 /* HCA: dense attention over chunk summaries, and the CSA/HCA blend           */
 /* ------------------------------------------------------------------------- */
