@@ -460,9 +460,26 @@ __device__ __forceinline__ uint4 dequant8_bf16_hw(uint2 w, uint32_t sbyte) {
 }
 
 // True when one of the 7 scale bytes of a token (bytes 0..6 of w) is 255.
+// Bytes equal to 255 become 0 in the complements; the pad byte 7 is cleared
+// first, so its complement is 0xff and never counts.
 __device__ __forceinline__ bool has_scale_255(uint2 w) {
-  const uint32_t a = ~w.x, b = ~(w.y | 0xff000000u);  // bytes equal to 255 become 0
+  const uint32_t a = ~w.x, b = ~(w.y & 0x00ffffffu);
   return (((a - 0x01010101u) & ~a) | ((b - 0x01010101u) & ~b)) & 0x80808080u;
+}
+
+// The software decode alone (for sub-tiles that hold a scale byte of 255).
+__device__ __forceinline__ uint4 dequant8_bf16_sw(uint2 w, uint32_t sbyte) {
+  const float s = ue8m0_to_f32(sbyte);
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t word = i < 2 ? w.x : w.y;
+    const uint32_t b0 = (word >> (16 * (i & 1))) & 0xffu;
+    const uint32_t b1 = (word >> (16 * (i & 1) + 8)) & 0xffu;
+    o[i] = static_cast<uint32_t>(float_to_bf16_bits(e4m3_to_f32(b0) * s)) |
+           (static_cast<uint32_t>(float_to_bf16_bits(e4m3_to_f32(b1) * s)) << 16);
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
 __device__ __forceinline__ uint4 dequant8_bf16(uint2 w, uint32_t sbyte) {
@@ -744,6 +761,351 @@ __global__ __launch_bounds__(kMfmaThreads) void dsv4_mfma_kernel(const bf16* __r
   }
 }
 
+// ---------------------------------------------------------------------------
+// Per-query grouped-head kernel (bf16 queries, automatic tiling): one
+// workgroup = (query, 16 heads) and the query's WHOLE slot list, so each
+// latent row is fetched once per workgroup, the split partials never leave
+// the CU and there is no merge launch.  Head groups of one query are blocks
+// b, b + 8, b + 16, ... -- the same XCD (blocks go to XCD blockIdx % 8), so
+// at H = 64 the four workgroups that read a query's rows share one L2.
+//
+// The 4 wavefronts split the slot list in 16-slot sub-tiles (wave w takes
+// sub-tiles w, w + 4, ...).  Per sub-tile a wavefront
+//   * loads the 16 rows (lane l: slot l%16, 16-byte chunks l/16 + 4i of the
+//     576-byte row, and the slot's 8 scale bytes), dequantises the e4m3 part
+//     to bf16 exactly as the reference dequant rounds it, and stores the
+//     [slot][dim] tile in its own LDS slice;
+//   * computes S^T = K Q^T on v_mfma_f32_16x16x32_bf16 (A = the tile row of
+//     slot l%16, read 16 bytes at a time; B = the query rows, in registers):
+//     lane l holds S^T[slot 4(l/16)+e][head l%16];
+//   * runs the online softmax of head l%16 over its 4 slots and the 3 lanes
+//     with the same l%16 (row swaps 16 and 32); the probabilities, rounded to
+//     bf16, are already the B operand of the PV product below;
+//   * accumulates O^T = V^T P^T on v_mfma_f32_16x16x16_bf16, 32 blocks of 16
+//     output dims; the A operand V^T[dim][slot 4g..4g+3] comes straight out
+//     of the row-major tile through ds_read_b64_tr_b16.  Lane l holds
+//     O^T[dim 16 blk + 4(l/16) + e][head l%16], so the softmax rescale of a
+//     lane is its own head's factor -- no transposes anywhere.
+// Finally the 4 wavefronts' (m, l, O) partials meet in LDS and each wavefront
+// merges a quarter of the output dims with the sink as a virtual token of
+// logit sink[h] and value 0 (csrc/dsv4_attention.cu:252-269).
+// MFMA lane layouts: 16x16x32 as above; 16x16x16: A lane l elem j =
+// A[l%16][4(l/16)+j], B lane l elem j = B[4(l/16)+j][l%16], C as 16x16x32.
+// ---------------------------------------------------------------------------
+constexpr int kQSub = 16;                 // slots per sub-tile
+constexpr int kQWaves = 4;
+constexpr int kQThreads = kQWaves * kWave;
+constexpr int kQHeads = 16;
+// LDS tile row: 536 bf16 = 1072 B = 67 16-byte units = 268 dwords (12 mod 64
+// banks).  The dequant's 16-byte stores (16 lanes: slots 0..15 of one column)
+// and the 16-byte A reads (slot l%16) step 3 units per slot, a permutation of
+// the 16 units of the 64 banks; the 4 rows of a transpose read (8 bytes x 4
+// lanes each) land on banks [0,8), [12,20), [24,32), [36,44): all
+// conflict-free.
+constexpr int kQRow = kDim + 24;
+constexpr int kQTileBytes = kQSub * kQRow * 2;
+// Merge rows: 516 floats (4 mod 64 banks), so the 16 heads' 16-byte stores
+// of one lane group cover all 64 banks.
+constexpr int kQOutStride = kDim + 4;
+constexpr int kQMergeBytes = kQWaves * kQHeads * kQOutStride * 4;
+constexpr int kQSmemBytes = kQMergeBytes > kQWaves * kQTileBytes ? kQMergeBytes : kQWaves * kQTileBytes;
+constexpr int kQBuf = 2;                  // sub-tiles of rows in flight per wavefront
+constexpr int kQNopeChunks = kNope / 16;  // 28 chunks of 16 e4m3 bytes
+constexpr int kQChunksPerLane = 9;        // 7 e4m3 chunks + 2 rope chunks
+
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
+
+struct QueryArgs {
+  int64_t nq;
+  int groups;         // head groups of 16
+  int nsub;           // 16-slot sub-tiles of the slot list
+  const float* sink;  // [heads] or null
+  bf16* out;
+};
+
+// One sub-tile of a lane's row data, as loaded.
+struct QRows {
+  uint4 c[kQChunksPerLane];
+  uint2 sc;
+  bool ok;
+};
+
+__global__ __launch_bounds__(kQThreads) void dsv4_query_kernel(const bf16* __restrict__ q, Dsv4Args a,
+                                                               QueryArgs g) {
+  __shared__ __align__(16) uint8_t smem[kQSmemBytes];
+  __shared__ float qml[kQWaves][kQHeads][2];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int lane = tid % kWave;
+  const int grp = lane / 16;
+  const int l16 = lane % 16;
+  const uint32_t blk = blockIdx.x;
+  const uint32_t r = blk / 8;
+  const int hg = static_cast<int>(r % static_cast<uint32_t>(g.groups));
+  const int64_t query = static_cast<int64_t>(r / static_cast<uint32_t>(g.groups)) * 8 + blk % 8;
+  if (query >= g.nq) return;
+  const int h0 = hg * kQHeads;
+  const int nh = min(kQHeads, a.heads - h0);
+
+  // Prologue batch: the query rows (B operand of S^T: head h0 + l16, dims
+  // 32 kk + 8 grp .. +7; heads past nh re-read head h0 + nh - 1 and are
+  // zeroed), the lengths and the sink -- unconditional loads, consumed later.
+  const void* anyp = static_cast<const void*>(q);
+  const int32_t len_raw = load_global_i32(a.lens ? static_cast<const void*>(a.lens + query) : anyp);
+  const int32_t elen_raw = load_global_i32(a.elens ? static_cast<const void*>(a.elens + query) : anyp);
+
+  const int total = a.topk_slots + a.extra_slots;
+  const uint8_t* dummy = reinterpret_cast<const uint8_t*>(q + (query * a.heads + h0) * kDim);  // >= 1 KiB, in bounds
+  // Slot index of sub-tile t for this lane (slot 16 t + l16): both index
+  // loads are unconditional (clamped positions), the choice comes later.
+  struct SlotIdx {
+    int32_t li, le;
+  };
+  auto idx_issue = [&](int t) -> SlotIdx {
+    const int s = t * kQSub + l16;
+    const int32_t* ip = a.topk_slots > 0 ? a.idx + query * a.topk_slots + min(s, a.topk_slots - 1)
+                                         : reinterpret_cast<const int32_t*>(dummy);
+    const int32_t* ep = a.extra_slots > 0
+                            ? a.eidx + query * a.extra_slots + min(max(s - a.topk_slots, 0), a.extra_slots - 1)
+                            : reinterpret_cast<const int32_t*>(dummy);
+    return SlotIdx{load_global_i32(ip), load_global_i32(ep)};
+  };
+  int n_swa = 0, n_extra = 0;  // set once the length loads are consumed
+  auto rows_issue = [&](int t, SlotIdx si, QRows& rw) {
+    const int s = t * kQSub + l16;
+    const bool in_swa = s < a.topk_slots;
+    const bool valid = s < total && (in_swa ? s < n_swa : s - a.topk_slots < n_extra);
+    const int32_t loc = valid ? (in_swa ? si.li : si.le) : -1;
+    const uint8_t* sr = nullptr;
+    const uint8_t* rr = loc >= 0 ? row_ptr(in_swa ? a.swa : a.extra, loc, &sr) : nullptr;
+    rw.ok = rr != nullptr;
+    const uint8_t* rp = rw.ok ? rr : dummy;
+    const uint8_t* sp = rw.ok ? sr : dummy;
+#pragma unroll
+    for (int i = 0; i < 7; ++i) rw.c[i] = load_global_u4(rp + 16 * (grp + 4 * i));
+#pragma unroll
+    for (int i = 0; i < 2; ++i) rw.c[7 + i] = load_global_u4(rp + kNope + 16 * (grp + 4 * i));
+    rw.sc = load_global_u2(sp);
+  };
+
+  const int nsub_w = g.nsub > wave ? (g.nsub - wave + kQWaves - 1) / kQWaves : 0;  // this wave's sub-tiles
+  static_assert(kQBuf == 2, "two row buffers below");
+  const int last_sub = max(g.nsub - 1, 0);
+  SlotIdx si0 = idx_issue(min(wave, last_sub)), si1 = idx_issue(min(wave + kQWaves, last_sub));
+  // The query rows and the sink go out after the lengths and the first
+  // indices, so waiting for those (the rows' addresses) does not wait for them.
+  uint4 qw[16];
+  const int hq = h0 + min(l16, nh - 1);
+#pragma unroll
+  for (int kk = 0; kk < 16; ++kk) qw[kk] = load_global_u4(q + (query * a.heads + hq) * kDim + 32 * kk + 8 * grp);
+  const float sink_raw = g.sink ? load_global_raw<float>(g.sink + hq) : -INFINITY;
+  asm volatile("" : "+v"(si0.li), "+v"(si0.le), "+v"(si1.li), "+v"(si1.le));
+  n_swa = a.lens ? max(0, min(len_raw, a.topk_slots)) : a.topk_slots;
+  n_extra = a.extra_slots > 0 ? (a.elens ? max(0, min(elen_raw, a.extra_slots)) : a.extra_slots) : 0;
+  // Sub-tile t of this wave is global sub-tile wave + 4 t; past the list a
+  // buffer is loaded from the dummy row with no valid slot.
+  auto sub_of = [&](int t) { return t < nsub_w ? wave + kQWaves * t : g.nsub; };
+  QRows cur, nxt;  // rows of this wave's sub-tiles t and t + 1
+  rows_issue(sub_of(0), si0, cur);
+  rows_issue(sub_of(1), si1, nxt);
+  SlotIdx sn = idx_issue(min(wave + kQWaves * kQBuf, last_sub));  // indices of sub-tile kQBuf
+  bf16x8_t qb[16];
+#pragma unroll
+  for (int kk = 0; kk < 16; ++kk) qb[kk] = __builtin_bit_cast(bf16x8_t, l16 < nh ? qw[kk] : make_uint4(0u, 0u, 0u, 0u));
+
+  uint16_t* tile = reinterpret_cast<uint16_t*>(smem + wave * kQTileBytes);
+  float m = -INFINITY, l = 0.f;  // online softmax of head l16 (this lane's 4 slots per sub-tile)
+  f32x4_t o[kDim / 16];
+#pragma unroll
+  for (int j = 0; j < kDim / 16; ++j) o[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  auto process = [&](const QRows& rw) {
+    const uint32_t valid16 = static_cast<uint32_t>(__ballot(rw.ok) & 0xffffull);  // slot bits (lanes 0..15)
+    if (valid16 == 0u) return;  // wave-uniform
+    // Scale byte 255 takes the software decode, decided once per sub-tile.
+    const bool any255 = __ballot(rw.ok && has_scale_255(rw.sc)) != 0ull;
+    uint16_t* trow = tile + l16 * kQRow;
+    if (!any255) {
+#pragma unroll
+      for (int i = 0; i < 7; ++i) {
+        const uint32_t sbyte = (i < 4 ? rw.sc.x >> (8 * i) : rw.sc.y >> (8 * (i - 4))) & 0xffu;
+        uint4 lo = dequant8_bf16_hw(make_uint2(rw.c[i].x, rw.c[i].y), sbyte);
+        uint4 hi = dequant8_bf16_hw(make_uint2(rw.c[i].z, rw.c[i].w), sbyte);
+        if (!rw.ok) lo = hi = make_uint4(0u, 0u, 0u, 0u);  // skipped slot: zero K and V
+        const int c = grp + 4 * i;
+        *reinterpret_cast<uint4*>(trow + 16 * c) = lo;
+        *reinterpret_cast<uint4*>(trow + 16 * c + 8) = hi;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 7; ++i) {  // rare (a scale byte of 255): the software decode
+        const uint32_t sbyte = (i < 4 ? rw.sc.x >> (8 * i) : rw.sc.y >> (8 * (i - 4))) & 0xffu;
+        uint4 lo = dequant8_bf16_sw(make_uint2(rw.c[i].x, rw.c[i].y), sbyte);
+        uint4 hi = dequant8_bf16_sw(make_uint2(rw.c[i].z, rw.c[i].w), sbyte);
+        if (!rw.ok) lo = hi = make_uint4(0u, 0u, 0u, 0u);
+        const int c = grp + 4 * i;
+        *reinterpret_cast<uint4*>(trow + 16 * c) = lo;
+        *reinterpret_cast<uint4*>(trow + 16 * c + 8) = hi;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      *reinterpret_cast<uint4*>(trow + kNope + 8 * (grp + 4 * i)) = rw.ok ? rw.c[7 + i] : make_uint4(0u, 0u, 0u, 0u);
+    wave_lds_sync();
+    // The A reads go out 8 at a time ahead of their MFMAs (one LDS round trip
+    // per 8, not per MFMA); two accumulators halve the dependent MFMA chain.
+    f32x4_t sacc0 = f32x4_t{0.f, 0.f, 0.f, 0.f}, sacc1 = sacc0;
+#pragma unroll
+    for (int k0 = 0; k0 < 16; k0 += 8) {
+      uint4 kr[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) kr[u] = *reinterpret_cast<const uint4*>(trow + 32 * (k0 + u) + 8 * grp);
+#pragma unroll
+      for (int u = 0; u < 8; u += 2) {
+        sacc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kr[u]), qb[k0 + u], sacc0, 0, 0, 0);
+        sacc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kr[u + 1]), qb[k0 + u + 1], sacc1,
+                                                        0, 0, 0);
+      }
+    }
+    float x[4];
+    float mt = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[e] = ((valid16 >> (4 * grp + e)) & 1u) ? (sacc0[e] + sacc1[e]) * a.qscale : -INFINITY;
+      mt = fmaxf(mt, x[e]);
+    }
+    mt = fmaxf(mt, __uint_as_float(lane_xor<16>(__float_as_uint(mt), lane)));
+    mt = fmaxf(mt, __uint_as_float(lane_xor<32>(__float_as_uint(mt), lane)));
+    // Lazy rescale: the running max m only moves when a score exceeds it by
+    // more than 2^8 (so probabilities stay below 2^8, exact enough in fp32
+    // and as bf16 PV operands) or on the first valid sub-tile; the output
+    // accumulators are rescaled only when some head of the wavefront moved.
+    const bool move = mt > m + 8.f;  // m = -inf: always
+    const float m_new = move ? mt : m;  // finite: the sub-tile has a valid slot
+    const float alpha = move ? fast_exp2(m - m_new) : 1.f;
+    float p[4];
+    float ps = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      p[e] = fast_exp2(x[e] - m_new);
+      ps += p[e];
+    }
+    l = l * alpha + ps;
+    m = m_new;
+    const bool rescale = __any(move);
+    const i16x4_t pb = __builtin_bit_cast(
+        i16x4_t, make_uint2(static_cast<uint32_t>(float_to_bf16_bits(p[0])) |
+                                (static_cast<uint32_t>(float_to_bf16_bits(p[1])) << 16),
+                            static_cast<uint32_t>(float_to_bf16_bits(p[2])) |
+                                (static_cast<uint32_t>(float_to_bf16_bits(p[3])) << 16)));
+    // V^T A operand of output block j: lane a of group g passes &V[4g + a/4][16 j + 4(a%4)].
+    const uint16_t* vsrc = tile + (4 * grp + l16 / 4) * kQRow + 4 * (l16 % 4);
+    if (rescale) {
+#pragma unroll
+      for (int j = 0; j < kDim / 16; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[j][e] *= alpha;
+    }
+#pragma unroll
+    for (int j0 = 0; j0 < kDim / 16; j0 += 8) {  // transposed reads 8 at a time ahead of their MFMAs
+      i16x4_t vt[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) vt[u] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(vsrc + 16 * (j0 + u)));
+#pragma unroll
+      for (int u = 0; u < 8; ++u) o[j0 + u] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt[u], pb, o[j0 + u], 0, 0, 0);
+    }
+    wave_lds_sync();  // the tile is rewritten by the next sub-tile
+  };
+
+  // One sub-tile per iteration (a single copy of its code: the kernel stays
+  // well inside the instruction cache); the row buffers rotate through
+  // registers and the rows kQBuf sub-tiles ahead are requested as soon as a
+  // buffer frees up, with their indices requested one round earlier.
+  for (int it = 0; it < nsub_w; ++it) {
+    process(cur);
+    cur = nxt;
+    if (it + kQBuf < nsub_w) {
+      rows_issue(sub_of(it + kQBuf), sn, nxt);
+      sn = idx_issue(min(wave + kQWaves * (it + kQBuf + 1), last_sub));
+    }
+  }
+  l += __uint_as_float(lane_xor<16>(__float_as_uint(l), lane));
+  l += __uint_as_float(lane_xor<32>(__float_as_uint(l), lane));
+
+  // Merge the 4 wavefronts' partials (the merge buffer reuses the tiles).
+  __syncthreads();
+  float* mrg = reinterpret_cast<float*>(smem);
+  if (l16 < nh) {
+#pragma unroll
+    for (int j = 0; j < kDim / 16; ++j)
+      *reinterpret_cast<f32x4_t*>(mrg + (wave * kQHeads + l16) * kQOutStride + 16 * j + 4 * grp) = o[j];
+    if (grp == 0) {
+      qml[wave][l16][0] = m;
+      qml[wave][l16][1] = l;
+    }
+  }
+  __syncthreads();
+  // Lane h < 16 forms head h's merge weights (w_j = 2^(m_j - M) for the 4
+  // wavefronts' partials, 1/L with the sink's 2^(sink - M)); every lane then
+  // takes them as scalars (readlane) and merges its 2 dims of the wavefront's
+  // quarter of the output for each head, the partial reads batched 4 heads
+  // at a time.
+  float wj[kQWaves], inv;
+  {
+    const int hh = min(l16, nh - 1);
+    float mj[kQWaves], lj[kQWaves];
+#pragma unroll
+    for (int j = 0; j < kQWaves; ++j) {
+      mj[j] = qml[j][hh][0];
+      lj[j] = qml[j][hh][1];
+    }
+    const float sk = g.sink ? sink_raw * kLog2e : -INFINITY;
+    float mx = sk;
+    bool nan_in = false;  // a NaN/inf score makes the softmax NaN, as torch.softmax does
+#pragma unroll
+    for (int j = 0; j < kQWaves; ++j) {
+      if (lj[j] > 0.f) mx = fmaxf(mx, mj[j]);
+      nan_in = nan_in || lj[j] != lj[j];
+    }
+    float L = 0.f;
+#pragma unroll
+    for (int j = 0; j < kQWaves; ++j) {
+      wj[j] = (lj[j] > 0.f && mx != -INFINITY) ? fast_exp2(mj[j] - mx) : 0.f;
+      L = fmaf(wj[j], lj[j] > 0.f ? lj[j] : 0.f, L);
+    }
+    if (g.sink && mx != -INFINITY) L += fast_exp2(sk - mx);
+    inv = nan_in ? __builtin_nanf("") : (L > 0.f ? 1.f / L : 0.f);
+  }
+  const int d = (kDim / kQWaves) * wave + 2 * lane;
+  bf16* orow = g.out + (query * a.heads + h0) * kDim + d;
+  for (int hb = 0; hb < nh; hb += 4) {
+    float2 v[4][kQWaves];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int j = 0; j < kQWaves; ++j)
+        v[u][j] = *reinterpret_cast<const float2*>(mrg + (j * kQHeads + min(hb + u, kQHeads - 1)) * kQOutStride + d);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int h = hb + u;
+      if (h < nh) {
+        float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+        for (int j = 0; j < kQWaves; ++j) {
+          const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wj[j]), h));
+          a0 = fmaf(w, v[u][j].x, a0);
+          a1 = fmaf(w, v[u][j].y, a1);
+        }
+        const float iv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, inv), h));
+        *reinterpret_cast<uint32_t*>(orow + static_cast<int64_t>(h) * kDim) =
+            static_cast<uint32_t>(float_to_bf16_bits(a0 * iv)) | (static_cast<uint32_t>(float_to_bf16_bits(a1 * iv)) << 16);
+      }
+    }
+  }
+}
+
 constexpr int kMergeThreads = kDim / 4;  // 4 output columns per thread
 constexpr int kMergeChunk = 1024;        // tile weights staged in LDS per pass
 constexpr int kMergeFastTiles = 16;      // tiles merged straight from registers
@@ -783,9 +1145,12 @@ __global__ __launch_bounds__(kMergeThreads) void dsv4_merge_kernel(const float* 
     }
     const float sk = sink ? sink[head] * kLog2e : -INFINITY;
     float mx = sk;
+    bool nan_in = false;  // a NaN/inf score makes the softmax NaN, as torch.softmax does
 #pragma unroll
-    for (int t = 0; t < kMergeFastTiles; ++t)
+    for (int t = 0; t < kMergeFastTiles; ++t) {
       if (t < num_tiles && v[t].y > 0.f) mx = fmaxf(mx, v[t].x);
+      nan_in = nan_in || (t < num_tiles && v[t].y != v[t].y);
+    }
     float L = 0.f;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     if (mx != -INFINITY) {
@@ -802,7 +1167,7 @@ __global__ __launch_bounds__(kMergeThreads) void dsv4_merge_kernel(const float* 
       }
       if (sink) L += fast_exp2(sk - mx);
     }
-    const float inv = L > 0.f ? 1.f / L : 0.f;
+    const float inv = nan_in ? __builtin_nanf("") : (L > 0.f ? 1.f / L : 0.f);
     T* o = out + qh * kDim + d;
     o[0] = from_f32<T>(acc.x * inv);
     o[1] = from_f32<T>(acc.y * inv);
@@ -813,10 +1178,13 @@ __global__ __launch_bounds__(kMergeThreads) void dsv4_merge_kernel(const float* 
   if (tid < kWave) {
     const float sk = sink ? sink[head] * kLog2e : -INFINITY;
     float mx = -INFINITY;
+    bool nan_in = false;
     for (int t = tid; t < num_tiles; t += kWave) {
       const float2 v = ml[t];
       if (v.y > 0.f) mx = fmaxf(mx, v.x);
+      nan_in = nan_in || v.y != v.y;
     }
+    nan_in = __any(nan_in);
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, xor_lanes(mx, off));
     mx = fmaxf(mx, sk);
@@ -831,7 +1199,7 @@ __global__ __launch_bounds__(kMergeThreads) void dsv4_merge_kernel(const float* 
     if (tid == 0) {
       if (sink && mx != -INFINITY) L += fast_exp2(sk - mx);
       s_mx = mx;
-      s_inv = L > 0.f ? 1.f / L : 0.f;
+      s_inv = nan_in ? __builtin_nanf("") : (L > 0.f ? 1.f / L : 0.f);
     }
   }
   __syncthreads();
@@ -914,6 +1282,21 @@ bool mfma_enabled() {
   return !(e && e[0] == '0');
 }
 
+// The per-query kernel takes a call when there are at least 64 (query, head
+// group) workgroups: each latent row is then fetched once per query and no
+// partial leaves the CU.  With fewer, one workgroup's sequential sub-tiles
+// (about 3 us each) outweigh that, and the split kernel + merge, whose splits
+// spread a query over many CUs, is faster (measured: nq 32 x H 64 15.2-18.7 us
+// per call against 18.3-21.4; nq 1 and nq 32 x H 8 8.9-11 us against 12-16).
+// CSAHCA_DSV4_QUERY=0 / =1 forces the choice (read per call).
+bool use_query_kernel(int64_t nq, int64_t heads, int64_t total_slots) {
+  const char* e = std::getenv("CSAHCA_DSV4_QUERY");
+  if (e && (e[0] == '0' || e[0] == '1')) return e[0] == '1';
+  (void)total_slots;
+  const int64_t groups = ceil_div(std::max<int64_t>(1, heads), kQHeads);
+  return nq * groups >= 64;
+}
+
 struct Dsv4Call {
   const void* q;
   int dtype;
@@ -976,6 +1359,18 @@ int dsv4_run(const Dsv4Call& c) {
   a.num_tiles = static_cast<int>(tiles);
   a.qscale = static_cast<float>(c.softmax_scale) * kLog2e;
   hipStream_t stream = static_cast<hipStream_t>(c.stream);
+  if (use_mfma && use_query_kernel(c.nq, c.heads, total)) {
+    QueryArgs qa;
+    qa.nq = c.nq;
+    qa.groups = static_cast<int>(ceil_div(c.heads, kQHeads));
+    qa.nsub = static_cast<int>(ceil_div(total, kQSub));
+    qa.sink = c.sink;
+    qa.out = static_cast<bf16*>(c.out);
+    const int64_t blocks = ceil_div(c.nq, 8) * 8 * qa.groups;  // query q's groups: blocks q%8 + 8 (g + G q/8)
+    CSAHCA_REQUIRE(blocks <= INT32_MAX, "too many DSV4 work items");
+    return launch("dsv4_query_kernel", dsv4_query_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kQThreads), 0,
+                  stream, static_cast<const bf16*>(c.q), a, qa);
+  }
   if (use_mfma) {
     MfmaArgs mm;
     mm.splits = static_cast<int>(tiles);

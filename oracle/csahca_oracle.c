@@ -486,7 +486,11 @@ ORC_API void orc_dsv4_attention(const float* q, int64_t nq, int64_t H, const uin
         sum += sc[t];
       }
       for (int d = 0; d < DSV4_DIM; ++d) o[d] = 0.0;
-      if (n == 0 || !(sum > 0.0)) continue;
+      /* No rows: the reference's softmax/mv over an empty (or sink-only) set
+       * gives zeros.  Otherwise a NaN or infinite score (a scale byte of 255
+       * decodes to 2^128 = inf in fp32) makes the softmax, and so the output,
+       * NaN exactly as torch.softmax does (:139-140). */
+      if (n == 0) continue;
       for (int64_t t = 0; t < n; ++t) {
         const double p = sc[t] / sum;
         for (int d = 0; d < DSV4_DIM; ++d) o[d] += p * (double)rows[t * DSV4_DIM + d];

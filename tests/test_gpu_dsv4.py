@@ -150,9 +150,13 @@ def test_unaligned_bytes_per_page_scalar_path():
     assert_close(gpu_out(c), oracle_out(c))
 
 
-def test_e4m3_and_scale_decode_exhaustive():
-    """Single valid slot, no sink, fp32 query: out = the dequantised row exactly.
-    Rows cover all 256 e4m3 codes (NaN codes excluded) under many scale bytes."""
+@pytest.mark.parametrize("path", ["valu-f32", "query-bf16", "split-bf16"])
+def test_e4m3_and_scale_decode_exhaustive(path, monkeypatch):
+    """Single valid slot, no sink: out = the dequantised row exactly (softmax
+    weight 1).  Rows cover all 256 e4m3 codes (NaN codes excluded) under many
+    scale bytes.  fp32 queries take the VALU kernel; bf16 queries the per-query
+    MFMA kernel or the split MFMA kernel + merge (both round the probability
+    1.0 and the bf16 row exactly)."""
     codes = np.array([b for b in range(256) if (b & 0x7F) != 0x7F], dtype=np.uint8)
     ps = 4
     bpp = dsv4_layout.bytes_per_page(ps)
@@ -170,10 +174,12 @@ def test_e4m3_and_scale_decode_exhaustive():
         cache[page, ps * 576 + r * 8:ps * 576 + r * 8 + 7] = [sb + 3 * j for j in range(7)]
     locs = np.arange(n, dtype=np.int32)
     want = oracle.dequant_dsv4_cache(cache, locs, page_size=ps).astype(np.float64)
-    q = torch.zeros(n, 1, 512, dtype=torch.float32, device=DEV)
+    if path != "valu-f32":
+        monkeypatch.setenv("CSAHCA_DSV4_QUERY", "1" if path == "query-bf16" else "0")
+    q = torch.zeros(n, 1, 512, dtype=torch.float32 if path == "valu-f32" else torch.bfloat16, device=DEV)
     idx = torch.from_numpy(locs.reshape(n, 1)).to(DEV)
     out = extension.dsv4_swa_decode_forward(q, torch.from_numpy(cache).to(DEV), idx, None, None, ps, SCALE)
-    got = out[:, 0].cpu().numpy().astype(np.float64)
+    got = out[:, 0].float().cpu().numpy().astype(np.float64)
     # the oracle dequant rounds nope values to bf16 (exact for e4m3 * 2^k)
     assert np.array_equal(got, want)
 
@@ -193,6 +199,55 @@ def test_mfma_path_matches_valu_path_and_oracle(ratio, nq, heads, monkeypatch):
     got_valu = gpu_out(c)
     assert_close(got_mfma, ref, what="mfma")
     assert_close(got_valu, ref, what="valu")
+
+
+@pytest.mark.parametrize("ratio,nq,heads,top_k,extra_top_k", [
+    (0, 1, 8, 128, 0),      # SWA window: 8 sub-tiles, 2 per wavefront
+    (4, 1, 8, 128, 64),     # 12 sub-tiles, 3 per wavefront
+    (128, 1, 64, 128, 64),  # 4 head groups of one query on one XCD
+    (4, 3, 24, 96, 40),     # second head group holds 8 heads
+    (4, 7, 70, 96, 40),     # 5 head groups, the last with 6 heads; 7 queries
+    (0, 2, 16, 600, 0),     # 38 sub-tiles: the row buffers refill 3 times
+    (4, 2, 8, 5, 3),        # 8 slots: one partial sub-tile, three idle wavefronts
+    (4, 9, 16, 40, 9),      # 9 queries: the grid's XCD mapping wraps
+])
+def test_query_kernel_matches_split_kernel_and_oracle(ratio, nq, heads, top_k, extra_top_k, monkeypatch):
+    """The per-query MFMA kernel (CSAHCA_DSV4_QUERY=1) and the split MFMA kernel
+    + merge (=0) against the oracle, with ragged lengths, -1 slots, a slot whose
+    page is past the cache, and with and without the sink."""
+    page = 256 if ratio == 128 else 64
+    c = make_dsv4_case(compress_ratio=ratio, num_queries=nq, heads=heads, num_tokens=1024, top_k=top_k,
+                       page_size=page, extra_tokens=1024, extra_top_k=extra_top_k, seed=31 + heads + top_k,
+                       device=DEV)
+    c.token_indices[0, min(5, top_k - 1)] = -1
+    c.token_indices[-1, 0] = 10_000_000
+    for sink in (True, False):
+        ref = oracle_out(c, sink=sink)
+        for route in ("1", "0"):
+            monkeypatch.setenv("CSAHCA_DSV4_QUERY", route)
+            assert_close(gpu_out(c, sink=sink), ref, what=f"query={route} sink={sink}")
+
+
+@pytest.mark.parametrize("route", ["1", "0"])
+def test_scale_byte_255_gives_nan_like_the_reference(route, monkeypatch):
+    """A scale byte of 255 is 2^128 = inf in the reference's fp32 dequant, so
+    every score of that query is NaN (q . k meets inf) and so is its output;
+    queries whose rows have no such byte stay finite and correct.  The MFMA
+    kernels decode such sub-tiles in software."""
+    monkeypatch.setenv("CSAHCA_DSV4_QUERY", route)
+    c = make_dsv4_case(compress_ratio=0, num_queries=3, heads=8, num_tokens=256, top_k=32, page_size=64, seed=9)
+    cache = c.cache.clone()
+    loc = int(c.token_indices[1, 3])
+    page, r = divmod(loc, 64)
+    cache[page, 64 * 576 + r * 8 + 2] = 255  # one scale byte of one row of query 1
+    c.cache = cache
+    c.topk_lengths = torch.full((3,), 32, dtype=torch.int32)
+    c.token_indices[0].masked_fill_(c.token_indices[0] == loc, (loc + 1) % 256)
+    c.token_indices[2].masked_fill_(c.token_indices[2] == loc, (loc + 1) % 256)
+    ref = oracle_out(c)
+    got = gpu_out(c).float().cpu().numpy()
+    assert np.isnan(ref[1]).all() and np.isnan(got[1]).all()
+    assert_close(torch.from_numpy(got[[0, 2]]), ref[[0, 2]])
 
 
 def test_sglang_adapter_end_to_end(monkeypatch):

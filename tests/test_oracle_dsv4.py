@@ -142,3 +142,37 @@ def test_pack_round_trip_error_bound():
     # e4m3 keeps 4 significant bits: relative error <= 2^-4 of the value; subnormal floor 2^-10 of the tile max
     bound = torch.maximum(ref[:, :448].reshape(64, 7, 64).abs() * 2 ** -4, tile_max * 2 ** -10)
     assert torch.all(err <= bound * 1.0001)
+
+
+def test_scale_byte_255_makes_the_query_nan():
+    """A scale byte of 255 decodes to 2^128 = inf in fp32 (dsv4_correctness.py:76),
+    so that query's scores meet inf and torch.softmax -- the reference's
+    normaliser (:139) -- returns NaN, which the output inherits; other queries
+    are untouched.  Checked against torch.softmax on the oracle's own
+    dequantised rows, and against the oracle with the byte cleared."""
+    import math
+
+    import torch
+
+    from csahca_amd.synthetic import make_dsv4_case
+
+    c = make_dsv4_case(compress_ratio=0, num_queries=3, heads=8, num_tokens=256, top_k=32, page_size=64, seed=9)
+    cache = c.cache.clone()
+    loc = int(c.token_indices[1, 3])
+    page, r = divmod(loc, 64)
+    cache[page, 64 * 576 + r * 8 + 2] = 255
+    for qi in (0, 2):
+        c.token_indices[qi].masked_fill_(c.token_indices[qi] == loc, (loc + 1) % 256)
+    lens = torch.full((3,), 32, dtype=torch.int32)
+    scale = 1.0 / math.sqrt(512)
+    out = oracle.dsv4_reference_attention(c.q, cache, c.token_indices, lens, c.attn_sink, page_size=64,
+                                          softmax_scale=scale)
+    rows = torch.from_numpy(oracle.dequant_dsv4_cache(cache.numpy(), c.token_indices[1].numpy().astype(np.int32),
+                                                      page_size=64).astype(np.float32))
+    assert torch.isinf(rows).any()
+    scores = torch.cat([c.attn_sink[:1], rows @ c.q[1, 0].float() * scale])
+    assert torch.isnan(torch.softmax(scores, dim=0)).all()
+    assert np.isnan(out[1]).all()
+    clean = oracle.dsv4_reference_attention(c.q, c.cache, c.token_indices, lens, c.attn_sink, page_size=64,
+                                            softmax_scale=scale)
+    assert np.isfinite(out[[0, 2]]).all() and np.array_equal(out[[0, 2]], clean[[0, 2]])
