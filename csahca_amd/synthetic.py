@@ -42,24 +42,32 @@ def make_synthetic_case(*, batch: int = 1, heads: int = 8, seq_len: int = 4096, 
 
 
 def plant_chunks(q: torch.Tensor, k_cache: torch.Tensor, chunks: torch.Tensor, chunk_size: int,
-                 alpha: float) -> torch.Tensor:
-    """Return a copy of ``k_cache`` whose listed chunks are biased towards ``q``.
+                 alpha: float, *, inplace: bool = False) -> torch.Tensor:
+    """Bias the listed chunks of ``k_cache`` towards ``q``.
 
-    ``chunks`` is ``[B, H, n]``; every token of chunk ``chunks[b,h,j]`` gets
-    ``(alpha * (n - j)) * q_hat`` added (``q_hat`` = unit ``q[b,h]``), so the
+    ``chunks`` is ``[B, H, n]`` (distinct ids per head); every token of chunk
+    ``chunks[b,h,j]`` gets ``(alpha * (n - j)) * q_hat`` added in fp32
+    (``q_hat`` = unit ``q[b,h]``) and is rounded back to the cache dtype, so the
     selected set AND its score order are known in advance when ``alpha`` dwarfs
-    the spread of the unbiased chunk scores.
+    the spread of the unbiased chunk scores.  Only the planted rows are read and
+    written (on whatever device the tensors live); returns a copy unless
+    ``inplace``.
     """
-    k = k_cache.float().clone()
+    k = k_cache if inplace else k_cache.clone()
+    B, H, S, D = k.shape
+    n = chunks.shape[-1]
+    C = S // chunk_size
     qf = q.float()
-    q_hat = qf / qf.norm(dim=-1, keepdim=True)
-    B, H, n = chunks.shape
-    for b in range(B):
-        for h in range(H):
-            for j in range(n):
-                c = int(chunks[b, h, j])
-                k[b, h, c * chunk_size:(c + 1) * chunk_size] += alpha * (n - j) * q_hat[b, h]
-    return k.to(k_cache.dtype)
+    q_hat = qf / qf.norm(dim=-1, keepdim=True)                                      # [B, H, D]
+    weight = alpha * (n - torch.arange(n, dtype=torch.float32, device=k.device))     # [n]
+    bias = weight[None, None, :, None] * q_hat.to(k.device)[:, :, None, :]           # [B, H, n, D]
+    kv = k[:, :, :C * chunk_size].view(B, H, C, chunk_size, D)
+    bi = torch.arange(B, device=k.device)[:, None, None]
+    hi = torch.arange(H, device=k.device)[None, :, None]
+    ci = chunks.to(device=k.device, dtype=torch.long)
+    rows = kv[bi, hi, ci].float()                                                   # [B, H, n, chunk, D]
+    kv[bi, hi, ci] = (rows + bias[:, :, :, None, :]).to(k.dtype)
+    return k
 
 
 def scattered_chunks(batch: int, heads: int, num_chunks: int, top_k: int) -> torch.Tensor:
@@ -137,6 +145,47 @@ def make_dsv4_case(*, compress_ratio: int, num_queries: int = 7, heads: int = 8,
         case.cache = pack_dsv4_cache(case.k_tokens.to(device), page_size=page_size)
         if compress_ratio:
             case.extra_cache = pack_dsv4_cache(case.extra_tokens.to(device), page_size=case.extra_page_size)
+    for name in ("q", "k_tokens", "token_indices", "topk_lengths", "attn_sink", "extra_tokens",
+                 "extra_token_indices", "extra_topk_lengths"):
+        t = getattr(case, name)
+        if t is not None:
+            setattr(case, name, t.to(device))
+    return case
+
+
+def make_dsv4_bench_case(*, compress_ratio: int, num_queries: int = 1, heads: int = 8, num_tokens: int = 4096,
+                         top_k: int = 64, page_size: int = 256, extra_tokens: int = 4096, extra_top_k: int = 0,
+                         q_dtype: torch.dtype = torch.bfloat16, seed: int = 0,
+                         device: str | torch.device = "cpu") -> Dsv4Case:
+    """The inputs of the reference DSV4 benchmark harness
+    (hybrid_attention/dsv4_benchmark.py:30-76) on a CPU generator: q, k_tokens,
+    token_indices (uniform over the pool), full lengths, sink, then for
+    compress_ratio 4/128 extra_tokens and extra_token_indices; extra page size
+    ``page_size // compress_ratio``; extra_top_k defaults to 512 (C4) / 128 (C128).
+    Its published H100 cases are nq 1, H 8, top_k 64, page 256 with extra_top_k
+    128 (C4) and 64 (C128) (docs/dsv4_abi_status.md:64-65)."""
+    g = torch.Generator(device="cpu")
+    g.manual_seed(seed)
+    q = torch.randn(num_queries, heads, HEAD_DIM, dtype=q_dtype, generator=g)
+    k_tokens = torch.randn(num_tokens, HEAD_DIM, dtype=torch.bfloat16, generator=g)
+    token_indices = torch.randint(0, num_tokens, (num_queries, top_k), dtype=torch.int32, generator=g)
+    topk_lengths = torch.full((num_queries,), top_k, dtype=torch.int32)
+    attn_sink = torch.randn(heads, dtype=torch.float32, generator=g)
+    case = Dsv4Case(q=q, k_tokens=k_tokens, cache=None, token_indices=token_indices, topk_lengths=topk_lengths,
+                    attn_sink=attn_sink, page_size=page_size)
+    if compress_ratio:
+        eps = page_size // compress_ratio
+        if eps <= 0:
+            raise ValueError("page_size // compress_ratio must be positive")
+        etop = extra_top_k or (512 if compress_ratio == 4 else 128)
+        case.extra_tokens = torch.randn(extra_tokens, HEAD_DIM, dtype=torch.bfloat16, generator=g)
+        case.extra_token_indices = torch.randint(0, extra_tokens, (num_queries, etop), dtype=torch.int32,
+                                                 generator=g)
+        case.extra_topk_lengths = torch.full((num_queries,), etop, dtype=torch.int32)
+        case.extra_page_size = eps
+    case.cache = pack_dsv4_cache(case.k_tokens.to(device), page_size=page_size)
+    if compress_ratio:
+        case.extra_cache = pack_dsv4_cache(case.extra_tokens.to(device), page_size=case.extra_page_size)
     for name in ("q", "k_tokens", "token_indices", "topk_lengths", "attn_sink", "extra_tokens",
                  "extra_token_indices", "extra_topk_lengths"):
         t = getattr(case, name)

@@ -175,3 +175,29 @@ def test_slot_order_is_irrelevant():
     a = oracle.csa_attend(case.q, case.k_cache, case.v_cache, idx, 64)
     b = oracle.csa_attend(case.q, case.k_cache, case.v_cache, idx[..., ::-1].copy(), 64)
     np.testing.assert_allclose(a, b, rtol=0, atol=1e-12)
+
+
+def test_torch_restatement_golden_and_oracle(small):
+    """oracle/torch_csa.py (the CPU baseline's torch-ops restatement) reproduces
+    the reference's golden selection and output, and the C oracle's step at a
+    larger shape (ids exactly; outputs within one bf16 ulp)."""
+    from oracle import torch_csa
+
+    def t(bits):
+        return torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16)
+
+    q, k, v = t(small["q"]), t(small["k"]), t(small["v"])
+    summ = torch.from_numpy(oracle.chunk_mean(bf16(small["k"]), 64).astype(np.float32))
+    idx = torch_csa.select_topk(q, summ, 4)
+    assert np.array_equal(idx.numpy(), small["selected"])
+    out = torch_csa.attend(q, k, v, idx, 64).float().numpy()
+    want = bf16(small["csa_out"])
+    assert np.all(np.abs(out - want) <= np.abs(want) * 2.0 ** -7 + 1e-6)
+    case = make_synthetic_case(batch=1, heads=4, seq_len=8192, head_dim=128, chunk_size=64, top_k=8, seed=5)
+    summ = torch.from_numpy(oracle.chunk_mean(case.k_cache, 64).astype(np.float32))
+    got = torch_csa.decode_step(case.q, case.k_cache, case.v_cache, summ, 64, 8).float().numpy()
+    want_idx, _ = oracle.select_topk(case.q, summ.numpy(), 8)
+    assert np.array_equal(torch_csa.select_topk(case.q, summ, 8).numpy(), want_idx)
+    ref = oracle.round_to(oracle.csa_attend(case.q, case.k_cache, case.v_cache, want_idx, 64,
+                                            prob_dtype=oracle.BF16), torch.bfloat16)
+    assert np.all(np.abs(got - ref) <= np.abs(ref) * 2.0 ** -7 + 1e-6), np.abs(got - ref).max()
