@@ -136,3 +136,49 @@ def test_prepare_indices_from_decode_metadata():
     core.swa_page_indices = torch.ones(4, 2, 16, dtype=torch.int32)
     with pytest.raises(RuntimeError, match="unsupported DSV4 SWA index shape"):
         sglang_dsv4.prepare_swa_indices(core=core, q=q)
+
+
+@pytest.mark.parametrize("change,msg", [
+    (dict(extra_indices=torch.zeros(3, 2, 8, dtype=torch.int32)), "unsupported extra_indices shape"),
+    (dict(extra_topk_lengths=None), "missing extra_topk_lengths for native CSAHCA DSV4 decode"),
+    (dict(extra_k_cache=torch.zeros(5, 16, 585, dtype=torch.uint8)), "unsupported extra_k_cache shape"),
+    # the first unusable argument in route order names the error
+    (dict(q=torch.zeros(8, 512), extra_k_cache=None), "unsupported q shape"),
+])
+def test_strict_mode_extra_arguments(captured, monkeypatch, change, msg):
+    md = metadata(ratio=128)
+    md.update(change)
+    assert sglang_dsv4.maybe_dsv4_decode_forward(**md) is None
+    monkeypatch.setenv("CSAHCA_DSV4_NATIVE_STRICT", "yes")
+    with pytest.raises(RuntimeError, match=msg):
+        sglang_dsv4.maybe_dsv4_decode_forward(**md)
+    assert captured == []
+
+
+def test_routes_cover_the_reference_ratios_only():
+    assert sorted(sglang_dsv4.ROUTES) == [0, 4, 128]
+    assert [s.name for s in sglang_dsv4.ROUTES[0].args] == ["q", "swa_k_cache", "swa_page_indices",
+                                                           "swa_topk_lengths"]
+    assert [s.name for s in sglang_dsv4.ROUTES[4].args][4:] == ["extra_k_cache", "extra_indices",
+                                                               "extra_topk_lengths"]
+
+
+def test_conform_folds_only_unit_axes():
+    spec = sglang_dsv4.paged_cache("c")
+    x = torch.arange(2 * 3 * 4, dtype=torch.uint8).view(2, 3, 1, 4)
+    assert torch.equal(sglang_dsv4.conform(spec, x), x.view(2, 12))
+    with pytest.raises(sglang_dsv4.Decline, match=r"unsupported c shape .*\(2, 3, 2, 2\)"):
+        sglang_dsv4.conform(spec, x.view(2, 3, 2, 2))
+    with pytest.raises(sglang_dsv4.Decline, match="unsupported n shape"):
+        sglang_dsv4.conform(sglang_dsv4.lengths("n"), torch.zeros(3, 1))
+
+
+def test_metadata_missing_extra_fields():
+    q = torch.zeros(2, 8, 512)
+    core = types.SimpleNamespace(c128_page_indices=torch.ones(2, 4, dtype=torch.int32))
+    with pytest.raises(RuntimeError, match="missing DSV4 extra indices/topk lengths for compress_ratio=128"):
+        sglang_dsv4.prepare_extra_indices(core=core, q=q, compress_ratio=128)
+    core = types.SimpleNamespace(swa_page_indices=torch.ones(2, 1, 1, 16, dtype=torch.int32),
+                                 swa_topk_lengths=torch.ones(2))
+    with pytest.raises(RuntimeError, match="unsupported DSV4 SWA index rank 4"):
+        sglang_dsv4.prepare_swa_indices(core=core, q=q)
