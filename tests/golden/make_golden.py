@@ -4,8 +4,8 @@ Run once, in the build container where the reference checkout exists:
 
     python tests/golden/make_golden.py --reference /root/reference
 
-It imports ``hybrid_attention.reference`` and ``hybrid_attention.dsv4_correctness``
-from the reference checkout (CPU only; the CUDA extension is never loaded) and
+It imports ``hybrid_attention.reference``, ``hybrid_attention.dsv4_correctness``
+and ``hybrid_attention.model_inference`` from the reference checkout (CPU only; the CUDA extension is never loaded) and
 saves small ``.npz`` fixtures next to this script.  The fixtures are data only:
 inputs, the reference's outputs, and SHA-256 digests of inputs regenerated from
 a seed.  Nothing under tests/ imports the reference at test time.
@@ -25,6 +25,14 @@ What each fixture pins (functions no closed form fixes bit for bit):
                      for the three compress ratios (nq 3, H 8, page 64).
   dsv4_pack_edges.npz  pack bytes at power-of-two scale boundaries, tiny tiles,
                      values needing the +-448 clamp and a rope passthrough.
+  block_mini.npz     MiniCSADecodeBlock.forward (hybrid_attention/model_inference.py:14-76)
+                     with the torch-csa backend and the block's own top-k
+                     selection, MLP ratio 0.0 and 2.0, B2 H2 D64 S512, chunk 64,
+                     k 4: its weights, inputs, selected chunks and output
+                     (odd hidden features zero, so the output there is the
+                     block's update alone).
+
+``--only NAME`` (repeatable: csa, hashes, dsv4, block) rewrites just those fixtures.
 """
 from __future__ import annotations
 
@@ -171,18 +179,53 @@ def dsv4_fixtures(DC) -> None:
                         bpp={ps: DC.bytes_per_page(ps) for ps in (1, 2, 4, 16, 64, 256)}.__repr__())
 
 
+def block_fixtures(MI, R) -> None:
+    bf = torch.bfloat16
+    g = torch.Generator().manual_seed(8)
+    hidden = torch.randn(2, 128, generator=g).to(bf)
+    # Odd features are zero: there the output is 0.01 * (attention + MLP) alone,
+    # so the block's composition shows above the residual's bf16 rounding.
+    hidden[:, 1::2] = 0
+    k = torch.randn(2, 2, 512, 64, generator=g).to(bf)
+    v = torch.randn(2, 2, 512, 64, generator=g).to(bf)
+    fx = dict(hidden=bits16(hidden), k=bits16(k), v=bits16(v), heads=2, head_dim=64, chunk_size=64, top_k=4)
+    for ratio in (0.0, 2.0):
+        tag = f"mlp{int(ratio)}"
+        torch.manual_seed(7)  # default nn.Linear init, as the reference benchmark seeds it
+        blk = MI.MiniCSADecodeBlock(heads=2, head_dim=64, dtype=bf, device=torch.device("cpu"), mlp_ratio=ratio)
+        with torch.no_grad():
+            out = blk(hidden, k, v, None, backend="torch-csa", chunk_size=64, top_k=4, tile_size=8)
+            sel = R.select_topk_chunks(blk.q_proj(hidden).view(2, 2, 64), k, 64, 4)
+        fx[f"{tag}_w_q"] = bits16(blk.q_proj.weight)
+        fx[f"{tag}_w_out"] = bits16(blk.out_proj.weight)
+        if blk.use_mlp:
+            fx[f"{tag}_w_up"] = bits16(blk.up_proj.weight)
+            fx[f"{tag}_w_down"] = bits16(blk.down_proj.weight)
+        fx[f"{tag}_selected"] = sel.numpy()
+        fx[f"{tag}_out"] = bits16(out)
+    np.savez_compressed(HERE / "block_mini.npz", **fx)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--reference", default="/root/reference")
+    ap.add_argument("--only", action="append", choices=["csa", "hashes", "dsv4", "block"])
     args = ap.parse_args()
     sys.path.insert(0, args.reference)
     from hybrid_attention import dsv4_correctness as DC  # noqa: E402
+    from hybrid_attention import model_inference as MI  # noqa: E402
     from hybrid_attention import reference as R  # noqa: E402
 
     torch.set_num_threads(4)
-    csa_fixtures(R)
-    synthetic_hashes(R, DC)
-    dsv4_fixtures(DC)
+    todo = set(args.only or ["csa", "hashes", "dsv4", "block"])
+    if "csa" in todo:
+        csa_fixtures(R)
+    if "hashes" in todo:
+        synthetic_hashes(R, DC)
+    if "dsv4" in todo:
+        dsv4_fixtures(DC)
+    if "block" in todo:
+        block_fixtures(MI, R)
     for p in sorted(HERE.glob("*.npz")) + [HERE / "synthetic_hash.json"]:
         print(p.name, p.stat().st_size)
 

@@ -1,11 +1,15 @@
 """GPU parity of the decode blocks (csahca_amd/block.py).
 
-MiniCSADecodeBlock restates hybrid_attention/model_inference.py:14-76; its
-reference here is the same block on the CPU in torch with identical weights and
-the oracle's CSA (cuda-csa semantics: fp32 probabilities).  HybridDecodeBlock
-(the hybrid block over a growing cache) is checked step by step against a CPU restatement that
-rounds exactly where the GPU block stores bf16 (q, the appended K/V, every
-linear output).  Tolerance: |got - ref| <= 2e-2 + 1e-2 |ref| on block outputs.
+MiniCSADecodeBlock restates hybrid_attention/model_inference.py:14-76.  It is
+checked against the reference block's own outputs (tests/golden/block_mini.npz,
+torch-csa backend) and against oracle.block.mini_block, the CPU restatement
+that fixture pins bit for bit, with cuda-csa math (fp32 probabilities).
+HybridDecodeBlock (the BASELINE config-2 block over a growing cache) is checked
+step by step against oracle.block.baseline_block_steps, pinned by closed forms,
+which rounds exactly where the GPU block stores bf16 (q, the appended K/V, every
+linear output) -- also at the stated shape: hidden 1024 (H8 D128), a 32768-token
+cache, std-0.02 weights, MLP ratio 2.0 and 0.0, across a chunk boundary.
+Tolerance: |got - ref| <= 2e-2 + 1e-2 |ref| on block outputs.
 """
 import numpy as np
 import pytest
@@ -14,6 +18,7 @@ import torch.nn.functional as F
 
 import oracle
 from csahca_amd import native
+from oracle import block as OB
 from csahca_amd.block import HybridDecodeBlock, MiniCSADecodeBlock, rms_norm
 
 pytestmark = pytest.mark.gpu
@@ -55,14 +60,9 @@ def make_static(B=1, H=8, S=4096, D=128, seed=0):
 def test_mini_block_matches_cpu_restatement(mlp_ratio, fused):
     hidden, k, v = make_static()
     blk = MiniCSADecodeBlock(heads=8, head_dim=128, dtype=BF, device=DEV, mlp_ratio=mlp_ratio, seed=1, fused=fused)
-    # CPU restatement with the same weights
-    q = F.linear(hidden, blk.w_q.cpu()).view(1, 8, 128)
-    sel = oracle.select_topk_chunks(q, k, 64, 8)
-    attn = cpu_csa(q, k, v, sel, 64)
-    out = F.linear(attn.reshape(1, 1024), blk.w_out.cpu())
-    if mlp_ratio:
-        out = out + F.linear(F.gelu(F.linear(hidden, blk.w_up.cpu())), blk.w_down.cpu())
-    want = hidden + 0.01 * out
+    mlp = dict(w_up=blk.w_up.cpu(), w_down=blk.w_down.cpu()) if mlp_ratio else {}
+    want, sel = OB.mini_block(hidden, blk.w_q.cpu(), blk.w_out.cpu(), k, v, chunk=64, top_k=8, prob_dtype=oracle.F32,
+                              **mlp)
     sel_t = torch.from_numpy(sel).to(torch.int32).to(DEV)
     got = blk(hidden.to(DEV), k.to(DEV), v.to(DEV), selection="precomputed", selected_chunks=sel_t)
     assert_close(got, want, what="precomputed")
@@ -102,29 +102,12 @@ def test_mini_block_graph_replays_match_eager(fused):
 
 
 def cpu_hybrid_reference(blk: HybridDecodeBlock, k0, v0, hiddens):
-    """The HybridDecodeBlock step on the CPU: bf16 storage where the GPU block
-    stores bf16, oracle selection over complete chunks, cuda-csa attention."""
+    """oracle.block.baseline_block_steps with the block's own weights."""
     w = {n: getattr(blk, n).cpu() for n in ("w_qkv", "w_out", "norm1", "norm2")}
     if blk.use_mlp:
         w["w_up"], w["w_down"] = blk.w_up.cpu(), blk.w_down.cpu()
-    B, H, D, chunk = blk.batch, blk.heads, blk.head_dim, blk.chunk_size
-    k, v = k0.clone(), v0.clone()
-    outs = []
-    for hidden in hiddens:
-        x = rms_norm(hidden, w["norm1"])
-        qkv = F.linear(x, w["w_qkv"]).view(B, 3, H, D)
-        q = qkv[:, 0].contiguous()
-        k = torch.cat([k, qkv[:, 1].unsqueeze(2)], dim=2)
-        v = torch.cat([v, qkv[:, 2].unsqueeze(2)], dim=2)
-        C = k.shape[2] // chunk
-        summ = oracle.chunk_mean(k[:, :, : C * chunk].contiguous(), chunk)
-        idx, _ = oracle.select_topk(q, summ, blk.top_k)
-        attn = cpu_csa(q, k, v, idx, chunk)
-        h = hidden + F.linear(attn.reshape(B, H * D), w["w_out"])
-        if blk.use_mlp:
-            h = h + F.linear(F.silu(F.linear(rms_norm(h, w["norm2"]), w["w_up"])), w["w_down"])
-        outs.append(h)
-    return outs
+    return OB.baseline_block_steps(w, k0, v0, hiddens, heads=blk.heads, head_dim=blk.head_dim,
+                                   chunk=blk.chunk_size, top_k=blk.top_k, prob_dtype=oracle.F32)
 
 
 @pytest.mark.parametrize("fused", [True, False])
@@ -148,6 +131,67 @@ def test_hybrid_block_steps_match_cpu_across_a_chunk_boundary(mlp_ratio, fused):
     # the summary of the chunk completed during decoding equals a fresh build
     fresh = native.csa_chunk_summary(blk.k_cache[:, :, :256].contiguous(), 64)
     torch.testing.assert_close(blk.summary, fresh, rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("fused", [True, False])
+@pytest.mark.parametrize("mlp_ratio", [0.0, 2.0])
+def test_mini_block_matches_the_reference_blocks_outputs(mlp_ratio, fused, golden_dir):
+    """The reference block's own output (torch-csa backend) and selection.
+    Odd hidden features are zero in the fixture, so there the output is the
+    block's update alone; its tolerance scales with that update's magnitude."""
+    z = np.load(golden_dir / "block_mini.npz")
+    tag = f"mlp{int(mlp_ratio)}"
+    bf = lambda name: torch.from_numpy(z[name].view(np.int16)).view(BF).to(DEV)  # noqa: E731
+    hidden, k, v = bf("hidden"), bf("k"), bf("v")
+    blk = MiniCSADecodeBlock(heads=2, head_dim=64, dtype=BF, device=DEV, mlp_ratio=mlp_ratio, fused=fused)
+    blk.w_q, blk.w_out = bf(f"{tag}_w_q"), bf(f"{tag}_w_out")
+    if mlp_ratio:
+        blk.w_up, blk.w_down = bf(f"{tag}_w_up"), bf(f"{tag}_w_down")
+    ref = torch.from_numpy(z[f"{tag}_out"].view(np.int16)).view(BF).float()
+    sel = torch.from_numpy(z[f"{tag}_selected"]).to(DEV)
+    summ = native.csa_chunk_summary(k, 64)
+    _, idx = native.csa_decode_step(native.block_linear(hidden, blk.w_q).view(2, 2, 64) if fused else
+                                    F.linear(hidden, blk.w_q).view(2, 2, 64), k, v, summ, 64, 4)
+    assert torch.equal(idx, sel)
+    for got in (blk(hidden, k, v, selection="dynamic", summary=summ, chunk_size=64, top_k=4),
+                blk(hidden, k, v, selection="precomputed", selected_chunks=sel, chunk_size=64)):
+        got = got.float().cpu()
+        assert_close(got[:, 0::2], ref[:, 0::2], what="input features")
+        scale = ref[:, 1::2].abs().max().item()
+        assert_close(got[:, 1::2], ref[:, 1::2], atol=2e-2 * scale, what="update-only features")
+
+
+@pytest.mark.parametrize("mlp_ratio", [0.0, 2.0])
+def test_hybrid_block_at_the_stated_shape_across_a_chunk_boundary(mlp_ratio):
+    """BASELINE config 2's block as stated: hidden 1024 (H8 D128), std-0.02
+    weights, a 32768-token cache, chunk 64, top 8.  The cache holds 32765
+    tokens; the third step's token completes chunk 511.  Every step is checked
+    against the CPU restatement; a graph of one step, replayed from the same
+    state, equals the eager steps bit for bit."""
+    B, H, D, S0, steps = 1, 8, 128, 32765, 6
+    mk = lambda: HybridDecodeBlock(batch=B, heads=H, head_dim=D, capacity=S0 + steps + 64, chunk_size=64,  # noqa: E731
+                                   top_k=8, mlp_ratio=mlp_ratio, device=DEV, seed=41)
+    eager, graphed = mk(), mk()
+    assert eager.fused and torch.equal(eager.w_qkv, graphed.w_qkv)
+    assert abs(eager.w_qkv.float().std().item() - 0.02) < 1e-3
+    g = torch.Generator().manual_seed(42)
+    k0 = torch.randn(B, H, S0, D, generator=g).to(BF)
+    v0 = torch.randn(B, H, S0, D, generator=g).to(BF)
+    hiddens = [torch.randn(B, H * D, generator=g).to(BF) for _ in range(steps)]
+    for blk in (eager, graphed):
+        blk.prefill(k0.to(DEV), v0.to(DEV))
+    want = cpu_hybrid_reference(eager, k0, v0, hiddens)
+    hbuf = hiddens[0].to(DEV)
+    replay, gout = graphed.capture(hbuf)
+    for i, hdn in enumerate(hiddens):
+        got = eager(hdn.to(DEV))
+        assert_close(got, want[i], what=f"step {i}")
+        hbuf.copy_(hdn.to(DEV))
+        assert torch.equal(replay(), got), f"graph step {i}"
+    assert int(eager.nchunks.item()) == 512 == int(graphed.nchunks.item())
+    fresh = native.csa_chunk_summary(eager.k_cache[:, :, :32768].contiguous(), 64)
+    torch.testing.assert_close(eager.summary[:, :, 511], fresh[:, :, 511], rtol=0, atol=0)
+    assert all(x == 0 for x in native.csa_step_status().values())
 
 
 def test_fused_hybrid_block_batch_two_matches_cpu():

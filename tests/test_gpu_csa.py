@@ -409,6 +409,42 @@ def test_workgroups_per_head_override_is_bounded_by_residency(monkeypatch):
     assert all(v == 0 for v in native.csa_step_status().values())
 
 
+GRID_REST = [  # BASELINE config 1 grid points beyond B = 1 (B32 S131072 has its own test below)
+    (8, 32768, 8), (8, 32768, 32), (8, 131072, 8), (8, 131072, 32),
+    (32, 8192, 8), (32, 8192, 32), (32, 32768, 8), (32, 32768, 32),
+]
+
+
+@pytest.mark.parametrize("B,S,k", GRID_REST)
+def test_sweep_grid_point_matches_oracle(B, S, k):
+    """The fused decode step at a config-1 grid point (H8 D128 chunk 64, bf16
+    N(0,1) drawn on the device) against the oracle: chunk summaries on the
+    first and last head, selection from the device summaries (ids bit-exact up
+    to 1e-5 score ties), and attention over the selected chunks' tokens, which
+    are gathered on the device so the oracle works on [B, H, k*64, D] copies."""
+    H, D, chunk = 8, 128, 64
+    g = torch.Generator(device=DEV).manual_seed(B * 31 + S // 1024 + k)
+    q = torch.randn(B, H, D, device=DEV, generator=g).to(torch.bfloat16)
+    kc = torch.randn(B, H, S, D, device=DEV, generator=g, dtype=torch.bfloat16)
+    vc = torch.randn(B, H, S, D, device=DEV, generator=g, dtype=torch.bfloat16)
+    summ = extension.csa_chunk_summary(kc, chunk)
+    out, idx = native.csa_decode_step(q, kc, vc, summ, chunk, k)
+    for b, h in ((0, 0), (B - 1, H - 1)):
+        np.testing.assert_allclose(summ[b:b + 1, h:h + 1].cpu().numpy(),
+                                   oracle.chunk_mean(kc[b:b + 1, h:h + 1].cpu(), chunk), rtol=1e-6, atol=2e-6)
+    want, scores = oracle.select_topk(q.cpu(), summ.cpu(), k)
+    assert_indices(idx, want, scores)
+    tok = (idx.long().unsqueeze(-1) * chunk + torch.arange(chunk, device=DEV)).reshape(B, H, k * chunk, 1)
+    kg = torch.gather(kc, 2, tok.expand(-1, -1, -1, D)).cpu()
+    vg = torch.gather(vc, 2, tok.expand(-1, -1, -1, D)).cpu()
+    local = torch.arange(k, dtype=torch.int32).expand(B, H, k).contiguous()
+    ref = oracle.csa_attend(q.cpu(), kg, vg, local, chunk, prob_dtype=oracle.F32)
+    assert_close(out, ref, 2e-2, 1e-2, f"B{B} S{S} k{k}")
+    assert all(v == 0 for v in native.csa_step_status().values())
+    del q, kc, vc, summ, out
+    torch.cuda.empty_cache()
+
+
 def test_largest_sweep_point_properties():
     """B32 H8 S131072 D128 top-32 (17 GiB of K/V) is too large for the CPU
     oracle, so parity rests on size-independent properties: planted chunks are
