@@ -161,8 +161,11 @@ def roofline(nbytes, flops, ms, extra=None):
         r = {"bound": "hbm", "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s"}
     else:
         r = {"bound": "mfma", "achieved": round(tflops, 3), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s"}
+    # hbm_frac / mfma_frac: each side on its own (mfma_frac is the algorithmic
+    # flops' share of the dense bf16 MFMA peak over the measured time).
     r.update({"frac": round(max(t_hbm, t_mfma) / t, 4), "bytes": int(nbytes), "flops": int(flops),
-              "hbm_gbps": round(gbps, 1), "tflops": round(tflops, 3)})
+              "hbm_gbps": round(gbps, 1), "tflops": round(tflops, 3), "hbm_frac": round(t_hbm / t, 4),
+              "mfma_frac": round(t_mfma / t, 5)})
     if extra:
         r.update(extra)
     return r
