@@ -181,7 +181,18 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
     const int grp = lane / SLPR, col = lane % SLPR;
     const float* __restrict__ sb = a.summary + h * Cs * D + col * 4;
     uint64_t* kg = a.keys + h * a.key_stride;
-    const int64_t c0 = Cs * p / P, c1 = Cs * (p + 1) / P;
+    // This workgroup's rows: 32-bit division whenever Cs * P fits (every
+    // practical shape); a 64-bit division is a long scalar sequence on the
+    // critical path of the step.
+    int64_t c0, c1;
+    if (Cs * P <= static_cast<int64_t>(UINT32_MAX)) {
+      const uint32_t cs = static_cast<uint32_t>(Cs), up = static_cast<uint32_t>(P);
+      c0 = cs * static_cast<uint32_t>(p) / up;
+      c1 = cs * static_cast<uint32_t>(p + 1) / up;
+    } else {
+      c0 = Cs * p / P;
+      c1 = Cs * (p + 1) / P;
+    }
     constexpr int US = kStepScoreUnroll;
     for (int64_t blk = c0; blk < c1; blk += kStepWaves * SRPL * US) {
       const int64_t base = blk + wave * SRPL * US;
@@ -311,8 +322,15 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
 
   // ---- C: attention over this workgroup's slots ---------------------------
   const int nslots = a.topk * a.chunk;
-  const int s0 = static_cast<int>(static_cast<int64_t>(nslots) * p / P);
-  const int s1 = static_cast<int>(static_cast<int64_t>(nslots) * (p + 1) / P);
+  int s0, s1;  // 32-bit division whenever nslots * P fits (as for the rows of phase A)
+  if (static_cast<int64_t>(nslots) * P <= static_cast<int64_t>(UINT32_MAX)) {
+    const uint32_t ns = static_cast<uint32_t>(nslots), up = static_cast<uint32_t>(P);
+    s0 = static_cast<int>(ns * static_cast<uint32_t>(p) / up);
+    s1 = static_cast<int>(ns * static_cast<uint32_t>(p + 1) / up);
+  } else {
+    s0 = static_cast<int>(static_cast<int64_t>(nslots) * p / P);
+    s1 = static_cast<int>(static_cast<int64_t>(nslots) * (p + 1) / P);
+  }
   const int grp = lane / LPR, col = lane % LPR;
   const T* qp = q + col * VEC;  // loaded inside attend_block, after the K/V rows
   const T* __restrict__ kb = static_cast<const T*>(a.kcache) + h * a.S * D + col * VEC;
