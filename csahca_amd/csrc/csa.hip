@@ -37,9 +37,11 @@ __global__ __launch_bounds__(64) void csa_attend_vec_kernel(
   const int lane = threadIdx.x;
   const int grp = lane / LPR;
   const int col = lane % LPR;
-  const int64_t item = blockIdx.x;
-  const int t = static_cast<int>(item % num_tiles);
-  const int64_t bh = item / num_tiles;
+  // 32-bit index arithmetic (the grid is < 2^32 blocks): a 64-bit division is
+  // a long scalar sequence at the head of every workgroup.
+  const uint32_t item = blockIdx.x;
+  const int t = static_cast<int>(item % static_cast<uint32_t>(num_tiles));
+  const int64_t bh = item / static_cast<uint32_t>(num_tiles);
 
   const T* qp = q + bh * D + col * VEC;
   const T* __restrict__ kb = k + bh * seq_len * D + col * VEC;
@@ -86,9 +88,11 @@ __global__ __launch_bounds__(64) void csa_attend_generic_kernel(
     int64_t seq_len, int D, int top_k, int chunk, int chunk_shift, int tile, int num_tiles,
     float qscale) {
   const int lane = threadIdx.x;
-  const int64_t item = blockIdx.x;
-  const int t = static_cast<int>(item % num_tiles);
-  const int64_t bh = item / num_tiles;
+  // 32-bit index arithmetic (the grid is < 2^32 blocks): a 64-bit division is
+  // a long scalar sequence at the head of every workgroup.
+  const uint32_t item = blockIdx.x;
+  const int t = static_cast<int>(item % static_cast<uint32_t>(num_tiles));
+  const int64_t bh = item / static_cast<uint32_t>(num_tiles);
   float qf[J], acc[J];
   T qr[J];
 #pragma unroll

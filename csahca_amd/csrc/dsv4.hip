@@ -222,11 +222,12 @@ static_assert(kSlotBatch * kHeadGroup == 32, "one reduce-scatter of 32 sums per 
 template <typename T, bool kVec>
 __global__ __launch_bounds__(64) void dsv4_tile_kernel(const T* __restrict__ q, Dsv4Args a) {
   const int lane = threadIdx.x;
-  const int64_t item = blockIdx.x;
-  const int t = static_cast<int>(item % a.num_tiles);
-  const int64_t rest = item / a.num_tiles;
-  const int hg = static_cast<int>(rest % a.head_groups);
-  const int64_t query = rest / a.head_groups;
+  // 32-bit index arithmetic (the grid is < 2^32 blocks).
+  const uint32_t item = blockIdx.x;
+  const int t = static_cast<int>(item % static_cast<uint32_t>(a.num_tiles));
+  const uint32_t rest = item / static_cast<uint32_t>(a.num_tiles);
+  const int hg = static_cast<int>(rest % static_cast<uint32_t>(a.head_groups));
+  const int64_t query = rest / static_cast<uint32_t>(a.head_groups);
   const int h0 = hg * kHeadGroup;
   const int nh = min(kHeadGroup, a.heads - h0);
 
@@ -520,11 +521,13 @@ __global__ __launch_bounds__(kMfmaThreads) void dsv4_mfma_kernel(const bf16* __r
   const int lane = tid % kWave;
   const int grp = lane / 16;  // lane group (MFMA k / row block)
   const int l16 = lane % 16;
-  const int64_t item = blockIdx.x;
-  const int split = static_cast<int>(item % m.splits);
-  const int64_t rest = item / m.splits;
-  const int hg = static_cast<int>(rest % m.mfma_groups);
-  const int64_t query = rest / m.mfma_groups;
+  // 32-bit index arithmetic (the grid is < 2^32 blocks): 64-bit divisions are
+  // long scalar sequences on the critical path.
+  const uint32_t item = blockIdx.x;
+  const int split = static_cast<int>(item % static_cast<uint32_t>(m.splits));
+  const uint32_t rest = item / static_cast<uint32_t>(m.splits);
+  const int hg = static_cast<int>(rest % static_cast<uint32_t>(m.mfma_groups));
+  const int64_t query = rest / static_cast<uint32_t>(m.mfma_groups);
   const int h0 = hg * kMfmaHeads;
   const int nh = min(kMfmaHeads, a.heads - h0);
 
@@ -1125,7 +1128,7 @@ __global__ __launch_bounds__(kMergeThreads) void dsv4_merge_kernel(const float* 
   __shared__ float s_w[kMergeChunk];
   __shared__ float s_mx, s_inv;
   const int64_t qh = blockIdx.x;
-  const int head = static_cast<int>(qh % heads);
+  const int head = static_cast<int>(blockIdx.x % static_cast<uint32_t>(heads));  // 32-bit (grid < 2^32)
   const int tid = threadIdx.x;
   const float2* ml = reinterpret_cast<const float2*>(part_ml) + qh * num_tiles;
   if (num_tiles <= kMergeFastTiles) {

@@ -44,8 +44,17 @@ __device__ __forceinline__ void hca_chunk_body(const T* __restrict__ q, const T*
   extern __shared__ float lds[];
   __shared__ float red[kHcaThreads / kWave];
   const int tid = threadIdx.x;
-  const int64_t bh = item / C;
-  const int64_t c = item - bh * C;
+  // 32-bit division whenever the item index fits (every practical shape).
+  int64_t bh, c;
+  if (item <= static_cast<int64_t>(UINT32_MAX) && C <= static_cast<int64_t>(UINT32_MAX)) {
+    const uint32_t it = static_cast<uint32_t>(item), cc = static_cast<uint32_t>(C);
+    const uint32_t b32 = it / cc;
+    bh = b32;
+    c = it - b32 * cc;
+  } else {
+    bh = item / C;
+    c = item - bh * C;
+  }
   const int nvc = D / VEC;
   const int tpr = min(nvc, kHcaThreads);
   const int R = kHcaThreads / tpr;
