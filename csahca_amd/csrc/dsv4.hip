@@ -51,12 +51,24 @@ struct CacheView {
   int64_t num_pages;
   int64_t bpp;
   int page_size;
+  int page_shift;  // log2(page_size) when it is a power of two, else -1
 };
+
+CacheView cache_view(const void* base, int64_t num_pages, int64_t bpp, int64_t page_size) {
+  int shift = -1;
+  if (page_size > 0 && (page_size & (page_size - 1)) == 0) {
+    shift = 0;
+    while ((int64_t{1} << shift) < page_size) ++shift;
+  }
+  return CacheView{static_cast<const uint8_t*>(base), num_pages, bpp, static_cast<int>(page_size), shift};
+}
 
 __device__ __forceinline__ const uint8_t* row_ptr(const CacheView& c, int32_t loc,
                                                   const uint8_t** scale_row) {
   if (loc < 0) return nullptr;
-  const int64_t page = loc / c.page_size;
+  // A shift for power-of-two pages: an integer division would sit between the
+  // slot index load and the row load it addresses.
+  const int64_t page = c.page_shift >= 0 ? (loc >> c.page_shift) : loc / c.page_size;
   if (page >= c.num_pages) return nullptr;
   const int64_t in_page = loc - page * c.page_size;
   const uint8_t* pg = c.base + page * c.bpp;
@@ -1456,7 +1468,7 @@ extern "C" int csahca_dsv4_decode_forward_tiled(
                    "extra_bytes_per_page is too small for DSV4 page layout");
     CSAHCA_REQUIRE(extra_bytes_per_page % 4 == 0,
                    "tiled DSV4 kernel requires extra_bytes_per_page divisible by 4 for vectorized loads");
-    c.extra = CacheView{extra_cache, extra_num_pages, extra_bytes_per_page, static_cast<int>(extra_page_size)};
+    c.extra = cache_view(extra_cache, extra_num_pages, extra_bytes_per_page, extra_page_size);
     c.eidx = extra_token_indices;
     c.extra_slots = extra_topk_slots;
     c.elens = extra_topk_lengths;
@@ -1465,7 +1477,7 @@ extern "C" int csahca_dsv4_decode_forward_tiled(
   c.dtype = dtype;
   c.nq = num_queries;
   c.heads = heads;
-  c.swa = CacheView{cache, num_pages, bytes_per_page, static_cast<int>(page_size)};
+  c.swa = cache_view(cache, num_pages, bytes_per_page, page_size);
   c.idx = token_indices;
   c.topk_slots = topk_slots;
   c.lens = topk_lengths;
@@ -1495,7 +1507,7 @@ extern "C" int csahca_dsv4_swa_decode_forward(const void* q, int dtype, int64_t 
   c.dtype = dtype;
   c.nq = num_queries;
   c.heads = heads;
-  c.swa = CacheView{cache, num_pages, bytes_per_page, static_cast<int>(page_size)};
+  c.swa = cache_view(cache, num_pages, bytes_per_page, page_size);
   c.idx = token_indices;
   c.topk_slots = topk_slots;
   c.lens = topk_lengths;
@@ -1529,7 +1541,7 @@ extern "C" int csahca_dsv4_sparse_decode_forward(
   const bool has_extra = extra_cache != nullptr && extra_token_indices != nullptr &&
                          extra_topk_slots > 0;
   if (has_extra) {
-    c.extra = CacheView{extra_cache, extra_num_pages, extra_bytes_per_page, static_cast<int>(extra_page_size)};
+    c.extra = cache_view(extra_cache, extra_num_pages, extra_bytes_per_page, extra_page_size);
     c.eidx = extra_token_indices;
     c.extra_slots = extra_topk_slots;
     c.elens = extra_topk_lengths;
@@ -1538,7 +1550,7 @@ extern "C" int csahca_dsv4_sparse_decode_forward(
   c.dtype = dtype;
   c.nq = num_queries;
   c.heads = heads;
-  c.swa = CacheView{cache, num_pages, bytes_per_page, static_cast<int>(page_size)};
+  c.swa = cache_view(cache, num_pages, bytes_per_page, page_size);
   c.idx = token_indices;
   c.topk_slots = topk_slots;
   c.lens = topk_lengths;
