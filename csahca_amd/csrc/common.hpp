@@ -263,6 +263,38 @@ __device__ __forceinline__ float xor_lanes(float v, int off) {
   }
 }
 
+// Sums each of the N values v[0..N) over the L lanes of the lane's aligned
+// group of L (N <= L, both powers of two), transposed: every exchange carries
+// values another lane needs, so log2(N) halving steps leave each lane with one
+// value, then plain steps finish it.  Lane l ends with the sum of value
+// (l % L) / (L / N).  Every sum is formed by the same pairwise tree (own +
+// partner at distances L/2, L/4, ..., 1) as a butterfly over each value, so
+// the bits are those of the butterfly; it takes N - 1 + log2(L / N)
+// exchanges instead of N log2(L).
+template <int N, int L>
+__device__ __forceinline__ float transposed_group_sum(float (&v)[N]) {
+  static_assert(N >= 1 && N <= L && L <= kWave && (N & (N - 1)) == 0 && (L & (L - 1)) == 0,
+                "transposed_group_sum: N <= L, powers of two");
+  const int lane = static_cast<int>(__lane_id());
+#pragma unroll
+  for (int half = N / 2, d = L / 2; half >= 1; half /= 2, d /= 2) {
+    // Bit-mask selects (v_bfi): a ternary over two array elements is turned by
+    // the compiler into a dynamically indexed read of the whole array.
+    const uint32_t up = (lane & d) ? 0xffffffffu : 0u;
+#pragma unroll
+    for (int i = 0; i < half; ++i) {
+      const uint32_t lo = __float_as_uint(v[i]), hi = __float_as_uint(v[i + half]);
+      const float send = __uint_as_float((lo & up) | (hi & ~up));
+      const float keep = __uint_as_float((hi & up) | (lo & ~up));
+      v[i] = keep + xor_lanes(send, d);
+    }
+  }
+  float s = v[0];
+#pragma unroll
+  for (int d = L / (2 * N); d >= 1; d /= 2) s += xor_lanes(s, d);
+  return s;
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v += xor_lanes(v, off);

@@ -262,22 +262,20 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
         for (int e = 0; e < 4; ++e) d = fmaf(qf[e], r4[e], d);
         sc[u] = d;
       }
-#pragma unroll
-      for (int off = SLPR / 2; off >= 1; off >>= 1)
-#pragma unroll
-        for (int u = 0; u < US; ++u) sc[u] += xor_lanes(sc[u], off);
+      // Row sums over the SLPR lanes of each row, transposed: lane col ends
+      // with row u = col / (SLPR / US), and one lane per row publishes its key
+      // (a wavefront's 16 B-row keys are consecutive words: one store).
+      static_assert(US <= SLPR, "one summed row per lane group of SLPR / US lanes");
+      const float ssum = transposed_group_sum<US, SLPR>(sc);
       const uint32_t tag = launch_tag(ep);
-      if (col == 0) {
-#pragma unroll
-        for (int u = 0; u < US; ++u) {
-          const int64_t c = base + grp + SRPL * u;
-          if (c < c1 && c < C) {
-            const uint32_t key = order_key(sc[u] * a.score_scale);
-            if (P > 1)
-              put_tagged(kg + c, tag, key);
-            else
-              keys_l[c] = key;
-          }
+      if (col % (SLPR / US) == 0) {
+        const int64_t c = base + grp + SRPL * (col / (SLPR / US));
+        if (c < c1 && c < C) {
+          const uint32_t key = order_key(ssum * a.score_scale);
+          if (P > 1)
+            put_tagged(kg + c, tag, key);
+          else
+            keys_l[c] = key;
         }
       }
     }
