@@ -58,19 +58,13 @@ __global__ __launch_bounds__(64) void csa_attend_vec_kernel(
   st.init();
   for (int base = s0; base < s1; base += RPL * U)
     attend_block<T, D, U>(st, qp, qscale, kb, vb, base, s1, grp, tok_of);
-  fold_row_groups(st);
+  // Row groups folded transposed: every lane stores kKeep of its columns' sums.
+  const int fbase = fold_row_groups_share(st);
   const int64_t p = bh * num_tiles + t;
-  if (grp == 0) {
-    float* dst = part_acc + p * D + col * VEC;
-    if constexpr (VEC % 4 == 0) {
+  {
+    float* dst = part_acc + p * D + col * VEC + fbase;
 #pragma unroll
-      for (int e = 0; e < VEC; e += 4)
-        *reinterpret_cast<float4*>(dst + e) =
-            make_float4(st.acc[e], st.acc[e + 1], st.acc[e + 2], st.acc[e + 3]);
-    } else {
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) dst[e] = st.acc[e];
-    }
+    for (int e = 0; e < FoldShare<T, D>::kKeep; ++e) dst[e] = st.acc[e];
   }
   if (lane == 0) {
     part_ml[2 * p] = st.m;
@@ -454,16 +448,13 @@ __global__ __launch_bounds__(64) void csa_score_vec_kernel(const T* __restrict__
     for (int e = 0; e < 4; ++e) d = fmaf(qf[e], r4[e], d);
     sc[u] = d;
   }
-#pragma unroll
-  for (int off = LPR / 2; off >= 1; off >>= 1)
-#pragma unroll
-    for (int u = 0; u < U; ++u) sc[u] += xor_lanes(sc[u], off);
-  if (col == 0) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t c = c0 + grp + RPL * u;
-      if (c < C) keys[bh * C + c] = order_key(sc[u] * scale);
-    }
+  // Transposed row sums (the bits of a butterfly per row; one key store per
+  // row from the lane that holds it).
+  static_assert(U <= LPR && (U & (U - 1)) == 0, "one summed row per lane group of LPR / U lanes");
+  const float ssum = transposed_group_sum<U, LPR>(sc);
+  if (col % (LPR / U) == 0) {
+    const int64_t c = c0 + grp + RPL * (col / (LPR / U));
+    if (c < C) keys[bh * C + c] = order_key(ssum * scale);
   }
 }
 

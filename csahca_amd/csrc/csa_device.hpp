@@ -423,17 +423,52 @@ __device__ __forceinline__ void attend_block(WaveSoftmax<T, D>& st, const T* qp,
   st.m = m_new;
 }
 
-// Fold the RPL row groups of a wavefront's state (afterwards every lane of
-// group 0 holds the full l and its VEC columns of acc).
-template <typename T, int D>
-__device__ __forceinline__ void fold_row_groups(WaveSoftmax<T, D>& st) {
-  using L = AttendLayout<T, D>;
+// Transposed fold of the row groups (RPL groups of LPR lanes): each step at
+// distance OFF (LPR, 2 LPR, ..., 32: the pairing of a butterfly over the
+// groups, so every column sum has that butterfly's bits) halves the acc
+// values a lane holds while it holds more than one.  A lane ends with kFoldKeep column sums, of columns
+// col * VEC + base .. + kFoldKeep - 1; l is summed over the groups in every lane.
+template <int M, int OFF>
+__device__ __forceinline__ void fold_groups_t(float* v, int lane, int& base) {
+  if constexpr (OFF < kWave) {
+    if constexpr (M > 1) {
+      constexpr int H = M / 2;
+      // Bit-mask selects keep every array access at a constant index.
+      const uint32_t up = (lane & OFF) ? 0xffffffffu : 0u;
 #pragma unroll
-  for (int off = L::LPR; off < kWave; off <<= 1) {
-    st.l += xor_lanes(st.l, off);
-#pragma unroll
-    for (int e = 0; e < L::VEC; ++e) st.acc[e] += xor_lanes(st.acc[e], off);
+      for (int i = 0; i < H; ++i) {
+        const uint32_t lo = __float_as_uint(v[i]), hi = __float_as_uint(v[i + H]);
+        const float send = __uint_as_float((lo & up) | (hi & ~up));
+        const float keep = __uint_as_float((hi & up) | (lo & ~up));
+        v[i] = keep + xor_lanes(send, OFF);
+      }
+      base += (lane & OFF) ? H : 0;
+      fold_groups_t<H, OFF * 2>(v, lane, base);
+    } else {
+      v[0] += xor_lanes(v[0], OFF);
+      fold_groups_t<1, OFF * 2>(v, lane, base);
+    }
   }
+}
+
+template <typename T, int D>
+struct FoldShare {
+  static constexpr int VEC = AttendLayout<T, D>::VEC;
+  static constexpr int RPL = AttendLayout<T, D>::RPL;
+  static constexpr int kKeep = VEC / RPL > 0 ? VEC / RPL : 1;
+};
+
+// Returns the first column (within the lane's VEC) of its kKeep sums, which
+// are left in st.acc[0 .. kKeep).
+template <typename T, int D>
+__device__ __forceinline__ int fold_row_groups_share(WaveSoftmax<T, D>& st) {
+  using L = AttendLayout<T, D>;
+  const int lane = static_cast<int>(__lane_id());
+#pragma unroll
+  for (int off = L::LPR; off < kWave; off <<= 1) st.l += xor_lanes(st.l, off);
+  int base = 0;
+  fold_groups_t<L::VEC, L::LPR>(st.acc, lane, base);
+  return base;
 }
 
 }  // namespace csahca

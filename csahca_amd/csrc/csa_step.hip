@@ -341,7 +341,9 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
   st.init();
   for (int blk = s0; blk < s1; blk += kStepWaves * RPL * U)
     attend_block<T, D, U>(st, qp, a.qscale, kb, vb, blk + wave * RPL * U, s1, grp, tok_of);
-  fold_row_groups(st);
+  // Row groups folded transposed: every lane holds, and stores, kKeep of its
+  // columns' sums.
+  const int fbase = fold_row_groups_share(st);
   float* cw = comb + wave * (D + 2);
   // A wavefront in which any lane timed out on a key marks its state with a
   // NaN weight, which poisons the head's output below.
@@ -350,10 +352,8 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
     cw[0] = st.m;
     cw[1] = wave_bad ? __builtin_nanf("") : st.l;
   }
-  if (grp == 0) {
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) cw[2 + col * VEC + e] = st.acc[e];
-  }
+  for (int e = 0; e < FoldShare<T, D>::kKeep; ++e) cw[2 + col * VEC + fbase + e] = st.acc[e];
   __syncthreads();
   float M = -INFINITY;
   bool poisoned = false;
