@@ -743,6 +743,10 @@ int decode_step_impl(const void* q, const void* k_cache, const void* v_cache, co
         int64_t{kStepWaves} * kStepAttendUnroll * std::max<int64_t>(1, kWave / (head_dim / (16 / esz)));
     P = std::max(ceil_div(num_chunks, score_rows), ceil_div(k * chunk_size, attend_rows));
     P = std::min<int64_t>(P, std::max<int64_t>(1, (2 * static_cast<int64_t>(ncu)) / std::max<int64_t>(bh, 1)));
+    // With a head per CU already, splitting a head pays only when its selected
+    // rows are many: at 256 heads, P = 1 beats P = 2 by 8-11% with 512 rows
+    // (top-8 of 64) and loses by 6% with 2048 (top-32).
+    if (bh >= ncu && k * chunk_size <= 1024) P = 1;
   }
   P = std::min<int64_t>({P, rg.max_p, ceil_div(num_chunks, 8), ceil_div(k * chunk_size, 16)});
   P = std::max<int64_t>(1, P);
