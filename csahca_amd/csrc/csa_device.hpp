@@ -334,25 +334,28 @@ struct WaveSoftmax {
   }
 };
 
-// Process rows base + grp + RPL*u (u < U) of the slot range [.., s1): tok_of(s,
-// tok) maps a slot to a token (false = skip).  kb/vb point at this lane's
-// columns of row 0 of the (b,h) cache, qp at this lane's 16 bytes of q (scaled
-// here by qscale).  Every row load is unconditional (a skipped slot reads row
-// 0 and is zeroed after the load) and q is loaded after the rows -- the newest
-// load, so one wait covers the batch and no hoisted use of q can make the rows
-// wait -- so the 2U + 1 loads of a lane are one batch in flight.
+// K and V rows of one batch of a lane (rows base + grp + RPL*u, u < U):
+// issued by attend_issue, consumed by attend_consume.
+template <int U>
+struct AttendRows {
+  uint4 rk[U], rv[U];
+  bool ok[U];
+};
+
+// Token lookup and the row loads of rows base + grp + RPL*u (u < U) of the
+// slot range [.., s1): tok_of(s, tok) maps a slot to a token (false = skip).
+// kb/vb point at this lane's columns of row 0 of the (b,h) cache.  Every row
+// load is unconditional (a skipped slot reads row 0 and is zeroed when
+// consumed).
 template <typename T, int D, int U, typename TokOf>
-__device__ __forceinline__ void attend_block(WaveSoftmax<T, D>& st, const T* qp, float qscale,
-                                             const T* __restrict__ kb, const T* __restrict__ vb,
+__device__ __forceinline__ void attend_issue(AttendRows<U>& r, const T* __restrict__ kb, const T* __restrict__ vb,
                                              int base, int s1, int grp, TokOf tok_of) {
-  using L = AttendLayout<T, D>;
-  constexpr int VEC = L::VEC, LPR = L::LPR, RPL = L::RPL;
+  constexpr int RPL = AttendLayout<T, D>::RPL;
   // Tokens first (chunk ids may come from global memory), then every row:
   // the empty asm takes all token positions, so no row load is scheduled
   // before the last id is known -- an id wait after a row load would, with
   // in-order wait counts, also wait for that row.
   int64_t toks[U];
-  bool ok[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     // Slots past s1 look up slot s1 - 1 (valid whenever this block runs) and
@@ -360,8 +363,8 @@ __device__ __forceinline__ void attend_block(WaveSoftmax<T, D>& st, const T* qp,
     const int s = base + grp + RPL * u;
     int64_t tok = 0;
     const bool found = tok_of(s < s1 ? s : s1 - 1, tok);
-    ok[u] = s < s1 && found;
-    toks[u] = ok[u] ? tok : 0;
+    r.ok[u] = s < s1 && found;
+    toks[u] = r.ok[u] ? tok : 0;
   }
   if constexpr (U == 4) {
     asm volatile("" : "+v"(toks[0]), "+v"(toks[1]), "+v"(toks[2]), "+v"(toks[3]));
@@ -369,22 +372,32 @@ __device__ __forceinline__ void attend_block(WaveSoftmax<T, D>& st, const T* qp,
 #pragma unroll
     for (int u = 0; u < U; ++u) asm volatile("" : "+v"(toks[u]));
   }
-  uint4 rk[U], rv[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    rk[u] = load_global_u4(kb + toks[u] * D);
-    rv[u] = load_global_u4(vb + toks[u] * D);
+    r.rk[u] = load_global_u4(kb + toks[u] * D);
+    r.rv[u] = load_global_u4(vb + toks[u] * D);
   }
-  float qf[VEC];
-  widen16<T>(load_global_u4(qp), qf);
+}
+
+// Scale this lane's 16 bytes of q by qscale (fp32).
+template <typename T, int D>
+__device__ __forceinline__ void attend_q(const uint4& q16, float qscale, float* qf) {
+  widen16<T>(q16, qf);
 #pragma unroll
-  for (int e = 0; e < VEC; ++e) qf[e] *= qscale;
+  for (int e = 0; e < AttendLayout<T, D>::VEC; ++e) qf[e] *= qscale;
+}
+
+// Online-softmax update of st with one issued batch of rows.
+template <typename T, int D, int U>
+__device__ __forceinline__ void attend_consume(WaveSoftmax<T, D>& st, const AttendRows<U>& r, const float* qf) {
+  using L = AttendLayout<T, D>;
+  constexpr int VEC = L::VEC, LPR = L::LPR;
   float kr[U][VEC], vr[U][VEC];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const uint4 z = make_uint4(0u, 0u, 0u, 0u);
-    widen16<T>(ok[u] ? rk[u] : z, kr[u]);
-    widen16<T>(ok[u] ? rv[u] : z, vr[u]);
+    widen16<T>(r.ok[u] ? r.rk[u] : z, kr[u]);
+    widen16<T>(r.ok[u] ? r.rv[u] : z, vr[u]);
   }
   float sc[U];
 #pragma unroll
@@ -402,7 +415,7 @@ __device__ __forceinline__ void attend_block(WaveSoftmax<T, D>& st, const T* qp,
   float mx = -INFINITY;
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    sc[u] = ok[u] ? sc[u] : -INFINITY;
+    sc[u] = r.ok[u] ? sc[u] : -INFINITY;
     mx = fmaxf(mx, sc[u]);
   }
 #pragma unroll
@@ -421,6 +434,52 @@ __device__ __forceinline__ void attend_block(WaveSoftmax<T, D>& st, const T* qp,
     for (int e = 0; e < VEC; ++e) st.acc[e] = fmaf(p, vr[u][e], st.acc[e]);
   }
   st.m = m_new;
+}
+
+// One batch issued and consumed: q (scaled here by qscale, qp at this lane's
+// 16 bytes) is loaded after the rows -- the newest load, so one wait covers
+// the batch and no hoisted use of q can make the rows wait -- so the 2U + 1
+// loads of a lane are one batch in flight.
+template <typename T, int D, int U, typename TokOf>
+__device__ __forceinline__ void attend_block(WaveSoftmax<T, D>& st, const T* qp, float qscale,
+                                             const T* __restrict__ kb, const T* __restrict__ vb,
+                                             int base, int s1, int grp, TokOf tok_of) {
+  AttendRows<U> r;
+  attend_issue<T, D, U>(r, kb, vb, base, s1, grp, tok_of);
+  float qf[AttendLayout<T, D>::VEC];
+  attend_q<T, D>(load_global_u4(qp), qscale, qf);
+  attend_consume<T, D, U>(st, r, qf);
+}
+
+// Several batches (base, base + stride, ... below s1), double-buffered: the
+// rows of batch i + 1 are requested before batch i is consumed, so a lane
+// keeps two batches in flight instead of waiting a memory round trip per
+// batch.  The last batch re-requests its own rows (cache hits) in place of a
+// next one, so no load sits under a branch (a branch join would make the
+// compiler wait for every outstanding load).  q is loaded first.
+template <typename T, int D, int U, typename TokOf>
+__device__ __forceinline__ void attend_pipelined(WaveSoftmax<T, D>& st, const T* qp, float qscale,
+                                                 const T* __restrict__ kb, const T* __restrict__ vb, int base,
+                                                 int stride, int s1, int grp, TokOf tok_of) {
+  if (base >= s1) return;
+  const uint4 q16 = load_global_u4(qp);
+  // Two buffers in turn (no copy between them: a copy lets the compiler load
+  // the next batch into the registers of the one still in flight, which makes
+  // every load wait for its predecessor).
+  AttendRows<U> ra, rb;
+  attend_issue<T, D, U>(ra, kb, vb, base, s1, grp, tok_of);
+  float qf[AttendLayout<T, D>::VEC];
+  attend_q<T, D>(q16, qscale, qf);
+  for (;;) {
+    attend_issue<T, D, U>(rb, kb, vb, base + stride < s1 ? base + stride : base, s1, grp, tok_of);
+    attend_consume<T, D, U>(st, ra, qf);
+    base += stride;
+    if (base >= s1) break;
+    attend_issue<T, D, U>(ra, kb, vb, base + stride < s1 ? base + stride : base, s1, grp, tok_of);
+    attend_consume<T, D, U>(st, rb, qf);
+    base += stride;
+    if (base >= s1) break;
+  }
 }
 
 // Transposed fold of the row groups (RPL groups of LPR lanes): each step at

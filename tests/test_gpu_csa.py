@@ -305,6 +305,10 @@ FUSED = [
     (8, 8, 8192, 128, 64, 16, torch.bfloat16),     # P = 8
     (32, 8, 4096, 128, 64, 8, torch.bfloat16),     # P = 2
     (64, 8, 2048, 128, 64, 4, torch.bfloat16),     # P = 1: one workgroup per head
+    # P = 1 on 256 heads: the double-buffered kernel; 70 chunks and 7 x 48 rows
+    # walk in ragged batches of 64
+    (32, 8, 3360, 128, 48, 7, torch.bfloat16),
+    (32, 8, 3360, 128, 48, 7, torch.float16),
     (1, 4, 8192, 64, 64, 8, torch.float16),
     (1, 2, 8192, 256, 32, 12, torch.float32),
     (1, 1, 1048576, 64, 64, 8, torch.bfloat16),    # 16384 chunks: keys stay in global memory
