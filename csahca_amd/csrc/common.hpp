@@ -247,6 +247,18 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Cross-workgroup words without cache maintenance: a 32-bit value travels in
+// a 64-bit word (tag << 32 | value), written and read with device-scope atomic
+// stores / loads, which are coherent across XCDs on their own.  A reader
+// accepts a word once it carries the tag it expects, so no fence orders it.
+__device__ __forceinline__ void put_tagged(uint64_t* p, uint32_t tag, uint32_t v) {
+  __hip_atomic_store(p, (static_cast<uint64_t>(tag) << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint64_t get_raw(const uint64_t* p) {
+  return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Value of lane (lane ^ off), off in {1, 2, 4, 8, 16, 32} (a constant once the
 // caller's loop is unrolled): DPP / row-swap moves, no LDS round trip.  The
 // whole wavefront must be active.
@@ -306,6 +318,8 @@ __device__ __forceinline__ float wave_sum(float v) {
 // ---------------------------------------------------------------------------
 int fail(int code, const char* msg);
 int fail_hip(hipError_t err, const char* where);
+// Compute units of the current device (cached per device; 0 if the query fails).
+int device_cu_count();
 void clear_error();
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }

@@ -102,14 +102,6 @@ struct StepParams {
   float qscale;
 };
 
-__device__ __forceinline__ void put_tagged(uint64_t* p, uint32_t tag, uint32_t v) {
-  __hip_atomic_store(p, (static_cast<uint64_t>(tag) << 32) | v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ uint64_t get_raw(const uint64_t* p) {
-  return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // Wait (bounded) until *p carries `tag`; returns its value bits.  On time-out
 // the sticky status bit is set and `bad` is raised: the caller poisons what it
 // computes from the word (the head's output becomes NaN and the head is
@@ -597,18 +589,6 @@ __global__ __launch_bounds__(kStepThreads) void csa_hybrid_kernel(StepParams a, 
     hca_chunk_body<T, true>(static_cast<const T*>(hp.q), static_cast<const T*>(hp.k), static_cast<const T*>(hp.v),
                             hp.scores, hp.means, hp.S, D, hp.chunk, hp.C, hp.scale, item);
   }
-}
-
-int device_cu_count() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (cached[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    cached[dev] = n;
-  }
-  return cached[dev];
 }
 
 size_t align256(size_t n) { return (n + 255) & ~size_t{255}; }

@@ -516,12 +516,21 @@ __device__ __forceinline__ uint4 dequant8_bf16(uint2 w, uint32_t sbyte) {
   return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
+// How a (query, head group, split) workgroup finishes.
+enum MfmaOut : int {
+  kMfmaPartials = 0,  // write (m, l, acc) partials for dsv4_merge_kernel
+  kMfmaDirect = 1,    // the only split: merge with the sink and write the output
+};
+
 struct MfmaArgs {
   int splits;           // slot-list splits per (query, head group)
   int tiles_per_split;  // 32-slot tiles per split
   int mfma_groups;      // head groups of 16
+  const float* sink;    // kMfmaDirect
+  bf16* out;
 };
 
+template <int kOut>
 __global__ __launch_bounds__(kMfmaThreads) void dsv4_mfma_kernel(const bf16* __restrict__ q, Dsv4Args a,
                                                                  MfmaArgs m) {
   __shared__ __align__(16) uint16_t vtile[kMfmaSlots * kVRowStride];     // [slot][dim] bf16 bits
@@ -758,21 +767,48 @@ __global__ __launch_bounds__(kMfmaThreads) void dsv4_mfma_kernel(const bf16* __r
     loc_n[1] = loc_nn[1];
   }
 
-  // Partials: m, l of head l16 (wave 0, lane group 0), acc rows of the C layout.
-  const int64_t pbase = (query * a.heads + h0) * m.splits + split;  // + h * splits
-  if (wave == 0 && lane < nh) {
-    const int64_t pi = pbase + static_cast<int64_t>(lane) * m.splits;
-    a.part_ml[2 * pi] = mh;
-    a.part_ml[2 * pi + 1] = lh;
-  }
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int h = 4 * grp + e;
-    if (h < nh) {
-      float* dst = a.part_acc + (pbase + static_cast<int64_t>(h) * m.splits) * kDim + wave * (kDim / kMfmaWaves) + l16;
-#pragma unroll
-      for (int j = 0; j < kOutTiles; ++j) dst[16 * j] = o[j][e];
+  if constexpr (kOut == kMfmaPartials) {
+    // Partials: m, l of head l16 (wave 0, lane group 0), acc rows of the C layout.
+    const int64_t pbase = (query * a.heads + h0) * m.splits + split;  // + h * splits
+    if (wave == 0 && lane < nh) {
+      const int64_t pi = pbase + static_cast<int64_t>(lane) * m.splits;
+      a.part_ml[2 * pi] = mh;
+      a.part_ml[2 * pi + 1] = lh;
     }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int h = 4 * grp + e;
+      if (h < nh) {
+        float* dst = a.part_acc + (pbase + static_cast<int64_t>(h) * m.splits) * kDim + wave * (kDim / kMfmaWaves) + l16;
+#pragma unroll
+        for (int j = 0; j < kOutTiles; ++j) dst[16 * j] = o[j][e];
+      }
+    }
+    return;
+  }
+
+  const int dcol = wave * (kDim / kMfmaWaves) + l16;  // this lane's output dims: dcol + 16 j
+  if constexpr (kOut == kMfmaDirect) {
+    // The merge of dsv4_merge_kernel over one partial (the sink a virtual token
+    // of logit sink[h] and value 0; the same operations).  Rows 4 grp + e of
+    // the C layout: their m, l sit in lanes 4 grp + e.
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int h = 4 * grp + e;
+      const float me = __shfl(mh, h), le = __shfl(lh, h);
+      if (h >= nh) continue;
+      const float sk = m.sink ? m.sink[h0 + h] * kLog2e : -INFINITY;
+      const float mx = le > 0.f ? fmaxf(sk, me) : sk;
+      const bool use = mx != -INFINITY && le > 0.f;
+      const float w = use ? fast_exp2(me - mx) : 0.f;
+      float L = use ? fmaf(le, w, 0.f) : 0.f;
+      if (m.sink && mx != -INFINITY) L += fast_exp2(sk - mx);
+      const float inv = le != le ? __builtin_nanf("") : (L > 0.f ? 1.f / L : 0.f);
+      bf16* orow = m.out + (query * a.heads + h0 + h) * kDim + dcol;
+#pragma unroll
+      for (int j = 0; j < kOutTiles; ++j) orow[16 * j] = from_f32<bf16>((use ? fmaf(w, o[j][e], 0.f) : 0.f) * inv);
+    }
+    return;
   }
 }
 
@@ -1391,9 +1427,17 @@ int dsv4_run(const Dsv4Call& c) {
     mm.splits = static_cast<int>(tiles);
     mm.tiles_per_split = static_cast<int>(tps);
     mm.mfma_groups = static_cast<int>(ceil_div(c.heads, kMfmaHeads));
+    mm.sink = c.sink;
+    mm.out = static_cast<bf16*>(c.out);
     const dim3 mgrid(static_cast<uint32_t>(c.nq * mm.mfma_groups * tiles));
-    const int rc = launch("dsv4_mfma_kernel", dsv4_mfma_kernel, mgrid, dim3(kMfmaThreads), 0, stream,
-                          static_cast<const bf16*>(c.q), a, mm);
+    const bf16* qp = static_cast<const bf16*>(c.q);
+    // One split (a slot list of at most one 32-slot tile per workgroup): the
+    // workgroup merges with the sink itself, no merge launch.
+    if (tiles == 1)
+      return launch("dsv4_mfma_kernel", dsv4_mfma_kernel<kMfmaDirect>, mgrid, dim3(kMfmaThreads), 0, stream, qp, a,
+                    mm);
+    const int rc = launch("dsv4_mfma_kernel", dsv4_mfma_kernel<kMfmaPartials>, mgrid, dim3(kMfmaThreads), 0, stream,
+                          qp, a, mm);
     if (rc != CSAHCA_OK) return rc;
     return launch("dsv4_merge_kernel", dsv4_merge_kernel<bf16>, dim3(static_cast<uint32_t>(c.nq * c.heads)),
                   dim3(kMergeThreads), 0, stream, static_cast<const float*>(a.part_ml),

@@ -47,6 +47,18 @@ int fail_hip(hipError_t err, const char* where) {
 
 void clear_error() { g_last_error.clear(); }
 
+int device_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 bool profiling_active() { return g_prof_on; }
 
 bool profile_take_events(hipEvent_t* start, hipEvent_t* stop) {
