@@ -19,6 +19,9 @@ SRC = PKG / "csrc"
 INCLUDE = ROOT / "include"
 BUILD = PKG / "_build"
 LIB = PKG / "libcsahca.so"
+# The same library with the decode step's phase stamps (csahca_amd/timeline.py).
+LIB_TIMELINE = PKG / "libcsahca_timeline.so"
+TIMELINE_SOURCE = "csa_step.hip"
 ARCH = os.environ.get("CSAHCA_OFFLOAD_ARCH", "gfx950")
 
 SOURCES = ["status.cpp", "csa.hip", "csa_step.hip", "dsv4.hip", "dsv4_pack.hip", "hca.hip", "block.hip"]
@@ -39,17 +42,31 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
 
 
+def _link(cc: str, objs, out: Path, verbose: bool) -> None:
+    tmp = out.with_suffix(".so.tmp")
+    cmd = [cc, "-shared", "-o", str(tmp)] + [str(o) for o in objs] + [f"--offload-arch={ARCH}"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, out)
+
+
 def build(verbose: bool = False, jobs: int | None = None) -> Path:
-    """Compile all sources (always) and link the shared library."""
+    """Compile all sources (always) and link the shared library, and beside it
+    the phase-timeline variant (the decode step built with its stamps)."""
     cc = hipcc()
     BUILD.mkdir(exist_ok=True)
     procs = []
     objs = []
-    for name in SOURCES:
-        src = SRC / name
-        obj = BUILD / (name.rsplit(".", 1)[0] + ".o")
-        objs.append(obj)
-        cmd = [cc, "-x", "hip", "-c", str(src), "-o", str(obj)] + COMMON_FLAGS
+    units = [(name, SRC / name, BUILD / (name.rsplit(".", 1)[0] + ".o"), []) for name in SOURCES]
+    tl_obj = BUILD / "csa_step_timeline.o"
+    units.append((TIMELINE_SOURCE + " (timeline)", SRC / TIMELINE_SOURCE, tl_obj, ["-DCSAHCA_STEP_TIMELINE"]))
+    for name, src, obj, extra in units:
+        if not extra:
+            objs.append(obj)
+        cmd = [cc, "-x", "hip", "-c", str(src), "-o", str(obj)] + COMMON_FLAGS + extra
         if verbose:
             print(" ".join(cmd), flush=True)
         procs.append((name, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
@@ -63,14 +80,9 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     if failed:
         msg = "\n".join(f"--- {n} ---\n{o}" for n, o in failed)
         raise RuntimeError(f"hipcc failed:\n{msg}")
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = [cc, "-shared", "-o", str(tmp)] + [str(o) for o in objs] + [f"--offload-arch={ARCH}"]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
-    os.replace(tmp, LIB)
+    _link(cc, objs, LIB, verbose)
+    step_obj = BUILD / (TIMELINE_SOURCE.rsplit(".", 1)[0] + ".o")
+    _link(cc, [tl_obj if o == step_obj else o for o in objs], LIB_TIMELINE, verbose)
     return LIB
 
 

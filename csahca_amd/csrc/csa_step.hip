@@ -54,6 +54,27 @@ size_t hca_workspace_means_offset(int64_t n_scores);
 
 namespace {
 
+// Phase timeline (a diagnostic build of its own, with -DCSAHCA_STEP_TIMELINE:
+// libcsahca_timeline.so, read by csahca_amd/timeline.py).  Thread 0 of each
+// workgroup records the device wall clock (100 MHz) at the phase boundaries
+// of the step: 0 entry, 1 phase A done (keys published), 2 keys gathered,
+// 3 top-k done, 4 attention done, 5 partial published, 6 output written (the
+// merging workgroup, or every workgroup when P = 1).  The product build
+// compiles none of it.
+#ifdef CSAHCA_STEP_TIMELINE
+constexpr int kTimelineBlocks = 4096;
+constexpr int kTimelineStamps = 8;
+__device__ uint64_t g_timeline[kTimelineBlocks][kTimelineStamps];
+#define CSAHCA_STAMP(i)                                                                   \
+  do {                                                                                    \
+    if (threadIdx.x == 0 && block < kTimelineBlocks) g_timeline[block][(i)] = wall_clock64(); \
+  } while (0)
+#else
+#define CSAHCA_STAMP(i) \
+  do {                  \
+  } while (0)
+#endif
+
 constexpr int kStepWaves = 4;
 constexpr int kStepThreads = kStepWaves * kWave;
 constexpr int kStepMaxP = 64;
@@ -162,6 +183,7 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
   int64_t pos_raw = 0;
   if constexpr (POS) pos_raw = load_global_raw<int64_t>(a.pos_dev);
   const T* __restrict__ q = static_cast<const T*>(a.q) + h * D;
+  CSAHCA_STAMP(0);
 
   // Loads that depend on nothing are issued together, unconditionally, and
   // consumed only after the summary rows are requested, so phase A costs one
@@ -312,6 +334,7 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
     }
   }
 
+  CSAHCA_STAMP(1);
   // ---- B: gather the head's keys, top-k -----------------------------------
   const uint32_t tag = launch_tag(epoch);
   // This thread timed out on a partner's word (or the head is poisoned: then
@@ -334,6 +357,7 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
     }
   }
   __syncthreads();
+  CSAHCA_STAMP(2);
   if (wave == 0) {
     int32_t* io = a.idx_out + h * a.topk;
     const bool write_ids = (p == 0);
@@ -348,6 +372,7 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
     for (int r = kk + lane; r < a.topk; r += kWave) emit(r, -1);
   }
   __syncthreads();
+  CSAHCA_STAMP(3);
 
   // ---- C: attention over this workgroup's slots ---------------------------
   const int nslots = a.topk * a.chunk;
@@ -380,6 +405,7 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
   }
   // Row groups folded transposed: every lane holds, and stores, kKeep of its
   // columns' sums.
+  CSAHCA_STAMP(4);
   const int fbase = fold_row_groups_share(st);
   float* cw = comb + wave * (D + 2);
   // A wavefront in which any lane timed out on a key marks its state with a
@@ -417,6 +443,7 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
   T* __restrict__ out = static_cast<T*>(a.out) + h * D;
   if (P == 1) {
     if (d < D) out[d] = from_f32<T>(poisoned ? Lsum : (Lsum > 0.f ? A / Lsum : 0.f));
+    CSAHCA_STAMP(6);
     return;
   }
 
@@ -430,6 +457,7 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
     put_tagged(pp, tag, __float_as_uint(M));
     put_tagged(pp + 1, tag, __float_as_uint(Lsum));
   }
+  CSAHCA_STAMP(5);
   if (p != 0) return;
   const uint64_t* ph = a.part + h * a.part_stride;
   if (P <= kRegMergeP) {
@@ -491,6 +519,7 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
       AA = fmaf(w, aj[j], AA);
     }
     if (d < D) out[d] = from_f32<T>(bad ? __builtin_nanf("") : (LL > 0.f ? AA / LL : 0.f));
+    CSAHCA_STAMP(6);
     // Every workgroup of the head has published, so each read this launch's
     // epoch long ago: the next launch's tags can start.  After a time-out (or
     // on a poisoned head) the head is poisoned.
@@ -544,6 +573,7 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
     for (int j = 0; j < P; ++j) AA = fmaf(wts[j], pb[j * (D + 2) + 2 + d], AA);
     out[d] = from_f32<T>(LL != LL ? LL : (LL > 0.f ? AA / LL : 0.f));
   }
+  CSAHCA_STAMP(6);
   __syncthreads();
   // A lost or poisoned partial poisons the head (see the register merge above).
   if (tid == 0)
@@ -1072,3 +1102,33 @@ extern "C" int csahca_csa_decode_step_noalloc(const void* q, const void* k_cache
                           num_chunks, nullptr, nullptr, chunk_size, top_k, nullptr, 0, stream_ptr, nullptr, 0,
                           nullptr, &rg);
 }
+
+#ifdef CSAHCA_STEP_TIMELINE
+// The timeline build's extra entry points: copy the stamps of the first
+// `blocks` workgroups of the last step launch (blocks x 8 uint64) to host
+// memory, zero them, and the stamps' clock rate.
+extern "C" int csahca_step_timeline_read(uint64_t* host, int64_t blocks) {
+  if (blocks < 0 || blocks > csahca::kTimelineBlocks) return CSAHCA_ERR_ARGUMENT;
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(csahca::g_timeline),
+                             sizeof(uint64_t) * csahca::kTimelineStamps * static_cast<size_t>(blocks), 0,
+                             hipMemcpyDeviceToHost) == hipSuccess
+             ? CSAHCA_OK
+             : CSAHCA_ERR_HIP;
+}
+
+// Frequency of the stamps' clock in kHz (0 if the query fails).
+extern "C" int64_t csahca_step_timeline_rate_khz() {
+  int dev = 0, khz = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess)
+    return 0;
+  return khz;
+}
+
+extern "C" int csahca_step_timeline_clear() {
+  static uint64_t zero[csahca::kTimelineBlocks][csahca::kTimelineStamps];
+  return hipMemcpyToSymbol(HIP_SYMBOL(csahca::g_timeline), zero, sizeof(zero), 0, hipMemcpyHostToDevice) ==
+                 hipSuccess
+             ? CSAHCA_OK
+             : CSAHCA_ERR_HIP;
+}
+#endif
