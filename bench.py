@@ -18,8 +18,12 @@ Infinity Cache would hold.  The timed loop therefore walks a rotation of
 touched bytes per lap -- with one cursor shared by every pass of the leg
 (warm-up, timed graph replays, eager passes), so no timed step reads a copy
 that an earlier pass touched less than a lap ago.  The K timed steps are
-HIP-graph replays on the stream the warm-up ran on, bracketed by HIP events
-on that stream; the roofline's time base is that replay period per launch.
+captured into one HIP graph on the stream the warm-up ran on, between two
+device clock stamps (csahca_device_clock_stamp: a one-wavefront kernel that
+stores the device wall clock), after an untimed pre-roll of up to 16 steps
+over copies outside the timed window; the graph is replayed once, between
+synchronizations, and the stamps' difference over K is the step period --
+the roofline's time base.  The graph's launch falls before the first stamp.
 
 Prints ONE JSON line on stdout; progress goes to stderr.
 """
@@ -107,25 +111,18 @@ def capture(stream, fns):
     return g
 
 
-def replay_timed(stream, graph, reps, tail=None, preroll=None):
-    """Replay `graph` `reps` times (then `tail` once) on `stream`; ms between
-    HIP events recorded on that stream around the replays.  `preroll` (a graph
-    over inputs already touched) runs untimed just before the start event, so
-    the host has submitted the timed replays before the device reaches them and
-    the events measure back-to-back execution, not the graph launch latency."""
+def replay_timed(stream, graph, reps):
+    """Replay `graph` `reps` times on `stream`; ms between HIP events recorded
+    on that stream around the replays."""
     import torch
 
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     with torch.cuda.stream(stream):
-        if preroll is not None:
-            preroll.replay()
         start.record(stream)
         for _ in range(reps):
             graph.replay()
-        if tail is not None:
-            tail.replay()
         end.record(stream)
     torch.cuda.synchronize()
     return start.elapsed_time(end)
@@ -261,20 +258,35 @@ def csa_bench(args, B=1, H=8, S=32768, D=128, chunk=64, top_k=8, copies=None, se
                sel_bytes=sel_bytes, summ_bytes=summ_bytes, planted=planted or "iid",
                trace_window={"kernel": "csa_step_kernel<", "skip": warmup + 1, "count": steps})
     if not args.no_graph:
-        per_graph = max(1, min(copies, steps))
+        # The K timed steps are captured into ONE graph between two device clock
+        # stamps (one-wavefront kernels storing the wall clock): the stamps time
+        # the steps on the device, back to back, and the graph's own launch --
+        # including a freshly captured graph's first-launch setup -- falls
+        # before the first stamp.  Step i reads copy (c0 + i) mod copies.  An
+        # untimed pre-roll of up to 16 steps over copies outside the timed
+        # window opens the graph: the device idles while the host captures, and
+        # the pre-roll brings it back to the state the warm-up left.
         c0 = cursor
-        graph = capture(s, [lambda j=(c0 + i) % copies: step(j) for i in range(per_graph)])
-        rem = steps % per_graph
-        tail = capture(s, [lambda j=(c0 + i) % copies: step(j) for i in range(rem)]) if rem else None
-        # Untimed pre-roll (~16 steps) over copies outside the timed window, run
-        # just before the start event: the device is busy while the host
-        # submits the timed replays.  The rotation then continues past them.
-        npre = min(16, copies - per_graph) if copies > per_graph else 0
-        pre = capture(s, [lambda j=(c0 + per_graph + i) % copies: step(j) for i in range(npre)]) if npre else None
-        res["ms_per_step_graph"] = replay_timed(s, graph, steps // per_graph, tail, pre) / steps
+        npre = min(16, copies - steps) if copies > steps else 0
+        stamps = torch.zeros(2, dtype=torch.int64, device=q.device)
+
+        def timed_steps():
+            for i in range(npre):
+                step((c0 + steps + i) % copies)
+            native.device_clock_stamp(stamps, 0)
+            for i in range(steps):
+                step((c0 + i) % copies)
+            native.device_clock_stamp(stamps, 1)
+
+        graph = capture(s, [timed_steps])
+        with torch.cuda.stream(s):
+            graph.replay()
+        torch.cuda.synchronize()
+        t = stamps.cpu().tolist()
+        res["ms_per_step_graph"] = (t[1] - t[0]) / native.device_clock_khz() / steps
         res["trace_window"]["skip"] += npre
-        cursor = c0 + per_graph + npre
-        del graph, tail, pre
+        cursor = c0 + steps + npre
+        del graph
     if eager_pass or args.no_graph:
         torch.cuda.synchronize()
         t0 = time.perf_counter()
@@ -350,7 +362,7 @@ def sweep_rows(args, points, steps):
         row = dict(B=B, S=S, top_k=k, keys=variant, copies=r["copies"], ms_per_step=round(ms, 5),
                    tokens_per_s=round(B / (ms * 1e-3), 1),
                    roofline=roofline(r["step_bytes"], step_flops(r), ms,
-                                     {"time_base": "graph replay period per step"}))
+                                     {"time_base": "step period in one HIP graph (device clock stamps)"}))
         log("sweep", json.dumps(row))
         rows.append(row)
         torch.cuda.empty_cache()
@@ -854,7 +866,7 @@ def summarize_trace(csv_path: Path, bench_json: Path) -> str:
             f"| median kernel duration | {statistics.median(dur):.3f} |",
             f"| mean start-to-start period | {statistics.fmean(period) if period else float('nan'):.3f} |",
             f"| first start to last end, per dispatch | {span:.3f} |",
-            f"| bench line `roofline.avg_launch_us` (HIP events around the replays) | {rl['avg_launch_us']:.3f} |",
+            f"| bench line `roofline.avg_launch_us` (device clock stamps around the timed steps) | {rl['avg_launch_us']:.3f} |",
             "", f"Roofline from the trace: {rl['bytes_per_launch']} B / {span:.3f} µs = "
                 f"{rl['bytes_per_launch'] / (span * 1e-6) / 1e9:.1f} GB/s = "
                 f"{rl['bytes_per_launch'] / (span * 1e-6) / 1e9 / PEAK_HBM_GBPS:.4f} of 8 TB/s "
@@ -936,10 +948,10 @@ def main():
         except (ValueError, AttributeError):
             traffic = None
     if args.route == "fused":
-        # One kernel per step: its launch period in the timed graph replays is the time base.
+        # One kernel per step: its period in the timed graph is the time base.
         dom, dom_bytes, dom_us = "csa_step_kernel", r["step_bytes"], ms * 1e3
         base = "eager step period" if args.no_graph else \
-            "graph replay period per launch (HIP events around the timed replays, on their stream)"
+            "step period in one HIP graph of the K steps (device clock stamps before and after them)"
     else:
         dom = max(kern, key=lambda n: kern[n]["total_ms"])
         dom_bytes, dom_us = kernel_bytes(dom, r), kern[dom]["avg_us"]
@@ -963,7 +975,7 @@ def main():
                                "summaries + split-KV attend + merge)",
                    "batch": 1, "heads": 8, "head_dim": 128, "seq_len": 32768, "chunk_size": 64, "top_k": 8,
                    "route": args.route, "tile": r["tile"] or None, "cache_copies_rotated": r["copies"],
-                   "timing": "eager launches" if args.no_graph else "hip graph replay",
+                   "timing": "eager launches" if args.no_graph else "one hip graph of the K steps, device clock stamps",
                    "parallelism": "single GPU"},
         "tokens_per_s": round(1e3 / ms, 1),
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS,

@@ -1,5 +1,6 @@
-// status.cpp -- error state of the C ABI (thread-local last-error message) and the
-// launch profiler (per-dispatch device durations from hipExtLaunchKernel events).
+// status.cpp -- error state of the C ABI (thread-local last-error message), the
+// launch profiler (per-dispatch device durations from hipExtLaunchKernel events)
+// and the device clock stamp (timing inside a captured graph).
 #include <hip/hip_runtime.h>
 
 #include <cstdio>
@@ -129,4 +130,32 @@ extern "C" int csahca_profile_result(int i, const char** name, int64_t* launches
   if (min_ms) *min_ms = p.min_ms;
   if (max_ms) *max_ms = p.max_ms;
   return CSAHCA_OK;
+}
+
+// Device clock stamp: one wavefront stores the device wall clock (a constant
+// rate counter, csahca_device_clock_khz) at dst when the stream reaches it.
+// Two stamps captured into one HIP graph around a run of kernels time that
+// run on the device, without the graph's own launch and without event
+// nodes in the graph.
+namespace csahca {
+namespace {
+__global__ __launch_bounds__(64) void clock_stamp_kernel(uint64_t* dst) {
+  if (threadIdx.x == 0) *dst = wall_clock64();
+}
+}  // namespace
+}  // namespace csahca
+
+extern "C" int csahca_device_clock_stamp(uint64_t* dst, void* stream) {
+  clear_error();
+  CSAHCA_REQUIRE(dst != nullptr, "null clock stamp pointer");
+  return launch("clock_stamp_kernel", clock_stamp_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), dst);
+}
+
+extern "C" int64_t csahca_device_clock_khz(void) {
+  int dev = 0, khz = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  return khz;
 }

@@ -72,6 +72,8 @@ _SIGNATURES = {
     "csahca_block_qkv": (_int, [_vp, _vp, _dbl, _vp, _vp, _vp, _vp, _vp, _vp, _int] + [_i64] * 5 + [_vp]),
     "csahca_profile_begin": (_int, []),
     "csahca_profile_end": (_int, []),
+    "csahca_device_clock_stamp": (_int, [_vp, _vp]),
+    "csahca_device_clock_khz": (_i64, []),
     "csahca_profile_result": (_int, [_int, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_i64),
                                      ctypes.POINTER(_dbl), ctypes.POINTER(_dbl), ctypes.POINTER(_dbl)]),
 }
@@ -766,6 +768,26 @@ def dsv4_sparse_decode_forward(q, paged_k_cache_u8, token_indices, topk_lengths,
             extra_token_indices.shape[1], _ptr(_opt(extra_topk_lengths)), _ptr(_opt(attn_sink)),
             float(softmax_scale), _ptr(out), _ptr(ws), ws.numel(), _stream()))
     return out
+
+
+# ---------------------------------------------------------------------------
+# Device clock stamps (timing inside captured graphs)
+# ---------------------------------------------------------------------------
+def device_clock_stamp(stamps: torch.Tensor, index: int) -> None:
+    """Store the device wall clock at stamps[index] (int64, on the device) when
+    the current stream reaches this point; capturable into a HIP graph."""
+    _check(stamps.is_cuda and stamps.dtype == torch.int64 and stamps.is_contiguous(),
+           "stamps must be a contiguous int64 CUDA tensor")
+    _check(0 <= index < stamps.numel(), "stamp index out of range")
+    _rc(lib().csahca_device_clock_stamp(stamps.data_ptr() + 8 * index, _stream()))
+
+
+def device_clock_khz() -> int:
+    """Rate of the device wall clock in kHz."""
+    khz = lib().csahca_device_clock_khz()
+    if khz <= 0:
+        raise RuntimeError("the device wall clock rate query failed")
+    return int(khz)
 
 
 # ---------------------------------------------------------------------------

@@ -358,6 +358,16 @@ int csahca_profile_end(void);
 int csahca_profile_result(int index, const char** kernel_name, int64_t* launches,
                           double* total_ms, double* min_ms, double* max_ms);
 
+/* No counterpart in the reference; a timing utility for callers that capture
+ * their steps into HIP graphs (bench.py times its decode steps this way).
+ * csahca_device_clock_stamp launches one wavefront that stores the device wall
+ * clock at *dst (device memory) when the stream reaches it; two stamps captured
+ * into one graph around a run of kernels time that run on the device, without
+ * the graph's launch.  csahca_device_clock_khz is that clock's rate (0 if the
+ * query fails). */
+int csahca_device_clock_stamp(uint64_t* dst, void* stream);
+int64_t csahca_device_clock_khz(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -35,6 +35,25 @@ def test_exports_every_header_symbol(lib):
     assert lib.csahca_abi_version() == native.ABI_VERSION == 1
 
 
+def test_clock_stamp_rejects_a_null_pointer_before_any_launch(lib):
+    assert lib.csahca_device_clock_stamp(None, None) == 1
+    assert b"null clock stamp pointer" in lib.csahca_last_error()
+
+
+def test_timeline_build_is_a_separate_library():
+    """The phase stamps live only in libcsahca_timeline.so (built beside the
+    product library); the product library exports none of their entry points."""
+    from csahca_amd import build
+
+    names = ("csahca_step_timeline_read", "csahca_step_timeline_clear", "csahca_step_timeline_rate_khz")
+    tl = ctypes.CDLL(str(build.LIB_TIMELINE))
+    for n in names:
+        assert hasattr(tl, n), n
+    prod = ctypes.CDLL(str(native.library_path()))
+    for n in names:
+        assert not hasattr(prod, n), n
+
+
 def test_workspace_sizes(lib):
     # B1 H8 D128 k8 chunk64 tile8: 64 tiles per head -> 8*64*(2 + 128) floats (+ alignment)
     n = lib.csahca_csa_decode_workspace_bytes(1, 8, 128, 8, 64, 8)
