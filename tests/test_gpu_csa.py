@@ -473,3 +473,49 @@ def test_largest_sweep_point_properties():
     assert all(v == 0 for v in native.csa_step_status().values())
     del q, kc, vc, summ, out, two
     torch.cuda.empty_cache()
+
+
+def test_device_clock_stamps_time_a_captured_run():
+    """Two clock stamps captured into one graph around decode steps: every
+    replay writes a later pair, the interval is positive and below the host's
+    wall time for the replay, and it grows with the number of steps inside."""
+    import time
+
+    B, H, S, D, chunk, k = 1, 8, 32768, 128, 64, 8
+    g = torch.Generator(device=DEV).manual_seed(7)
+    q = torch.randn(B, H, D, device=DEV, generator=g).to(torch.bfloat16)
+    kc = torch.randn(B, H, S, D, device=DEV, generator=g, dtype=torch.bfloat16)
+    vc = torch.randn(B, H, S, D, device=DEV, generator=g, dtype=torch.bfloat16)
+    summ = extension.csa_chunk_summary(kc, chunk)
+    khz = native.device_clock_khz()
+    assert khz > 0
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        native.csa_decode_step(q, kc, vc, summ, chunk, k)
+    torch.cuda.synchronize()
+    spans = {}
+    for n in (1, 8):
+        stamps = torch.zeros(2, dtype=torch.int64, device=DEV)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            native.device_clock_stamp(stamps, 0)
+            for _ in range(n):
+                native.csa_decode_step(q, kc, vc, summ, chunk, k)
+            native.device_clock_stamp(stamps, 1)
+        prev = None
+        for _ in range(3):
+            t0 = time.perf_counter()
+            with torch.cuda.stream(s):
+                graph.replay()
+            torch.cuda.synchronize()
+            wall_ms = (time.perf_counter() - t0) * 1e3
+            a, b = stamps.cpu().tolist()
+            assert b > a
+            assert (b - a) / khz < wall_ms
+            if prev is not None:
+                assert a > prev
+            prev = b
+        spans[n] = (b - a) / khz
+    assert spans[8] > 4 * spans[1]
+    assert all(v == 0 for v in native.csa_step_status().values())
