@@ -678,6 +678,35 @@ def hca_bench(steps=256, copies=4, hca_chunk=256):
     kv_bytes = 2 * B * H * S * D * 2
     out = {"config": f"B{B} H{H} S{S} D{D} bf16, hca_chunk {hca_chunk}; hybrid adds the CSA step "
                      f"(chunk 64, top-8, cached summaries) and the 0.7/0.3 blend"}
+
+    # The chunk-summary build (fp32 means of 64-row chunks): reads one cache,
+    # 64 MiB, and writes 2 MiB; the 8 K and V tensors above rotate as inputs
+    # (512 MiB, beyond the MALL).
+    srcs = ks + vs
+
+    def summary(j):
+        return native.csa_chunk_summary(srcs[j], 64)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for j in range(len(srcs)):
+            summary(j)
+    gr = capture(s, [lambda j=j: summary(j) for j in range(len(srcs))])
+    reps = max(1, steps // len(srcs))
+    ms = replay_timed(s, gr, reps) / (reps * len(srcs))
+    with torch.cuda.stream(s), native.profile_launches() as prof:
+        for _ in range(4):
+            for j in range(len(srcs)):
+                summary(j)
+    us = prof.results["csa_summary_vec_kernel"]["avg_us"]
+    sum_bytes = B * H * S * D * 2 + B * H * (S // 64) * D * 4
+    out["summary"] = {"config": f"csa_chunk_summary B{B} H{H} S{S} D{D} bf16, chunk 64 -> fp32",
+                      "ms_per_call_graph": round(ms, 5), "kernel_us": round(us, 3),
+                      "roofline": roofline(sum_bytes, 0, us * 1e-3,
+                                           {"kernel": "csa_summary_vec_kernel", "time_base": "per-dispatch HIP events"})}
+    log(f"summary: {out['summary']}")
+    del gr
     for name, fn in (("hca", hca), ("hybrid", hybrid)):
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
