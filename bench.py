@@ -1015,6 +1015,13 @@ def main():
         "attend_only_ms": round(r["attend_only_ms"], 6) if "attend_only_ms" in r else None,
         "attend_only_note": "precomputed selection, split-KV op (tile %s) + merge; the reference's "
                             "cuda-csa-tiled headline mode (H100: 0.0232 ms)" % r.get("attend_only_tile"),
+        # The reference's byte count for that mode (benchmark.py:153-155): the
+        # selected K and V rows, plus q, out and the chunk ids.
+        "attend_only_roofline": (roofline(r["sel_bytes"] + 2 * r["B"] * r["H"] * r["D"] * 2
+                                          + r["B"] * r["H"] * min(r["top_k"], r["S"] // r["chunk"]) * 4,
+                                          4 * r["B"] * r["H"] * r["D"] * min(r["top_k"], r["S"] // r["chunk"]) * r["chunk"],
+                                          r["attend_only_ms"], {"time_base": "graph replay period per call"})
+                                 if "attend_only_ms" in r else None),
         "ms_per_step_eager": round(r["ms_per_step_eager"], 6),
         "kernels_avg_us": {n: round(v["avg_us"], 3) for n, v in kern.items()},
     }
