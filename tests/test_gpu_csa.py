@@ -519,3 +519,27 @@ def test_device_clock_stamps_time_a_captured_run():
         spans[n] = (b - a) / khz
     assert spans[8] > 4 * spans[1]
     assert all(v == 0 for v in native.csa_step_status().values())
+
+
+def test_phase_timeline_tool_runs_the_stamped_build():
+    """python -m csahca_amd.timeline (libcsahca_timeline.so, in a child process
+    of its own) reports every phase boundary of the decode step in order."""
+    import re
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    r = subprocess.run([sys.executable, "-m", "csahca_amd.timeline", "--seq", "8192", "--steps", "5", "--copies", "2"],
+                       cwd=root, capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stderr[-2000:]
+    rows = [ln for ln in r.stdout.splitlines() if ln.startswith("| ") and not ln.startswith("| boundary")]
+    times = {}
+    for ln in rows:
+        cells = [c.strip() for c in ln.strip("|").split("|")]
+        times[cells[0]] = float(cells[1])
+    names = [n for n in times if not n.startswith("last workgroup")]
+    assert any(n.startswith("A:") for n in names) and any(n.startswith("D: output") for n in names)
+    seq = [times[n] for n in names]
+    assert all(b >= a for a, b in zip(seq, seq[1:])) and seq[0] > 0
+    assert re.search(r"clock \d+ kHz", r.stdout)
