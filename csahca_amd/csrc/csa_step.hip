@@ -16,7 +16,9 @@
 //   D. every workgroup publishes its partial (m, l, acc[D]); workgroup 0 of the
 //      head gathers the P partials and merges them (log-sum-exp) into the
 //      output.
-// With P == 1 a workgroup owns its head and nothing crosses workgroups.
+// With P == 1 a workgroup owns its head and nothing crosses workgroups; the
+// wide instantiation (16 wavefronts, P == 1) serves grids of about one head
+// per CU with large selections.
 //
 // Cross-workgroup exchange without cache maintenance: on gfx950 an agent-scope
 // fence writes back / invalidates the whole L2 of an XCD, which at hundreds of
@@ -143,9 +145,11 @@ __device__ __forceinline__ uint32_t wait_tagged(const uint64_t* p, uint64_t w, u
 }
 
 // PIPE: walk several batches of rows double-buffered (an instantiation of its
-// own, so the batch-by-batch kernel keeps its code).
-template <typename T, int D, int TOPK_M, bool POS, bool PIPE = false>
+// own, so the batch-by-batch kernel keeps its code).  W: wavefronts per
+// workgroup (the wide instantiation serves a head from one workgroup of 16).
+template <typename T, int D, int TOPK_M, bool POS, bool PIPE = false, int W = kStepWaves>
 __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
+  constexpr int NT = W * kWave;
   using L = AttendLayout<T, D>;
   constexpr int VEC = L::VEC, LPR = L::LPR, RPL = L::RPL;
   constexpr int SLPR = D / 4, SRPL = kWave / SLPR;  // fp32 summary rows
@@ -163,7 +167,7 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
   int32_t* sel = sidx + a.topk;
   uint32_t* lcount = reinterpret_cast<uint32_t*>(sel + a.topk);
   float* comb = reinterpret_cast<float*>(lcount + 1);
-  uint32_t* keys_l = reinterpret_cast<uint32_t*>(comb + kStepWaves * (D + 2));
+  uint32_t* keys_l = reinterpret_cast<uint32_t*>(comb + W * (D + 2));
 
   const int tid = threadIdx.x;
   const int wave = tid / kWave;
@@ -210,7 +214,7 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
       c1 = Cs * (p + 1) / P;
     }
     constexpr int US = kStepScoreUnroll;
-    constexpr int64_t kScoreStride = kStepWaves * SRPL * US;
+    constexpr int64_t kScoreStride = W * SRPL * US;
     // Rows blk + wave*SRPL*US + grp + SRPL*u (u < US); rows past the range
     // re-read row c0 (their scores are dropped).
     auto issue_rows = [&](int64_t blk, uint4 (&rs)[US]) {
@@ -250,7 +254,7 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
         C = min<int64_t>(nc, Cs);
         const int64_t cn = C - 1;
         const bool build = n > 0 && nc * a.chunk == n && nc <= Cs && n <= a.S;
-        if (build && cn >= blk && cn < blk + kStepWaves * SRPL * US && cn < c1) {
+        if (build && cn >= blk && cn < blk + W * SRPL * US && cn < c1) {
           if (wave == 0) {
             const int g2 = lane / LPR, c2 = lane % LPR;
             const T* kb0 = static_cast<const T*>(a.kcache) + (h * a.S + cn * a.chunk) * D + c2 * VEC;
@@ -342,16 +346,16 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
   bool bad = epoch == kPoisonEpoch;
   if (P > 1 && !bad) {
     const uint64_t* kg = a.keys + h * a.key_stride;
-    for (int64_t i0 = tid; i0 < C; i0 += kStepThreads * B8) {
+    for (int64_t i0 = tid; i0 < C; i0 += NT * B8) {
       uint64_t w[B8];
 #pragma unroll
       for (int j = 0; j < B8; ++j) {
-        const int64_t i = i0 + j * kStepThreads;
+        const int64_t i = i0 + j * NT;
         w[j] = i < C ? get_raw(kg + i) : 0;
       }
 #pragma unroll
       for (int j = 0; j < B8; ++j) {
-        const int64_t i = i0 + j * kStepThreads;
+        const int64_t i = i0 + j * NT;
         if (i < C) keys_l[i] = wait_tagged(kg + i, w[j], tag, a.status, bad);
       }
     }
@@ -396,7 +400,7 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
   WaveSoftmax<T, D> st;
   st.init();
   // Batch by batch, or double-buffered when this workgroup has its CU alone.
-  constexpr int kAttendStride = kStepWaves * RPL * U;
+  constexpr int kAttendStride = W * RPL * U;
   if (!PIPE || s1 - s0 <= kAttendStride) {
     for (int blk = s0; blk < s1; blk += kAttendStride)
       attend_block<T, D, U>(st, qp, a.qscale, kb, vb, blk + wave * RPL * U, s1, grp, tok_of);
@@ -421,7 +425,7 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
   float M = -INFINITY;
   bool poisoned = false;
 #pragma unroll
-  for (int w = 0; w < kStepWaves; ++w) {
+  for (int w = 0; w < W; ++w) {
     const float lw = comb[w * (D + 2) + 1];
     poisoned = poisoned || lw != lw;
     if (lw > 0.f) M = fmaxf(M, comb[w * (D + 2)]);
@@ -430,7 +434,7 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
   const int d = tid;
   if (M != -INFINITY) {
 #pragma unroll
-    for (int w = 0; w < kStepWaves; ++w) {
+    for (int w = 0; w < W; ++w) {
       const float lw = comb[w * (D + 2) + 1];
       if (lw > 0.f) {
         const float wt = fast_exp2(comb[w * (D + 2)] - M);
@@ -531,16 +535,16 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
   // spread over the 256 threads, then merge from LDS.
   float* pb = reinterpret_cast<float*>(keys_l);
   const int nw = P * (D + 2);
-  for (int i0 = bad ? nw : tid; i0 < nw; i0 += kStepThreads * kGather) {
+  for (int i0 = bad ? nw : tid; i0 < nw; i0 += NT * kGather) {
     uint64_t w[kGather];
 #pragma unroll
     for (int j = 0; j < kGather; ++j) {
-      const int i = i0 + j * kStepThreads;
+      const int i = i0 + j * NT;
       w[j] = i < nw ? get_raw(ph + i) : 0;
     }
 #pragma unroll
     for (int j = 0; j < kGather; ++j) {
-      const int i = i0 + j * kStepThreads;
+      const int i = i0 + j * NT;
       if (i < nw) {
         bool late = false;
         const uint32_t v = wait_tagged(ph + i, w[j], tag, a.status, late);
@@ -580,9 +584,9 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
     __hip_atomic_store(&a.epoch[h], LL != LL ? kPoisonEpoch : tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <typename T, int D, int TOPK_M, bool POS, bool PIPE = false>
-__global__ __launch_bounds__(kStepThreads) void csa_step_kernel(StepParams a) {
-  csa_step_body<T, D, TOPK_M, POS, PIPE>(a, blockIdx.x);
+template <typename T, int D, int TOPK_M, bool POS, bool PIPE = false, int W = kStepWaves>
+__global__ __launch_bounds__(W * kWave) void csa_step_kernel(StepParams a) {
+  csa_step_body<T, D, TOPK_M, POS, PIPE, W>(a, blockIdx.x);
 }
 
 // The hybrid step: blocks [0, step_blocks) run the decode step above, the rest
@@ -685,6 +689,31 @@ StepKernelFn step_kernel_pipelined(int dtype, int64_t head_dim, int m) {
     return m == 8 ? csa_step_kernel<f16, 128, 8, false, true>
                   : m == 32 ? csa_step_kernel<f16, 128, 32, false, true> : csa_step_kernel<f16, 128, 0, false, true>;
   return nullptr;
+}
+
+// The wide instantiation: a head's whole step in one workgroup of
+// kWideWaves wavefronts (P = 1, so nothing crosses workgroups), its summary and
+// K/V batches double-buffered.  bf16/f16, head_dim 128, count modes; nullptr
+// elsewhere.
+constexpr int kWideWaves = 16;
+StepKernelFn step_kernel_wide(int dtype, int64_t head_dim, int m) {
+  if (head_dim != 128) return nullptr;
+  if (dtype == CSAHCA_BF16)
+    return m == 8    ? csa_step_kernel<bf16, 128, 8, false, true, kWideWaves>
+           : m == 32 ? csa_step_kernel<bf16, 128, 32, false, true, kWideWaves>
+                     : csa_step_kernel<bf16, 128, 0, false, true, kWideWaves>;
+  if (dtype == CSAHCA_F16)
+    return m == 8    ? csa_step_kernel<f16, 128, 8, false, true, kWideWaves>
+           : m == 32 ? csa_step_kernel<f16, 128, 32, false, true, kWideWaves>
+                     : csa_step_kernel<f16, 128, 0, false, true, kWideWaves>;
+  return nullptr;
+}
+
+// CSAHCA_STEP_WIDE=0 / 1 turns the wide instantiation off / on wherever it
+// applies (read per call); unset (-1): the measured rule of decode_step_impl.
+int env_step_wide() {
+  const char* s = std::getenv("CSAHCA_STEP_WIDE");
+  return s ? (std::atoi(s) != 0 ? 1 : 0) : -1;
 }
 
 HybridKernelFn hybrid_kernel_for(int dtype, int m) {
@@ -799,13 +828,27 @@ int decode_step_impl(const void* q, const void* k_cache, const void* v_cache, co
                         16) == 0;
   const bool fused_dtype = dtype == CSAHCA_BF16 || dtype == CSAHCA_F16 || dtype == CSAHCA_F32;
   const bool fused_dim = head_dim == 64 || head_dim == 128 || head_dim == 256;
+  // One wide workgroup (16 wavefronts) per head where the grid holds about one
+  // head per CU and a head selects more than 1024 rows: there the split kernel
+  // would take P = 2 and its exchange, while 16 wavefronts keep more of the
+  // head's loads in flight (measured at 256 heads, top-32 of 64-token chunks:
+  // 2.5-5% faster).  With fewer heads the split kernel is faster: one CU
+  // returns about 64 B per clock to its wavefronts, so a head read through
+  // one CU takes ~4 us per 256 KiB, where P workgroups share it.
+  const int wide_env = env_step_wide();
+  const bool wide_ok = k > 0 && k <= kStepMaxK && (dtype == CSAHCA_BF16 || dtype == CSAHCA_F16) &&
+                       head_dim == 128 && aligned && ncu > 0 && pos_dev == nullptr && hybrid == nullptr &&
+                       env_wgs_per_head() == 0;
+  const bool wide = wide_ok && (wide_env >= 0 ? wide_env == 1
+                                              : (bh <= ncu && 2 * bh > ncu && k * chunk_size > 1024));
+  const int waves = wide ? kWideWaves : kStepWaves;
   const size_t lds_base = kCandBytes + (256 + 3 * static_cast<size_t>(k) + 1) * 4 +
-                          static_cast<size_t>(kStepWaves * (head_dim + 2)) * 4;
+                          static_cast<size_t>(waves * (head_dim + 2)) * 4;
   // Workgroups per head: the smallest P at which every wavefront streams its
   // share of summary rows and of selected K/V rows in ONE batch of loads (a
   // dependent HBM round trip, ~1.5 us, costs more than the cross-workgroup
   // exchange a larger P adds), capped at ~2 workgroups per CU over the grid.
-  int64_t P = env_wgs_per_head();
+  int64_t P = wide ? 1 : env_wgs_per_head();
   if (P == 0 && ncu > 0) {
     const int64_t esz = dtype == CSAHCA_F32 ? 4 : 2;
     const int64_t score_rows = int64_t{kStepWaves} * kStepScoreUnroll * std::max<int64_t>(1, kWave / (head_dim / 4));
@@ -883,6 +926,11 @@ int decode_step_impl(const void* q, const void* k_cache, const void* v_cache, co
       *hybrid_launched = true;
       return launch("csa_hybrid_kernel", hfn, dim3(static_cast<uint32_t>(bh * P + hblocks)), dim3(kStepThreads),
                     launch_lds(), stream, pr, *hybrid, static_cast<uint32_t>(bh * P));
+    }
+    if (wide) {
+      const StepKernelFn wf = step_kernel_wide(dtype, head_dim, m);
+      return launch("csa_step_kernel", wf, dim3(static_cast<uint32_t>(bh)), dim3(kWideWaves * kWave), lds, stream,
+                    pr);
     }
     StepKernelFn run = sfn;
     // (only where some wavefront has more than one batch of rows to walk)

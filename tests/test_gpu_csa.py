@@ -341,6 +341,43 @@ def test_fused_step_matches_oracle_and_two_pass(B, H, S, D, chunk, k, dtype):
     assert all(v == 0 for v in native.csa_step_status().values())
 
 
+WIDE = [
+    # B, H, S, D, chunk, k, dtype: the 16-wavefront instantiation forced
+    # (CSAHCA_STEP_WIDE=1); phase A batches of 256 summary rows, phase C of 256
+    # selected rows
+    (1, 8, 32768, 128, 64, 8, torch.bfloat16),   # 512 chunks, 512 rows: two double-buffered batches each
+    (4, 8, 8192, 128, 48, 7, torch.float16),     # 170 chunks (one batch), 336 rows (ragged second batch)
+    (2, 4, 16384, 128, 64, 40, torch.bfloat16),  # 256 chunks, 2560 rows: ten batches of attention
+    (1, 2, 99968, 128, 64, 8, torch.bfloat16),   # 1562 chunks: seven batches, the last ragged
+    (32, 8, 2048, 128, 64, 20, torch.bfloat16),  # 256 heads, 1280 rows: the default rule's own choice
+]
+
+
+@pytest.mark.parametrize("B,H,S,D,chunk,k,dtype", WIDE)
+def test_wide_step_matches_oracle_and_split_step(B, H, S, D, chunk, k, dtype, monkeypatch):
+    """One workgroup of 16 wavefronts per head against the oracle (ids bit-exact
+    up to 1e-5 score ties, outputs within the bf16 bar) and against the split
+    kernel on the same inputs (identical ids)."""
+    g = torch.Generator().manual_seed(B * 5 + H + k + S // 1024)
+    q = torch.randn(B, H, D, generator=g).to(dtype)
+    kc = torch.randn(B, H, S, D, generator=g).to(dtype)
+    vc = torch.randn(B, H, S, D, generator=g).to(dtype)
+    qd, kd, vd = q.to(DEV), kc.to(DEV), vc.to(DEV)
+    summ = extension.csa_chunk_summary(kd, chunk)
+    monkeypatch.setenv("CSAHCA_STEP_WIDE", "1")
+    out, idx = native.csa_decode_step(qd, kd, vd, summ, chunk, k)
+    monkeypatch.setenv("CSAHCA_STEP_WIDE", "0")
+    out_split, idx_split = native.csa_decode_step(qd, kd, vd, summ, chunk, k)
+    assert torch.equal(idx, idx_split)
+    want, scores = oracle.select_topk(q, summ.cpu(), k)
+    assert_indices(idx, want, scores)
+    atol, rtol = tol_for(dtype)
+    ref = oracle.csa_attend(q, kc, vc, idx.cpu(), chunk, prob_dtype=oracle.F32)
+    assert_close(out, ref, atol, rtol, "wide step vs oracle")
+    assert torch.allclose(out.float(), out_split.float(), atol=atol, rtol=rtol)
+    assert all(v == 0 for v in native.csa_step_status().values())
+
+
 def test_fused_step_ties_and_planted_selections():
     B, H, S, D, chunk, k = 1, 8, 32768, 128, 64, 8  # P = 8 workgroups per head exchange keys
     q = torch.ones(B, H, D, dtype=torch.bfloat16, device=DEV)
