@@ -465,49 +465,58 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
   if (p != 0) return;
   const uint64_t* ph = a.part + h * a.part_stride;
   if (P <= kRegMergeP) {
-    // Few partials: the thread of column d gathers every (m_j, l_j) and its
-    // acc_j[d] itself -- one batch of tagged loads (partials past P re-read
-    // partial 0, columns past D re-read column 0; both dropped) -- and forms
-    // the weights and its column: no LDS and no barrier.  Partials are
-    // combined in the same order and with the same operations as below.
-    const int dd = d < D ? d : 0;
-    uint64_t wm[kRegMergeP], wl[kRegMergeP], wa[kRegMergeP];
-#pragma unroll
-    for (int j = 0; j < kRegMergeP; ++j) {
-      const uint64_t* pj = ph + static_cast<int64_t>(j < P ? j : 0) * (D + 2);
-      wm[j] = get_raw(pj);
-      wl[j] = get_raw(pj + 1);
-      wa[j] = get_raw(pj + 2 + dd);
-    }
+    // Few partials: the thread of column d gathers every acc_j[d] itself, and
+    // lane l of each wavefront one of the 16 words (m_j, l_j), j = (l % 16) / 2,
+    // which the wavefront shares by lane permutes -- one batch of 9 tagged loads
+    // per thread (partials past P re-read partial 0, columns past D re-read
+    // column 0; both dropped) -- and forms the weights and its column: no LDS
+    // and no barrier.  Partials are combined in the same order and with the
+    // same operations as below.
     // Words not yet tagged are re-read all together, one round trip per
-    // round (a word-by-word wait would cost a round trip per late word).
-    for (uint32_t it = 0;; ++it) {
-      bool ready = true;
+    // round; readiness is decided per wavefront (its lanes hold the (m_j, l_j)
+    // words every lane needs).  (Measured: 9 loads per thread per round in
+    // place of 24 -- every (m_j, l_j) in every thread -- took the B1 H8 S32768
+    // step from 10.63 to 10.20 us; a second round kept in flight half a round
+    // trip behind the first was slower, 10.37 us.)
+    const int dd = d < D ? d : 0;
+    const int jm = (lane & 15) >> 1;
+    const uint64_t* pml = ph + static_cast<int64_t>(jm < P ? jm : 0) * (D + 2) + (lane & 1);
+    constexpr int NW = kRegMergeP + 1;
+    auto poll = [&](uint64_t(&w)[NW]) {
 #pragma unroll
-      for (int j = 0; j < kRegMergeP; ++j)
-        ready = ready && static_cast<uint32_t>(wm[j] >> 32) == tag && static_cast<uint32_t>(wl[j] >> 32) == tag &&
-                static_cast<uint32_t>(wa[j] >> 32) == tag;
-      if (ready || bad) break;
+      for (int j = 0; j < kRegMergeP; ++j) w[j] = get_raw(ph + static_cast<int64_t>(j < P ? j : 0) * (D + 2) + 2 + dd);
+      w[kRegMergeP] = get_raw(pml);
+    };
+    auto ready = [&](const uint64_t(&w)[NW]) {
+      bool r = true;
+#pragma unroll
+      for (int j = 0; j < NW; ++j) r = r && static_cast<uint32_t>(w[j] >> 32) == tag;
+      return __all(r) != 0;
+    };
+    // Wavefronts past the last column have nothing to merge (wavefront 0, which
+    // publishes the epoch, always has columns).
+    if (wave * kWave >= D) return;
+    // A key that timed out anywhere in the wavefront poisons its columns: no wait.
+    if (__any(bad)) bad = true;
+    uint64_t wf[NW];
+    poll(wf);
+    for (uint32_t it = 0;; ++it) {
+      if (bad || ready(wf)) break;
       if (it >= kSpinLimit) {
         __hip_atomic_fetch_or(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         bad = true;
         break;
       }
       __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-      for (int j = 0; j < kRegMergeP; ++j) {
-        const uint64_t* pj = ph + static_cast<int64_t>(j < P ? j : 0) * (D + 2);
-        wm[j] = get_raw(pj);
-        wl[j] = get_raw(pj + 1);
-        wa[j] = get_raw(pj + 2 + dd);
-      }
+      poll(wf);
     }
     float mj[kRegMergeP], lj[kRegMergeP], aj[kRegMergeP];
+    const uint32_t mlv = static_cast<uint32_t>(wf[kRegMergeP]);
 #pragma unroll
     for (int j = 0; j < kRegMergeP; ++j) {
-      mj[j] = __uint_as_float(static_cast<uint32_t>(wm[j]));
-      lj[j] = __uint_as_float(static_cast<uint32_t>(wl[j]));
-      aj[j] = __uint_as_float(static_cast<uint32_t>(wa[j]));
+      mj[j] = __uint_as_float(static_cast<uint32_t>(__shfl(static_cast<int>(mlv), 2 * j, kWave)));
+      lj[j] = __uint_as_float(static_cast<uint32_t>(__shfl(static_cast<int>(mlv), 2 * j + 1, kWave)));
+      aj[j] = __uint_as_float(static_cast<uint32_t>(wf[j]));
     }
     float mx = -INFINITY;
 #pragma unroll
