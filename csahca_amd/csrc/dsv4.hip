@@ -860,6 +860,11 @@ constexpr int kQTileBytes = kQSub * kQRow * 2;
 constexpr int kQOutStride = kDim + 4;
 constexpr int kQMergeBytes = kQWaves * kQHeads * kQOutStride * 4;
 constexpr int kQSmemBytes = kQMergeBytes > kQWaves * kQTileBytes ? kQMergeBytes : kQWaves * kQTileBytes;
+// Query rows in LDS (the B operand of S^T, shared by the 4 wavefronts): 520
+// bf16 = 1040 B = 260 dwords (4 mod 64 banks), so the 16 heads' 16-byte reads
+// of one lane group cover the 64 banks once.
+constexpr int kQQRow = kDim + 8;
+constexpr int kQQUnits = kQHeads * (kDim / 8) / kQThreads;  // 16-byte query units per thread
 constexpr int kQBuf = 2;                  // sub-tiles of rows in flight per wavefront
 constexpr int kQNopeChunks = kNope / 16;  // 28 chunks of 16 e4m3 bytes
 constexpr int kQChunksPerLane = 9;        // 7 e4m3 chunks + 2 rope chunks
@@ -885,6 +890,7 @@ struct QRows {
 __global__ __launch_bounds__(kQThreads) void dsv4_query_kernel(const bf16* __restrict__ q, Dsv4Args a,
                                                                QueryArgs g) {
   __shared__ __align__(16) uint8_t smem[kQSmemBytes];
+  __shared__ __align__(16) uint16_t qlds[kQHeads * kQQRow];
   __shared__ float qml[kQWaves][kQHeads][2];
 
   const int tid = threadIdx.x;
@@ -947,10 +953,16 @@ __global__ __launch_bounds__(kQThreads) void dsv4_query_kernel(const bf16* __res
   SlotIdx si0 = idx_issue(min(wave, last_sub)), si1 = idx_issue(min(wave + kQWaves, last_sub));
   // The query rows and the sink go out after the lengths and the first
   // indices, so waiting for those (the rows' addresses) does not wait for them.
-  uint4 qw[16];
-  const int hq = h0 + min(l16, nh - 1);
+  // Thread t loads the workgroup's 16-byte query units t + 256 u (head e / 64,
+  // dims 8 (e % 64) .. +7; heads past nh re-read head h0 + nh - 1 and are
+  // stored as zeros), staged once in LDS for all 4 wavefronts.
+  uint4 qw[kQQUnits];
 #pragma unroll
-  for (int kk = 0; kk < 16; ++kk) qw[kk] = load_global_u4(q + (query * a.heads + hq) * kDim + 32 * kk + 8 * grp);
+  for (int u = 0; u < kQQUnits; ++u) {
+    const int e = tid + kQThreads * u;
+    qw[u] = load_global_u4(q + (query * a.heads + h0 + min(e / (kDim / 8), nh - 1)) * kDim + 8 * (e % (kDim / 8)));
+  }
+  const int hq = h0 + min(l16, nh - 1);
   const float sink_raw = g.sink ? load_global_raw<float>(g.sink + hq) : -INFINITY;
   asm volatile("" : "+v"(si0.li), "+v"(si0.le), "+v"(si1.li), "+v"(si1.le));
   n_swa = a.lens ? max(0, min(len_raw, a.topk_slots)) : a.topk_slots;
@@ -962,9 +974,14 @@ __global__ __launch_bounds__(kQThreads) void dsv4_query_kernel(const bf16* __res
   rows_issue(sub_of(0), si0, cur);
   rows_issue(sub_of(1), si1, nxt);
   SlotIdx sn = idx_issue(min(wave + kQWaves * kQBuf, last_sub));  // indices of sub-tile kQBuf
-  bf16x8_t qb[16];
 #pragma unroll
-  for (int kk = 0; kk < 16; ++kk) qb[kk] = __builtin_bit_cast(bf16x8_t, l16 < nh ? qw[kk] : make_uint4(0u, 0u, 0u, 0u));
+  for (int u = 0; u < kQQUnits; ++u) {
+    const int e = tid + kQThreads * u;
+    *reinterpret_cast<uint4*>(qlds + (e / (kDim / 8)) * kQQRow + 8 * (e % (kDim / 8))) =
+        e / (kDim / 8) < nh ? qw[u] : make_uint4(0u, 0u, 0u, 0u);
+  }
+  lds_barrier();  // every wavefront's query units are in LDS before the first sub-tile
+  const uint16_t* qrow = qlds + l16 * kQQRow + 8 * grp;  // B operand: head l16, dims 32 kk + 8 grp ..
 
   uint16_t* tile = reinterpret_cast<uint16_t*>(smem + wave * kQTileBytes);
   float m = -INFINITY, l = 0.f;  // online softmax of head l16 (this lane's 4 slots per sub-tile)
@@ -1005,19 +1022,23 @@ __global__ __launch_bounds__(kQThreads) void dsv4_query_kernel(const bf16* __res
     for (int i = 0; i < 2; ++i)
       *reinterpret_cast<uint4*>(trow + kNope + 8 * (grp + 4 * i)) = rw.ok ? rw.c[7 + i] : make_uint4(0u, 0u, 0u, 0u);
     wave_lds_sync();
-    // The A reads go out 8 at a time ahead of their MFMAs (one LDS round trip
-    // per 8, not per MFMA); two accumulators halve the dependent MFMA chain.
+    // The A reads (tile rows) and B reads (query rows) go out 8 at a time
+    // ahead of their MFMAs (one LDS round trip per 8, not per MFMA); two
+    // accumulators halve the dependent MFMA chain.
     f32x4_t sacc0 = f32x4_t{0.f, 0.f, 0.f, 0.f}, sacc1 = sacc0;
 #pragma unroll
     for (int k0 = 0; k0 < 16; k0 += 8) {
-      uint4 kr[8];
+      uint4 kr[8], qr[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u) kr[u] = *reinterpret_cast<const uint4*>(trow + 32 * (k0 + u) + 8 * grp);
 #pragma unroll
+      for (int u = 0; u < 8; ++u) qr[u] = *reinterpret_cast<const uint4*>(qrow + 32 * (k0 + u));
+#pragma unroll
       for (int u = 0; u < 8; u += 2) {
-        sacc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kr[u]), qb[k0 + u], sacc0, 0, 0, 0);
-        sacc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kr[u + 1]), qb[k0 + u + 1], sacc1,
-                                                        0, 0, 0);
+        sacc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kr[u]),
+                                                        __builtin_bit_cast(bf16x8_t, qr[u]), sacc0, 0, 0, 0);
+        sacc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kr[u + 1]),
+                                                        __builtin_bit_cast(bf16x8_t, qr[u + 1]), sacc1, 0, 0, 0);
       }
     }
     float x[4];
