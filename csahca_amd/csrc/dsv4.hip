@@ -820,29 +820,41 @@ __global__ __launch_bounds__(kMfmaThreads) void dsv4_mfma_kernel(const bf16* __r
 // b, b + 8, b + 16, ... -- the same XCD (blocks go to XCD blockIdx % 8), so
 // at H = 64 the four workgroups that read a query's rows share one L2.
 //
-// The 4 wavefronts split the slot list in 16-slot sub-tiles (wave w takes
-// sub-tiles w, w + 4, ...).  Per sub-tile a wavefront
-//   * loads the 16 rows (lane l: slot l%16, 16-byte chunks l/16 + 4i of the
-//     576-byte row, and the slot's 8 scale bytes), dequantises the e4m3 part
-//     to bf16 exactly as the reference dequant rounds it, and stores the
-//     [slot][dim] tile in its own LDS slice;
+// The slot list goes in rounds of 4 sub-tiles of 16 slots (wavefront w takes
+// sub-tile w of each round).  Per round each wavefront
+//   * loads its sub-tile's 16 rows (lane l: slot l%16, 16-byte chunks l/16 +
+//     4i of the 576-byte row, and the slot's 8 scale bytes), dequantises the
+//     e4m3 part to bf16 exactly as the reference dequant rounds it, and stores
+//     the [slot][dim] tile in its own LDS slice;
 //   * computes S^T = K Q^T on v_mfma_f32_16x16x32_bf16 (A = the tile row of
-//     slot l%16, read 16 bytes at a time; B = the query rows, in registers):
-//     lane l holds S^T[slot 4(l/16)+e][head l%16];
-//   * runs the online softmax of head l%16 over its 4 slots and the 3 lanes
-//     with the same l%16 (row swaps 16 and 32); the probabilities, rounded to
-//     bf16, are already the B operand of the PV product below;
-//   * accumulates O^T = V^T P^T on v_mfma_f32_16x16x16_bf16, 32 blocks of 16
-//     output dims; the A operand V^T[dim][slot 4g..4g+3] comes straight out
-//     of the row-major tile through ds_read_b64_tr_b16.  Lane l holds
-//     O^T[dim 16 blk + 4(l/16) + e][head l%16], so the softmax rescale of a
-//     lane is its own head's factor -- no transposes anywhere.
-// Finally the 4 wavefronts' (m, l, O) partials meet in LDS and each wavefront
-// merges a quarter of the output dims with the sink as a virtual token of
-// logit sink[h] and value 0 (csrc/dsv4_attention.cu:252-269).
+//     slot l%16, B = the query rows, both read from LDS 16 bytes at a time):
+//     lane l holds S^T[slot 4(l/16)+e][head l%16], and publishes the masked,
+//     scaled scores in LDS;
+//   * after a barrier, runs the online softmax of head l%16 over the round's
+//     4 sub-tiles (its 4 slots of each and the 3 lanes with the same l%16, row
+//     swaps 16 and 32) -- every wavefront the same, so m and l agree -- with
+//     the bf16-rounded probabilities as the B operand of the PV product;
+//   * accumulates O^T = V^T P^T on v_mfma_f32_16x16x16_bf16 for ITS 128 output
+//     dims (8 blocks of 16) over all 4 tiles; the A operand V^T[dim][slot
+//     4g..4g+3] comes straight out of the row-major tiles through
+//     ds_read_b64_tr_b16.  Lane l holds O^T[dim 16 blk + 4(l/16) + e][head
+//     l%16], so the softmax rescale of a lane is its own head's factor.
+// Finally each wavefront normalises its dims with the sink as a virtual token
+// of logit sink[h] and value 0 (csrc/dsv4_attention.cu:252-269) and stores
+// them: no partials to merge.
 // MFMA lane layouts: 16x16x32 as above; 16x16x16: A lane l elem j =
 // A[l%16][4(l/16)+j], B lane l elem j = B[4(l/16)+j][l%16], C as 16x16x32.
 // ---------------------------------------------------------------------------
+// float_to_bf16_bits without a branch (the same bits: round to nearest even,
+// infinities unchanged, NaN quietened), so that no control flow sits between
+// the MFMAs whose accumulators it feeds.
+__device__ __forceinline__ uint32_t bf16_bits_nb(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  return (u & 0x7fffffffu) > 0x7f800000u ? ((u >> 16) | 0x40u) : r;
+}
+__device__ __forceinline__ uint32_t bf16x2_nb(float lo, float hi) { return bf16_bits_nb(lo) | (bf16_bits_nb(hi) << 16); }
+
 constexpr int kQSub = 16;                 // slots per sub-tile
 constexpr int kQWaves = 4;
 constexpr int kQThreads = kQWaves * kWave;
@@ -855,11 +867,10 @@ constexpr int kQHeads = 16;
 // conflict-free.
 constexpr int kQRow = kDim + 24;
 constexpr int kQTileBytes = kQSub * kQRow * 2;
-// Merge rows: 516 floats (4 mod 64 banks), so the 16 heads' 16-byte stores
-// of one lane group cover all 64 banks.
-constexpr int kQOutStride = kDim + 4;
-constexpr int kQMergeBytes = kQWaves * kQHeads * kQOutStride * 4;
-constexpr int kQSmemBytes = kQMergeBytes > kQWaves * kQTileBytes ? kQMergeBytes : kQWaves * kQTileBytes;
+constexpr int kQOutBlocks = kDim / kQWaves / 16;  // 16-dim output blocks per wavefront
+// The 4 tiles, then each wavefront's masked scores (a lane's 4 floats) and
+// its sub-tile's slot bits.
+constexpr int kQSmemBytes = kQWaves * kQTileBytes + kQWaves * kWave * 4 * 4 + kQWaves * 4;
 // Query rows in LDS (the B operand of S^T, shared by the 4 wavefronts): 520
 // bf16 = 1040 B = 260 dwords (4 mod 64 banks), so the 16 heads' 16-byte reads
 // of one lane group cover the 64 banks once.
@@ -891,7 +902,6 @@ __global__ __launch_bounds__(kQThreads) void dsv4_query_kernel(const bf16* __res
                                                                QueryArgs g) {
   __shared__ __align__(16) uint8_t smem[kQSmemBytes];
   __shared__ __align__(16) uint16_t qlds[kQHeads * kQQRow];
-  __shared__ float qml[kQWaves][kQHeads][2];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -984,14 +994,22 @@ __global__ __launch_bounds__(kQThreads) void dsv4_query_kernel(const bf16* __res
   const uint16_t* qrow = qlds + l16 * kQQRow + 8 * grp;  // B operand: head l16, dims 32 kk + 8 grp ..
 
   uint16_t* tile = reinterpret_cast<uint16_t*>(smem + wave * kQTileBytes);
-  float m = -INFINITY, l = 0.f;  // online softmax of head l16 (this lane's 4 slots per sub-tile)
-  f32x4_t o[kDim / 16];
+  float* xs = reinterpret_cast<float*>(smem + kQWaves * kQTileBytes);  // [wave][lane][4] masked scores
+  uint32_t* flags = reinterpret_cast<uint32_t*>(xs + kQWaves * kWave * 4);  // [wave] valid-slot bits
+  float m = -INFINITY, l = 0.f;  // online softmax of head l16 (this lane's 4 slots of each sub-tile)
+  f32x4_t o[kQOutBlocks];
 #pragma unroll
-  for (int j = 0; j < kDim / 16; ++j) o[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < kQOutBlocks; ++j) o[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // V^T A operand of output block j (dims 128 wave + 16 j ..) of a tile: lane a
+  // of group g passes &V[4g + a/4][128 wave + 16 j + 4(a%4)].
+  const int vofs = (4 * grp + l16 / 4) * kQRow + 4 * (l16 % 4) + (kDim / kQWaves) * wave;
 
-  auto process = [&](const QRows& rw) {
-    const uint32_t valid16 = static_cast<uint32_t>(__ballot(rw.ok) & 0xffffull);  // slot bits (lanes 0..15)
-    if (valid16 == 0u) return;  // wave-uniform
+  // This wavefront's sub-tile of the round: dequantise it into its tile, score
+  // it against the 16 heads, publish the masked scores and the slot bits.
+  auto score_own = [&](const QRows& rw, bool has) {
+    const uint32_t valid16 = has ? static_cast<uint32_t>(__ballot(rw.ok) & 0xffffull) : 0u;  // wave-uniform
+    if (lane == 0) flags[wave] = valid16;
+    if (valid16 == 0u) return;
     // Scale byte 255 takes the software decode, decided once per sub-tile.
     const bool any255 = __ballot(rw.ok && has_scale_255(rw.sc)) != 0ull;
     uint16_t* trow = tile + l16 * kQRow;
@@ -1041,139 +1059,116 @@ __global__ __launch_bounds__(kQThreads) void dsv4_query_kernel(const bf16* __res
                                                         __builtin_bit_cast(bf16x8_t, qr[u + 1]), sacc1, 0, 0, 0);
       }
     }
-    float x[4];
-    float mt = -INFINITY;
+    f32x4_t x;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
+    for (int e = 0; e < 4; ++e)
       x[e] = ((valid16 >> (4 * grp + e)) & 1u) ? (sacc0[e] + sacc1[e]) * a.qscale : -INFINITY;
-      mt = fmaxf(mt, x[e]);
-    }
-    mt = fmaxf(mt, __uint_as_float(lane_xor<16>(__float_as_uint(mt), lane)));
-    mt = fmaxf(mt, __uint_as_float(lane_xor<32>(__float_as_uint(mt), lane)));
-    // Lazy rescale: the running max m only moves when a score exceeds it by
-    // more than 2^8 (so probabilities stay below 2^8, exact enough in fp32
-    // and as bf16 PV operands) or on the first valid sub-tile; the output
-    // accumulators are rescaled only when some head of the wavefront moved.
-    const bool move = mt > m + 8.f;  // m = -inf: always
-    const float m_new = move ? mt : m;  // finite: the sub-tile has a valid slot
-    const float alpha = move ? fast_exp2(m - m_new) : 1.f;
-    float p[4];
-    float ps = 0.f;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      p[e] = fast_exp2(x[e] - m_new);
-      ps += p[e];
-    }
-    l = l * alpha + ps;
-    m = m_new;
-    const bool rescale = __any(move);
-    const i16x4_t pb = __builtin_bit_cast(
-        i16x4_t, make_uint2(static_cast<uint32_t>(float_to_bf16_bits(p[0])) |
-                                (static_cast<uint32_t>(float_to_bf16_bits(p[1])) << 16),
-                            static_cast<uint32_t>(float_to_bf16_bits(p[2])) |
-                                (static_cast<uint32_t>(float_to_bf16_bits(p[3])) << 16)));
-    // V^T A operand of output block j: lane a of group g passes &V[4g + a/4][16 j + 4(a%4)].
-    const uint16_t* vsrc = tile + (4 * grp + l16 / 4) * kQRow + 4 * (l16 % 4);
-    if (rescale) {
-#pragma unroll
-      for (int j = 0; j < kDim / 16; ++j)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) o[j][e] *= alpha;
-    }
-#pragma unroll
-    for (int j0 = 0; j0 < kDim / 16; j0 += 8) {  // transposed reads 8 at a time ahead of their MFMAs
-      i16x4_t vt[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) vt[u] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(vsrc + 16 * (j0 + u)));
-#pragma unroll
-      for (int u = 0; u < 8; ++u) o[j0 + u] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt[u], pb, o[j0 + u], 0, 0, 0);
-    }
-    wave_lds_sync();  // the tile is rewritten by the next sub-tile
+    *reinterpret_cast<f32x4_t*>(xs + (wave * kWave + lane) * 4) = x;
   };
 
-  // One sub-tile per iteration (a single copy of its code: the kernel stays
-  // well inside the instruction cache); the row buffers rotate through
-  // registers and the rows kQBuf sub-tiles ahead are requested as soon as a
-  // buffer frees up, with their indices requested one round earlier.
-  for (int it = 0; it < nsub_w; ++it) {
-    process(cur);
+  // Rounds of 4 sub-tiles (wavefront w's sub-tile of round r is 4 r + w).
+  // Every wavefront runs the same online softmax over the round's 64 slots --
+  // the same scores in the same order, so the same m and l everywhere -- and
+  // accumulates O^T for its own 128 output dims from all 4 tiles: no partials
+  // to merge at the end.  Sub-tiles with no valid slot take no part.
+  const int rounds = (g.nsub + kQWaves - 1) / kQWaves;
+  for (int rd = 0; rd < rounds; ++rd) {
+    score_own(cur, rd < nsub_w);
     cur = nxt;
-    if (it + kQBuf < nsub_w) {
-      rows_issue(sub_of(it + kQBuf), sn, nxt);
-      sn = idx_issue(min(wave + kQWaves * (it + kQBuf + 1), last_sub));
+    if (rd + kQBuf < nsub_w) {
+      rows_issue(sub_of(rd + kQBuf), sn, nxt);
+      sn = idx_issue(min(wave + kQWaves * (rd + kQBuf + 1), last_sub));
     }
+    lds_barrier();  // the round's tiles, scores and slot bits are in LDS
+    uint32_t fl[kQWaves];
+    uint32_t any = 0u;
+#pragma unroll
+    for (int u = 0; u < kQWaves; ++u) {
+      fl[u] = flags[u];
+      any |= fl[u];
+    }
+    if (any != 0u) {  // workgroup-uniform
+      float xr[kQWaves][4];
+      float mt = -INFINITY;
+#pragma unroll
+      for (int u = 0; u < kQWaves; ++u) {
+        const f32x4_t v = fl[u] ? *reinterpret_cast<const f32x4_t*>(xs + (u * kWave + lane) * 4)
+                                : f32x4_t{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          xr[u][e] = v[e];
+          mt = fmaxf(mt, v[e]);
+        }
+      }
+      mt = fmaxf(mt, __uint_as_float(lane_xor<16>(__float_as_uint(mt), lane)));
+      mt = fmaxf(mt, __uint_as_float(lane_xor<32>(__float_as_uint(mt), lane)));
+      // Lazy rescale: the running max m only moves when a score exceeds it by
+      // more than 2^8 (so probabilities stay below 2^8, exact enough in fp32
+      // and as bf16 PV operands) or on the first round with a valid slot; the
+      // output accumulators are rescaled only when some head of the wavefront
+      // moved.
+      const bool move = mt > m + 8.f;  // m = -inf: always
+      const float m_new = move ? mt : m;
+      const float alpha = move ? fast_exp2(m - m_new) : 1.f;
+      float ps = 0.f;
+      i16x4_t pb[kQWaves];
+#pragma unroll
+      for (int u = 0; u < kQWaves; ++u) {
+        float p[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          p[e] = fast_exp2(xr[u][e] - m_new);
+          ps += p[e];
+        }
+        // an empty sub-tile's probabilities are zero (its scores are -inf)
+        pb[u] = __builtin_bit_cast(i16x4_t, make_uint2(bf16x2_nb(p[0], p[1]), bf16x2_nb(p[2], p[3])));
+      }
+      l = l * alpha + ps;
+      m = m_new;
+      if (__any(move)) {
+#pragma unroll
+        for (int j = 0; j < kQOutBlocks; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[j][e] *= alpha;
+      }
+      // An empty sub-tile (no tile written this round) reads the first valid
+      // tile's rows against its zero probabilities: no branch around the
+      // MFMAs (a branch there moves the accumulators out of the registers
+      // the MFMAs keep them in, and back, for every tile).
+      const int first = fl[0] ? 0 : fl[1] ? 1 : fl[2] ? 2 : 3;
+#pragma unroll
+      for (int u = 0; u < kQWaves; ++u) {
+        const uint16_t* vsrc = reinterpret_cast<const uint16_t*>(smem + (fl[u] ? u : first) * kQTileBytes) + vofs;
+        i16x4_t vt[kQOutBlocks];
+#pragma unroll
+        for (int j = 0; j < kQOutBlocks; ++j)
+          vt[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(vsrc + 16 * j));
+#pragma unroll
+        for (int j = 0; j < kQOutBlocks; ++j)
+          o[j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt[j], pb[u], o[j], 0, 0, 0);
+      }
+    }
+    lds_barrier();  // the tiles and scores are rewritten by the next round
   }
   l += __uint_as_float(lane_xor<16>(__float_as_uint(l), lane));
   l += __uint_as_float(lane_xor<32>(__float_as_uint(l), lane));
 
-  // Merge the 4 wavefronts' partials (the merge buffer reuses the tiles).
-  __syncthreads();
-  float* mrg = reinterpret_cast<float*>(smem);
+  // Normalise with the sink as a virtual token of logit sink[h] and value 0
+  // (csrc/dsv4_attention.cu:252-269): M = max(sink, m), L = l 2^(m - M) +
+  // 2^(sink - M), out = O 2^(m - M) / L; a NaN score makes the head NaN, as
+  // torch.softmax does in the oracle.
+  const float sk = g.sink ? sink_raw * kLog2e : -INFINITY;
+  const float mx = l > 0.f ? fmaxf(sk, m) : sk;
+  const float w = (l > 0.f && mx != -INFINITY) ? fast_exp2(m - mx) : 0.f;
+  float L = w * (l > 0.f ? l : 0.f);
+  if (g.sink && mx != -INFINITY) L += fast_exp2(sk - mx);
+  const float sc = l != l ? __builtin_nanf("") : (L > 0.f ? w / L : 0.f);
   if (l16 < nh) {
+    bf16* orow = g.out + (query * a.heads + h0 + l16) * kDim + (kDim / kQWaves) * wave + 4 * grp;
 #pragma unroll
-    for (int j = 0; j < kDim / 16; ++j)
-      *reinterpret_cast<f32x4_t*>(mrg + (wave * kQHeads + l16) * kQOutStride + 16 * j + 4 * grp) = o[j];
-    if (grp == 0) {
-      qml[wave][l16][0] = m;
-      qml[wave][l16][1] = l;
-    }
-  }
-  __syncthreads();
-  // Lane h < 16 forms head h's merge weights (w_j = 2^(m_j - M) for the 4
-  // wavefronts' partials, 1/L with the sink's 2^(sink - M)); every lane then
-  // takes them as scalars (readlane) and merges its 2 dims of the wavefront's
-  // quarter of the output for each head, the partial reads batched 4 heads
-  // at a time.
-  float wj[kQWaves], inv;
-  {
-    const int hh = min(l16, nh - 1);
-    float mj[kQWaves], lj[kQWaves];
-#pragma unroll
-    for (int j = 0; j < kQWaves; ++j) {
-      mj[j] = qml[j][hh][0];
-      lj[j] = qml[j][hh][1];
-    }
-    const float sk = g.sink ? sink_raw * kLog2e : -INFINITY;
-    float mx = sk;
-    bool nan_in = false;  // a NaN/inf score makes the softmax NaN, as torch.softmax does
-#pragma unroll
-    for (int j = 0; j < kQWaves; ++j) {
-      if (lj[j] > 0.f) mx = fmaxf(mx, mj[j]);
-      nan_in = nan_in || lj[j] != lj[j];
-    }
-    float L = 0.f;
-#pragma unroll
-    for (int j = 0; j < kQWaves; ++j) {
-      wj[j] = (lj[j] > 0.f && mx != -INFINITY) ? fast_exp2(mj[j] - mx) : 0.f;
-      L = fmaf(wj[j], lj[j] > 0.f ? lj[j] : 0.f, L);
-    }
-    if (g.sink && mx != -INFINITY) L += fast_exp2(sk - mx);
-    inv = nan_in ? __builtin_nanf("") : (L > 0.f ? 1.f / L : 0.f);
-  }
-  const int d = (kDim / kQWaves) * wave + 2 * lane;
-  bf16* orow = g.out + (query * a.heads + h0) * kDim + d;
-  for (int hb = 0; hb < nh; hb += 4) {
-    float2 v[4][kQWaves];
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-#pragma unroll
-      for (int j = 0; j < kQWaves; ++j)
-        v[u][j] = *reinterpret_cast<const float2*>(mrg + (j * kQHeads + min(hb + u, kQHeads - 1)) * kQOutStride + d);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int h = hb + u;
-      if (h < nh) {
-        float a0 = 0.f, a1 = 0.f;
-#pragma unroll
-        for (int j = 0; j < kQWaves; ++j) {
-          const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wj[j]), h));
-          a0 = fmaf(w, v[u][j].x, a0);
-          a1 = fmaf(w, v[u][j].y, a1);
-        }
-        const float iv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, inv), h));
-        *reinterpret_cast<uint32_t*>(orow + static_cast<int64_t>(h) * kDim) =
-            static_cast<uint32_t>(float_to_bf16_bits(a0 * iv)) | (static_cast<uint32_t>(float_to_bf16_bits(a1 * iv)) << 16);
-      }
+    for (int j = 0; j < kQOutBlocks; ++j) {
+      *reinterpret_cast<uint2*>(orow + 16 * j) =
+          make_uint2(bf16x2_nb(o[j][0] * sc, o[j][1] * sc), bf16x2_nb(o[j][2] * sc, o[j][3] * sc));
     }
   }
 }
@@ -1431,7 +1426,7 @@ int dsv4_run(const Dsv4Call& c) {
   a.num_tiles = static_cast<int>(tiles);
   a.qscale = static_cast<float>(c.softmax_scale) * kLog2e;
   hipStream_t stream = static_cast<hipStream_t>(c.stream);
-  if (use_mfma && use_query_kernel(c.nq, c.heads, total)) {
+  if (use_mfma && reinterpret_cast<uintptr_t>(c.out) % 8 == 0 && use_query_kernel(c.nq, c.heads, total)) {
     QueryArgs qa;
     qa.nq = c.nq;
     qa.groups = static_cast<int>(ceil_div(c.heads, kQHeads));
