@@ -820,8 +820,9 @@ __global__ __launch_bounds__(kMfmaThreads) void dsv4_mfma_kernel(const bf16* __r
 // b, b + 8, b + 16, ... -- the same XCD (blocks go to XCD blockIdx % 8), so
 // at H = 64 the four workgroups that read a query's rows share one L2.
 //
-// The slot list goes in rounds of 4 sub-tiles of 16 slots (wavefront w takes
-// sub-tile w of each round).  Per round each wavefront
+// The slot list goes in rounds of W sub-tiles of 16 slots (W = 4 or 8
+// wavefronts; wavefront w takes sub-tile w of each round).  Per round each
+// wavefront
 //   * loads its sub-tile's 16 rows (lane l: slot l%16, 16-byte chunks l/16 +
 //     4i of the 576-byte row, and the slot's 8 scale bytes), dequantises the
 //     e4m3 part to bf16 exactly as the reference dequant rounds it, and stores
@@ -831,11 +832,11 @@ __global__ __launch_bounds__(kMfmaThreads) void dsv4_mfma_kernel(const bf16* __r
 //     lane l holds S^T[slot 4(l/16)+e][head l%16], and publishes the masked,
 //     scaled scores in LDS;
 //   * after a barrier, runs the online softmax of head l%16 over the round's
-//     4 sub-tiles (its 4 slots of each and the 3 lanes with the same l%16, row
+//     W sub-tiles (its 4 slots of each and the 3 lanes with the same l%16, row
 //     swaps 16 and 32) -- every wavefront the same, so m and l agree -- with
 //     the bf16-rounded probabilities as the B operand of the PV product;
-//   * accumulates O^T = V^T P^T on v_mfma_f32_16x16x16_bf16 for ITS 128 output
-//     dims (8 blocks of 16) over all 4 tiles; the A operand V^T[dim][slot
+//   * accumulates O^T = V^T P^T on v_mfma_f32_16x16x16_bf16 for ITS 512 / W
+//     output dims (blocks of 16) over all W tiles; the A operand V^T[dim][slot
 //     4g..4g+3] comes straight out of the row-major tiles through
 //     ds_read_b64_tr_b16.  Lane l holds O^T[dim 16 blk + 4(l/16) + e][head
 //     l%16], so the softmax rescale of a lane is its own head's factor.
@@ -856,8 +857,6 @@ __device__ __forceinline__ uint32_t bf16_bits_nb(float x) {
 __device__ __forceinline__ uint32_t bf16x2_nb(float lo, float hi) { return bf16_bits_nb(lo) | (bf16_bits_nb(hi) << 16); }
 
 constexpr int kQSub = 16;                 // slots per sub-tile
-constexpr int kQWaves = 4;
-constexpr int kQThreads = kQWaves * kWave;
 constexpr int kQHeads = 16;
 // LDS tile row: 536 bf16 = 1072 B = 67 16-byte units = 268 dwords (12 mod 64
 // banks).  The dequant's 16-byte stores (16 lanes: slots 0..15 of one column)
@@ -867,15 +866,10 @@ constexpr int kQHeads = 16;
 // conflict-free.
 constexpr int kQRow = kDim + 24;
 constexpr int kQTileBytes = kQSub * kQRow * 2;
-constexpr int kQOutBlocks = kDim / kQWaves / 16;  // 16-dim output blocks per wavefront
-// The 4 tiles, then each wavefront's masked scores (a lane's 4 floats) and
-// its sub-tile's slot bits.
-constexpr int kQSmemBytes = kQWaves * kQTileBytes + kQWaves * kWave * 4 * 4 + kQWaves * 4;
-// Query rows in LDS (the B operand of S^T, shared by the 4 wavefronts): 520
+// Query rows in LDS (the B operand of S^T, shared by the wavefronts): 520
 // bf16 = 1040 B = 260 dwords (4 mod 64 banks), so the 16 heads' 16-byte reads
 // of one lane group cover the 64 banks once.
 constexpr int kQQRow = kDim + 8;
-constexpr int kQQUnits = kQHeads * (kDim / 8) / kQThreads;  // 16-byte query units per thread
 constexpr int kQBuf = 2;                  // sub-tiles of rows in flight per wavefront
 constexpr int kQNopeChunks = kNope / 16;  // 28 chunks of 16 e4m3 bytes
 constexpr int kQChunksPerLane = 9;        // 7 e4m3 chunks + 2 rope chunks
@@ -898,9 +892,16 @@ struct QRows {
   bool ok;
 };
 
-__global__ __launch_bounds__(kQThreads) void dsv4_query_kernel(const bf16* __restrict__ q, Dsv4Args a,
-                                                               QueryArgs g) {
-  __shared__ __align__(16) uint8_t smem[kQSmemBytes];
+template <int W>
+__global__ __launch_bounds__(W * kWave) void dsv4_query_kernel(const bf16* __restrict__ q, Dsv4Args a, QueryArgs g) {
+  constexpr int NT = W * kWave;
+  constexpr int QOB = kDim / W / 16;                    // 16-dim output blocks per wavefront
+  constexpr int QQU = kQHeads * (kDim / 8) / NT;       // 16-byte query units per thread
+  // The W tiles, then each wavefront's masked scores (a lane's 4 floats) and
+  // its sub-tile's slot bits.
+  constexpr int QSM = W * kQTileBytes + W * kWave * 4 * 4 + W * 4;
+  static_assert(QSM + kQHeads * kQQRow * 2 <= 160 * 1024, "LDS of one workgroup");
+  __shared__ __align__(16) uint8_t smem[QSM];
   __shared__ __align__(16) uint16_t qlds[kQHeads * kQQRow];
 
   const int tid = threadIdx.x;
@@ -957,19 +958,19 @@ __global__ __launch_bounds__(kQThreads) void dsv4_query_kernel(const bf16* __res
     rw.sc = load_global_u2(sp);
   };
 
-  const int nsub_w = g.nsub > wave ? (g.nsub - wave + kQWaves - 1) / kQWaves : 0;  // this wave's sub-tiles
+  const int nsub_w = g.nsub > wave ? (g.nsub - wave + W - 1) / W : 0;  // this wave's sub-tiles
   static_assert(kQBuf == 2, "two row buffers below");
   const int last_sub = max(g.nsub - 1, 0);
-  SlotIdx si0 = idx_issue(min(wave, last_sub)), si1 = idx_issue(min(wave + kQWaves, last_sub));
+  SlotIdx si0 = idx_issue(min(wave, last_sub)), si1 = idx_issue(min(wave + W, last_sub));
   // The query rows and the sink go out after the lengths and the first
   // indices, so waiting for those (the rows' addresses) does not wait for them.
-  // Thread t loads the workgroup's 16-byte query units t + 256 u (head e / 64,
+  // Thread t loads the workgroup's 16-byte query units t + 64 W u (head e / 64,
   // dims 8 (e % 64) .. +7; heads past nh re-read head h0 + nh - 1 and are
-  // stored as zeros), staged once in LDS for all 4 wavefronts.
-  uint4 qw[kQQUnits];
+  // stored as zeros), staged once in LDS for all the wavefronts.
+  uint4 qw[QQU];
 #pragma unroll
-  for (int u = 0; u < kQQUnits; ++u) {
-    const int e = tid + kQThreads * u;
+  for (int u = 0; u < QQU; ++u) {
+    const int e = tid + NT * u;
     qw[u] = load_global_u4(q + (query * a.heads + h0 + min(e / (kDim / 8), nh - 1)) * kDim + 8 * (e % (kDim / 8)));
   }
   const int hq = h0 + min(l16, nh - 1);
@@ -979,14 +980,14 @@ __global__ __launch_bounds__(kQThreads) void dsv4_query_kernel(const bf16* __res
   n_extra = a.extra_slots > 0 ? (a.elens ? max(0, min(elen_raw, a.extra_slots)) : a.extra_slots) : 0;
   // Sub-tile t of this wave is global sub-tile wave + 4 t; past the list a
   // buffer is loaded from the dummy row with no valid slot.
-  auto sub_of = [&](int t) { return t < nsub_w ? wave + kQWaves * t : g.nsub; };
+  auto sub_of = [&](int t) { return t < nsub_w ? wave + W * t : g.nsub; };
   QRows cur, nxt;  // rows of this wave's sub-tiles t and t + 1
   rows_issue(sub_of(0), si0, cur);
   rows_issue(sub_of(1), si1, nxt);
-  SlotIdx sn = idx_issue(min(wave + kQWaves * kQBuf, last_sub));  // indices of sub-tile kQBuf
+  SlotIdx sn = idx_issue(min(wave + W * kQBuf, last_sub));  // indices of sub-tile kQBuf
 #pragma unroll
-  for (int u = 0; u < kQQUnits; ++u) {
-    const int e = tid + kQThreads * u;
+  for (int u = 0; u < QQU; ++u) {
+    const int e = tid + NT * u;
     *reinterpret_cast<uint4*>(qlds + (e / (kDim / 8)) * kQQRow + 8 * (e % (kDim / 8))) =
         e / (kDim / 8) < nh ? qw[u] : make_uint4(0u, 0u, 0u, 0u);
   }
@@ -994,15 +995,15 @@ __global__ __launch_bounds__(kQThreads) void dsv4_query_kernel(const bf16* __res
   const uint16_t* qrow = qlds + l16 * kQQRow + 8 * grp;  // B operand: head l16, dims 32 kk + 8 grp ..
 
   uint16_t* tile = reinterpret_cast<uint16_t*>(smem + wave * kQTileBytes);
-  float* xs = reinterpret_cast<float*>(smem + kQWaves * kQTileBytes);  // [wave][lane][4] masked scores
-  uint32_t* flags = reinterpret_cast<uint32_t*>(xs + kQWaves * kWave * 4);  // [wave] valid-slot bits
+  float* xs = reinterpret_cast<float*>(smem + W * kQTileBytes);  // [wave][lane][4] masked scores
+  uint32_t* flags = reinterpret_cast<uint32_t*>(xs + W * kWave * 4);  // [wave] valid-slot bits
   float m = -INFINITY, l = 0.f;  // online softmax of head l16 (this lane's 4 slots of each sub-tile)
-  f32x4_t o[kQOutBlocks];
+  f32x4_t o[QOB];
 #pragma unroll
-  for (int j = 0; j < kQOutBlocks; ++j) o[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < QOB; ++j) o[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   // V^T A operand of output block j (dims 128 wave + 16 j ..) of a tile: lane a
   // of group g passes &V[4g + a/4][128 wave + 16 j + 4(a%4)].
-  const int vofs = (4 * grp + l16 / 4) * kQRow + 4 * (l16 % 4) + (kDim / kQWaves) * wave;
+  const int vofs = (4 * grp + l16 / 4) * kQRow + 4 * (l16 % 4) + (kDim / W) * wave;
 
   // This wavefront's sub-tile of the round: dequantise it into its tile, score
   // it against the 16 heads, publish the masked scores and the slot bits.
@@ -1066,32 +1067,32 @@ __global__ __launch_bounds__(kQThreads) void dsv4_query_kernel(const bf16* __res
     *reinterpret_cast<f32x4_t*>(xs + (wave * kWave + lane) * 4) = x;
   };
 
-  // Rounds of 4 sub-tiles (wavefront w's sub-tile of round r is 4 r + w).
-  // Every wavefront runs the same online softmax over the round's 64 slots --
+  // Rounds of W sub-tiles (wavefront w's sub-tile of round r is W r + w).
+  // Every wavefront runs the same online softmax over the round's 16 W slots --
   // the same scores in the same order, so the same m and l everywhere -- and
-  // accumulates O^T for its own 128 output dims from all 4 tiles: no partials
+  // accumulates O^T for its own 512 / W output dims from all W tiles: no partials
   // to merge at the end.  Sub-tiles with no valid slot take no part.
-  const int rounds = (g.nsub + kQWaves - 1) / kQWaves;
+  const int rounds = (g.nsub + W - 1) / W;
   for (int rd = 0; rd < rounds; ++rd) {
     score_own(cur, rd < nsub_w);
     cur = nxt;
     if (rd + kQBuf < nsub_w) {
       rows_issue(sub_of(rd + kQBuf), sn, nxt);
-      sn = idx_issue(min(wave + kQWaves * (rd + kQBuf + 1), last_sub));
+      sn = idx_issue(min(wave + W * (rd + kQBuf + 1), last_sub));
     }
     lds_barrier();  // the round's tiles, scores and slot bits are in LDS
-    uint32_t fl[kQWaves];
+    uint32_t fl[W];
     uint32_t any = 0u;
 #pragma unroll
-    for (int u = 0; u < kQWaves; ++u) {
+    for (int u = 0; u < W; ++u) {
       fl[u] = flags[u];
       any |= fl[u];
     }
     if (any != 0u) {  // workgroup-uniform
-      float xr[kQWaves][4];
+      float xr[W][4];
       float mt = -INFINITY;
 #pragma unroll
-      for (int u = 0; u < kQWaves; ++u) {
+      for (int u = 0; u < W; ++u) {
         const f32x4_t v = fl[u] ? *reinterpret_cast<const f32x4_t*>(xs + (u * kWave + lane) * 4)
                                 : f32x4_t{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
@@ -1111,9 +1112,9 @@ __global__ __launch_bounds__(kQThreads) void dsv4_query_kernel(const bf16* __res
       const float m_new = move ? mt : m;
       const float alpha = move ? fast_exp2(m - m_new) : 1.f;
       float ps = 0.f;
-      i16x4_t pb[kQWaves];
+      i16x4_t pb[W];
 #pragma unroll
-      for (int u = 0; u < kQWaves; ++u) {
+      for (int u = 0; u < W; ++u) {
         float p[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -1127,7 +1128,7 @@ __global__ __launch_bounds__(kQThreads) void dsv4_query_kernel(const bf16* __res
       m = m_new;
       if (__any(move)) {
 #pragma unroll
-        for (int j = 0; j < kQOutBlocks; ++j)
+        for (int j = 0; j < QOB; ++j)
 #pragma unroll
           for (int e = 0; e < 4; ++e) o[j][e] *= alpha;
       }
@@ -1135,16 +1136,18 @@ __global__ __launch_bounds__(kQThreads) void dsv4_query_kernel(const bf16* __res
       // tile's rows against its zero probabilities: no branch around the
       // MFMAs (a branch there moves the accumulators out of the registers
       // the MFMAs keep them in, and back, for every tile).
-      const int first = fl[0] ? 0 : fl[1] ? 1 : fl[2] ? 2 : 3;
+      int first = W - 1;
 #pragma unroll
-      for (int u = 0; u < kQWaves; ++u) {
+      for (int u = W - 1; u >= 0; --u) first = fl[u] ? u : first;
+#pragma unroll
+      for (int u = 0; u < W; ++u) {
         const uint16_t* vsrc = reinterpret_cast<const uint16_t*>(smem + (fl[u] ? u : first) * kQTileBytes) + vofs;
-        i16x4_t vt[kQOutBlocks];
+        i16x4_t vt[QOB];
 #pragma unroll
-        for (int j = 0; j < kQOutBlocks; ++j)
+        for (int j = 0; j < QOB; ++j)
           vt[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(vsrc + 16 * j));
 #pragma unroll
-        for (int j = 0; j < kQOutBlocks; ++j)
+        for (int j = 0; j < QOB; ++j)
           o[j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt[j], pb[u], o[j], 0, 0, 0);
       }
     }
@@ -1164,9 +1167,9 @@ __global__ __launch_bounds__(kQThreads) void dsv4_query_kernel(const bf16* __res
   if (g.sink && mx != -INFINITY) L += fast_exp2(sk - mx);
   const float sc = l != l ? __builtin_nanf("") : (L > 0.f ? w / L : 0.f);
   if (l16 < nh) {
-    bf16* orow = g.out + (query * a.heads + h0 + l16) * kDim + (kDim / kQWaves) * wave + 4 * grp;
+    bf16* orow = g.out + (query * a.heads + h0 + l16) * kDim + (kDim / W) * wave + 4 * grp;
 #pragma unroll
-    for (int j = 0; j < kQOutBlocks; ++j) {
+    for (int j = 0; j < QOB; ++j) {
       *reinterpret_cast<uint2*>(orow + 16 * j) =
           make_uint2(bf16x2_nb(o[j][0] * sc, o[j][1] * sc), bf16x2_nb(o[j][2] * sc, o[j][3] * sc));
     }
@@ -1364,6 +1367,18 @@ bool use_query_kernel(int64_t nq, int64_t heads, int64_t total_slots) {
   return nq * groups >= 64;
 }
 
+// Wavefronts per workgroup of the per-query kernel (4 or 8; a round covers
+// that many 16-slot sub-tiles): 8 where the slot list fits one round of 8
+// (measured per launch, per-query kernel at nq 1-32 x H 8-64: the 128-slot
+// SWA window 7-11% faster than two rounds of 4), else 4 (192 slots: two
+// rounds of 8, the second half empty, are no faster than three of 4).
+// CSAHCA_DSV4_QWAVES=4/8 forces either.
+int query_waves(int64_t total_slots) {
+  const char* e = std::getenv("CSAHCA_DSV4_QWAVES");
+  if (e && (e[0] == '4' || e[0] == '8') && e[1] == 0) return e[0] - '0';
+  return total_slots <= 8 * kQSub ? 8 : 4;
+}
+
 struct Dsv4Call {
   const void* q;
   int dtype;
@@ -1435,7 +1450,10 @@ int dsv4_run(const Dsv4Call& c) {
     qa.out = static_cast<bf16*>(c.out);
     const int64_t blocks = ceil_div(c.nq, 8) * 8 * qa.groups;  // query q's groups: blocks q%8 + 8 (g + G q/8)
     CSAHCA_REQUIRE(blocks <= INT32_MAX, "too many DSV4 work items");
-    return launch("dsv4_query_kernel", dsv4_query_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(kQThreads), 0,
+    if (query_waves(total) == 8)
+      return launch("dsv4_query_kernel", dsv4_query_kernel<8>, dim3(static_cast<uint32_t>(blocks)), dim3(8 * kWave), 0,
+                    stream, static_cast<const bf16*>(c.q), a, qa);
+    return launch("dsv4_query_kernel", dsv4_query_kernel<4>, dim3(static_cast<uint32_t>(blocks)), dim3(4 * kWave), 0,
                   stream, static_cast<const bf16*>(c.q), a, qa);
   }
   if (use_mfma) {

@@ -228,6 +228,26 @@ def test_query_kernel_matches_split_kernel_and_oracle(ratio, nq, heads, top_k, e
             assert_close(gpu_out(c, sink=sink), ref, what=f"query={route} sink={sink}")
 
 
+@pytest.mark.parametrize("ratio,nq,heads,top_k,extra_top_k", [
+    (0, 1, 8, 128, 0),     # one round of 8 sub-tiles, two of 4
+    (4, 3, 24, 96, 40),    # 9 sub-tiles: two rounds of 8 (the second nearly empty), three of 4
+    (0, 2, 16, 600, 0),    # 38 sub-tiles
+])
+@pytest.mark.parametrize("waves", ["4", "8"])
+def test_query_kernel_wavefront_counts(ratio, nq, heads, top_k, extra_top_k, waves, monkeypatch):
+    """The per-query kernel with 4 and with 8 wavefronts per workgroup
+    (CSAHCA_DSV4_QWAVES) against the oracle, with ragged lengths and a -1 slot."""
+    page = 256 if ratio == 128 else 64
+    c = make_dsv4_case(compress_ratio=ratio, num_queries=nq, heads=heads, num_tokens=1024, top_k=top_k,
+                       page_size=page, extra_tokens=1024, extra_top_k=extra_top_k, seed=7 + heads + top_k,
+                       device=DEV)
+    c.token_indices[0, min(5, top_k - 1)] = -1
+    monkeypatch.setenv("CSAHCA_DSV4_QUERY", "1")
+    monkeypatch.setenv("CSAHCA_DSV4_QWAVES", waves)
+    for sink in (True, False):
+        assert_close(gpu_out(c, sink=sink), oracle_out(c, sink=sink), what=f"waves={waves} sink={sink}")
+
+
 @pytest.mark.parametrize("route", ["1", "0"])
 def test_scale_byte_255_gives_nan_like_the_reference(route, monkeypatch):
     """A scale byte of 255 is 2^128 = inf in the reference's fp32 dequant, so
