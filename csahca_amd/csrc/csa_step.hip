@@ -17,7 +17,7 @@
 //      head gathers the P partials and merges them (log-sum-exp) into the
 //      output.
 // With P == 1 a workgroup owns its head and nothing crosses workgroups; the
-// wide instantiation (16 wavefronts, P == 1) serves grids of about one head
+// wide instantiation (8 wavefronts, P == 1) serves grids of about one head
 // per CU with large selections.
 //
 // Cross-workgroup exchange without cache maintenance: on gfx950 an agent-scope
@@ -146,7 +146,7 @@ __device__ __forceinline__ uint32_t wait_tagged(const uint64_t* p, uint64_t w, u
 
 // PIPE: walk several batches of rows double-buffered (an instantiation of its
 // own, so the batch-by-batch kernel keeps its code).  W: wavefronts per
-// workgroup (the wide instantiation serves a head from one workgroup of 16).
+// workgroup (the wide instantiation serves a head from one workgroup of 8).
 template <typename T, int D, int TOPK_M, bool POS, bool PIPE = false, int W = kStepWaves>
 __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
   constexpr int NT = W * kWave;
@@ -703,8 +703,9 @@ StepKernelFn step_kernel_pipelined(int dtype, int64_t head_dim, int m) {
 // The wide instantiation: a head's whole step in one workgroup of
 // kWideWaves wavefronts (P = 1, so nothing crosses workgroups), its summary and
 // K/V batches double-buffered.  bf16/f16, head_dim 128, count modes; nullptr
-// elsewhere.
-constexpr int kWideWaves = 16;
+// elsewhere.  (8 wavefronts: at 256 heads with top-32 selections 1-4% faster
+// than 16, whose extra loads in flight one CU cannot return any faster.)
+constexpr int kWideWaves = 8;
 StepKernelFn step_kernel_wide(int dtype, int64_t head_dim, int m) {
   if (head_dim != 128) return nullptr;
   if (dtype == CSAHCA_BF16)
@@ -837,11 +838,11 @@ int decode_step_impl(const void* q, const void* k_cache, const void* v_cache, co
                         16) == 0;
   const bool fused_dtype = dtype == CSAHCA_BF16 || dtype == CSAHCA_F16 || dtype == CSAHCA_F32;
   const bool fused_dim = head_dim == 64 || head_dim == 128 || head_dim == 256;
-  // One wide workgroup (16 wavefronts) per head where the grid holds about one
+  // One wide workgroup (8 wavefronts) per head where the grid holds about one
   // head per CU and a head selects more than 1024 rows: there the split kernel
-  // would take P = 2 and its exchange, while 16 wavefronts keep more of the
+  // would take P = 2 and its exchange, while 8 wavefronts keep more of the
   // head's loads in flight (measured at 256 heads, top-32 of 64-token chunks:
-  // 2.5-5% faster).  With fewer heads the split kernel is faster: one CU
+  // 3-5% faster).  With fewer heads the split kernel is faster: one CU
   // returns about 64 B per clock to its wavefronts, so a head read through
   // one CU takes ~4 us per 256 KiB, where P workgroups share it.
   const int wide_env = env_step_wide();

@@ -342,20 +342,20 @@ def test_fused_step_matches_oracle_and_two_pass(B, H, S, D, chunk, k, dtype):
 
 
 WIDE = [
-    # B, H, S, D, chunk, k, dtype: the 16-wavefront instantiation forced
-    # (CSAHCA_STEP_WIDE=1); phase A batches of 256 summary rows, phase C of 256
-    # selected rows
-    (1, 8, 32768, 128, 64, 8, torch.bfloat16),   # 512 chunks, 512 rows: two double-buffered batches each
-    (4, 8, 8192, 128, 48, 7, torch.float16),     # 170 chunks (one batch), 336 rows (ragged second batch)
-    (2, 4, 16384, 128, 64, 40, torch.bfloat16),  # 256 chunks, 2560 rows: ten batches of attention
-    (1, 2, 99968, 128, 64, 8, torch.bfloat16),   # 1562 chunks: seven batches, the last ragged
-    (32, 8, 2048, 128, 64, 20, torch.bfloat16),  # 256 heads, 1280 rows: the default rule's own choice
+    # B, H, S, D, chunk, k, dtype: the 8-wavefront instantiation forced
+    # (CSAHCA_STEP_WIDE=1); phase A batches of 128 summary rows, phase C of 128
+    # selected rows, double-buffered
+    (1, 8, 32768, 128, 64, 8, torch.bfloat16),   # 512 chunks, 512 rows: four batches each
+    (4, 8, 8192, 128, 48, 7, torch.float16),     # 170 chunks, 336 rows: ragged last batches
+    (2, 4, 16384, 128, 64, 40, torch.bfloat16),  # 256 chunks, 2560 rows: twenty batches of attention
+    (1, 2, 99968, 128, 64, 8, torch.bfloat16),   # 1562 chunks: thirteen batches, the last ragged
+    (32, 8, 2048, 128, 64, 20, torch.bfloat16),  # 256 heads, 32 chunks (one short batch), 1280 rows: the default rule's choice
 ]
 
 
 @pytest.mark.parametrize("B,H,S,D,chunk,k,dtype", WIDE)
 def test_wide_step_matches_oracle_and_split_step(B, H, S, D, chunk, k, dtype, monkeypatch):
-    """One workgroup of 16 wavefronts per head against the oracle (ids bit-exact
+    """One workgroup of 8 wavefronts per head against the oracle (ids bit-exact
     up to 1e-5 score ties, outputs within the bf16 bar) and against the split
     kernel on the same inputs (identical ids)."""
     g = torch.Generator().manual_seed(B * 5 + H + k + S // 1024)
