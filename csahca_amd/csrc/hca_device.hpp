@@ -9,7 +9,11 @@ namespace csahca {
 
 constexpr int kHcaThreads = 256;
 
-constexpr int kRowBatch = 8;          // rows of K and V in flight per thread
+// Rows of K and V in flight per thread (4: 128 B of loads per lane.  Measured
+// chunk pass, chunk 256, D 128: B1 H8 S32768 level with 8 at 0.68-0.69 of 8
+// TB/s; B4 0.71 against 0.68 for 8 and 0.64 for 16 -- more bytes in flight per
+// lane than the memory system drains only queue.)
+constexpr int kRowBatch = 4;
 
 template <typename T>
 __device__ __forceinline__ float round_to(float x) {
