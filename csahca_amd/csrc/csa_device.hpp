@@ -289,23 +289,25 @@ struct AttendLayout {
 
 // Column sums of `chunk` consecutive [*, D] rows by one wavefront in the
 // AttendLayout split: lane (grp, col) adds rows grp, grp + RPL, ... of its VEC
-// columns at `base` (row 0, column col * VEC), four rows per batch of loads,
-// then the row groups are folded by a butterfly, so every lane ends with the
-// sums of its columns.  The chunk-summary kernel and the fused decode step both
-// build summaries through this one function, so their rows agree bit for bit.
-template <typename T, int D>
+// columns at `base` (row 0, column col * VEC), U rows per batch of loads, then
+// the row groups are folded by a butterfly, so every lane ends with the sums
+// of its columns.  The chunk-summary kernel (U = 16: a 64-row chunk in one
+// batch) and the fused decode step (U = 4, in the few registers it has left)
+// both build summaries through this one function; a lane adds its rows in row
+// order whatever U is, so their rows agree bit for bit.
+template <typename T, int D, int U = 4>
 __device__ __forceinline__ void wave_chunk_colsum(const T* __restrict__ base, int chunk, int grp, float* acc) {
   using L = AttendLayout<T, D>;
   constexpr int VEC = L::VEC, LPR = L::LPR, RPL = L::RPL;
 #pragma unroll
   for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
   int r = grp;
-  for (; r + 3 * RPL < chunk; r += 4 * RPL) {
-    float a[4][VEC];
+  for (; r + (U - 1) * RPL < chunk; r += U * RPL) {
+    float a[U][VEC];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) load16<T>(base + static_cast<int64_t>(r + u * RPL) * D, a[u]);
+    for (int u = 0; u < U; ++u) load16<T>(base + static_cast<int64_t>(r + u * RPL) * D, a[u]);
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
+    for (int u = 0; u < U; ++u)
 #pragma unroll
       for (int e = 0; e < VEC; ++e) acc[e] += a[u][e];
   }
