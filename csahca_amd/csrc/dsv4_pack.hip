@@ -26,21 +26,18 @@ constexpr int kPackScaleBytes = 8;
 constexpr int kPackWaves = 4;          // wavefronts per workgroup
 constexpr int kPackTokensPerWave = 1;  // tokens per wavefront (4 measured slower: 30.6 vs 28.2 us / 65536)
 
-// fp32 -> OCP e4m3fn byte, round to nearest even, for |x| <= 448 (larger
-// magnitudes and NaN give the NaN code).  Normal range: keep 3 mantissa bits of
-// the fp32 encoding with RNE on the 20 dropped bits (a carry moves into the
-// exponent); below 2^-6 the quantum is 2^-9.
-__device__ __forceinline__ uint32_t e4m3fn_rne(float x) {
-  const uint32_t u = __float_as_uint(x);
-  const uint32_t sign = (u >> 24) & 0x80u;
-  const uint32_t a = u & 0x7fffffffu;
-  if (a > 0x7f800000u) return sign | 0x7fu;
-  if (a >= 0x3c800000u) {  // |x| >= 2^-6
-    const uint32_t r = (a + 0x7ffffu + ((a >> 20) & 1u)) >> 20;  // (fp32 exponent << 3) | 3-bit mantissa
-    const uint32_t code = r - (120u << 3);                       // rebias 127 -> 7
-    return sign | (code > 0x7eu ? 0x7fu : code);
-  }
-  return sign | static_cast<uint32_t>(__builtin_rintf(__uint_as_float(a) * 512.0f));
+// Four clamped fp32 values -> four OCP e4m3fn bytes (byte i = value i), round
+// to nearest even, on the gfx950 conversion v_cvt_pk_fp8_f32.  The values this
+// kernel converts are v / 2^E clamped to [-448, 448], v bf16 and 2^E exact:
+// bf16 values in that range, or values that round to +-0.  On all of them the
+// instruction gives the bytes of the integer rounding it replaces (keep 3
+// mantissa bits of the fp32 encoding with RNE on the dropped 20 bits; a
+// quantum of 2^-9 below 2^-6): checked on the device over every bf16 bit
+// pattern and tiny fp32 values, and pinned here by the oracle comparisons of
+// every finite bf16 value in range (tests/test_gpu_dsv4_pack.py).
+__device__ __forceinline__ uint32_t e4m3fn_rne4(float a, float b, float c, float d) {
+  const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true));
 }
 
 // ceil(log2(r)) for a positive finite fp32 r, exactly.
@@ -91,12 +88,10 @@ __device__ __forceinline__ void pack_token(const uint4 w, int64_t loc, int lane,
   const float r = fmaxf(mx, 1e-8f) / 448.0f;
   const int E = ceil_log2(r);
   const float inv = __builtin_ldexpf(1.0f, -E);  // exact: E in [-35, 121] for bf16 inputs
-  uint32_t b[2] = {0u, 0u};
+  float qv[8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float qv = fminf(fmaxf(v[i] * inv, -448.0f), 448.0f);
-    b[i / 4] |= e4m3fn_rne(qv) << (8 * (i % 4));
-  }
+  for (int i = 0; i < 8; ++i) qv[i] = fminf(fmaxf(v[i] * inv, -448.0f), 448.0f);
+  const uint32_t b[2] = {e4m3fn_rne4(qv[0], qv[1], qv[2], qv[3]), e4m3fn_rne4(qv[4], qv[5], qv[6], qv[7])};
   uint8_t* dst = row + 8 * lane;
   if (kVec) {
     *reinterpret_cast<uint2*>(dst) = make_uint2(b[0], b[1]);

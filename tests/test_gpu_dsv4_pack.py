@@ -56,6 +56,32 @@ def test_pack_matches_oracle_bit_exact(page_size):
     assert diff.size == 0, f"{diff.size} bytes differ, first at {diff[:8]}"
 
 
+def test_every_bf16_value_in_range_converts_like_the_oracle():
+    """Each 64-value tile holds 448 (so max_abs / 448 = 1, E = 0 and the values
+    are stored unscaled) and 63 of the finite bf16 values with |v| <= 448 --
+    all of them over the tokens, subnormals and both zeros included: every
+    value the e4m3 conversion can meet, bit-exact against the oracle."""
+    vals = (np.arange(65536, dtype=np.uint32) << 16).view(np.float32)
+    vals = vals[np.isfinite(vals) & (np.abs(vals) <= 448.0)]
+    ntiles = -(-vals.size // 63)
+    tiles = np.zeros((ntiles, 64), dtype=np.float32)
+    tiles[:, 0] = 448.0
+    body = np.zeros(ntiles * 63, dtype=np.float32)
+    body[:vals.size] = vals
+    tiles[:, 1:] = body.reshape(ntiles, 63)
+    T = -(-ntiles // 7)
+    nope = np.zeros((T * 7, 64), dtype=np.float32)
+    nope[:ntiles] = tiles
+    x = np.zeros((T, 512), dtype=np.float32)
+    x[:, :448] = nope.reshape(T, 448)
+    x[:, 448:] = np.random.default_rng(5).standard_normal((T, 64))
+    tok = torch.from_numpy(x).to(torch.bfloat16)
+    assert np.array_equal(tok[:, :448].float().numpy(), x[:, :448])  # the values are exact bf16
+    want = oracle.pack_dsv4_cache(tok, page_size=64)
+    got = native.dsv4_pack_tokens(tok.to(DEV), 64)
+    assert np.array_equal(got.cpu().numpy(), np.asarray(want))
+
+
 def test_power_of_two_boundaries_and_rounding_ties():
     # tiles whose max is 448 * 2^k exactly (E = k), one ulp above (E = k + 1), and
     # values on e4m3 rounding ties
