@@ -580,3 +580,41 @@ def test_phase_timeline_tool_runs_the_stamped_build():
     seq = [times[n] for n in names]
     assert all(b >= a for a, b in zip(seq, seq[1:])) and seq[0] > 0
     assert re.search(r"clock \d+ kHz", r.stdout)
+
+
+
+COLOCATE = [
+    # B, H, S, D, chunk, k, dtype: the placement of a head's P workgroups
+    (1, 8, 32768, 128, 64, 8, torch.bfloat16),   # headline: P = 8, one head per XCD
+    (1, 8, 32768, 128, 64, 32, torch.float16),   # 2048 slots
+    (1, 2, 4096, 128, 48, 5, torch.bfloat16),    # 2 heads (not a multiple of 8), ragged split
+    (8, 8, 8192, 128, 64, 8, torch.bfloat16),    # 64 heads
+    (32, 8, 4096, 128, 64, 8, torch.bfloat16),   # 256 heads, P = 2
+    (1, 4, 8192, 64, 64, 8, torch.float16),
+]
+
+
+@pytest.mark.parametrize("B,H,S,D,chunk,k,dtype", COLOCATE)
+def test_colocated_workgroups_give_the_same_bits(B, H, S, D, chunk, k, dtype, monkeypatch):
+    """Block b serving head b % (B*H) (a head's workgroups on one XCD,
+    CSAHCA_STEP_COLOCATE=1) or head b / P (=0) changes only where each
+    (head, workgroup) runs: ids and outputs are identical, and both match the
+    oracle."""
+    g = torch.Generator().manual_seed(B * 11 + H + k + S // 1024)
+    q = torch.randn(B, H, D, generator=g).to(dtype)
+    kc = torch.randn(B, H, S, D, generator=g).to(dtype)
+    vc = torch.randn(B, H, S, D, generator=g).to(dtype)
+    qd, kd, vd = q.to(DEV), kc.to(DEV), vc.to(DEV)
+    summ = extension.csa_chunk_summary(kd, chunk)
+    outs = {}
+    for colo in ("1", "0"):
+        monkeypatch.setenv("CSAHCA_STEP_COLOCATE", colo)
+        outs[colo] = native.csa_decode_step(qd, kd, vd, summ, chunk, k)
+    assert torch.equal(outs["1"][1], outs["0"][1])
+    assert torch.equal(outs["1"][0], outs["0"][0])
+    want, scores = oracle.select_topk(q, summ.cpu(), k)
+    assert_indices(outs["1"][1], want, scores)
+    atol, rtol = tol_for(dtype)
+    ref = oracle.csa_attend(q, kc, vc, outs["1"][1].cpu(), chunk, prob_dtype=oracle.F32)
+    assert_close(outs["1"][0], ref, atol, rtol, "colocated")
+    assert all(v == 0 for v in native.csa_step_status().values())
