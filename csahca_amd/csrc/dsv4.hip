@@ -892,10 +892,14 @@ struct QRows {
   bool ok;
 };
 
-template <int W>
+// DS: workgroups per (query, 16 heads), each writing kDim / DS of the output
+// dims (every one of them dequantises and scores the whole slot list; the
+// PV products are split).  The DS workgroups of a query share its XCD.
+template <int W, int DS = 1>
 __global__ __launch_bounds__(W * kWave) void dsv4_query_kernel(const bf16* __restrict__ q, Dsv4Args a, QueryArgs g) {
   constexpr int NT = W * kWave;
-  constexpr int QOB = kDim / W / 16;                    // 16-dim output blocks per wavefront
+  constexpr int DW = kDim / DS;                         // output dims of this workgroup
+  constexpr int QOB = DW / W / 16;                      // 16-dim output blocks per wavefront
   constexpr int QQU = kQHeads * (kDim / 8) / NT;       // 16-byte query units per thread
   // The W tiles, then each wavefront's masked scores (a lane's 4 floats) and
   // its sub-tile's slot bits.
@@ -911,8 +915,11 @@ __global__ __launch_bounds__(W * kWave) void dsv4_query_kernel(const bf16* __res
   const int l16 = lane % 16;
   const uint32_t blk = blockIdx.x;
   const uint32_t r = blk / 8;
-  const int hg = static_cast<int>(r % static_cast<uint32_t>(g.groups));
-  const int64_t query = static_cast<int64_t>(r / static_cast<uint32_t>(g.groups)) * 8 + blk % 8;
+  const uint32_t gx = static_cast<uint32_t>(g.groups) * DS;  // (head group, dim part) pairs of a query
+  const uint32_t hgx = r % gx;
+  const int hg = static_cast<int>(hgx / DS);
+  const int part = static_cast<int>(hgx % DS);
+  const int64_t query = static_cast<int64_t>(r / gx) * 8 + blk % 8;
   if (query >= g.nq) return;
   const int h0 = hg * kQHeads;
   const int nh = min(kQHeads, a.heads - h0);
@@ -1003,7 +1010,7 @@ __global__ __launch_bounds__(W * kWave) void dsv4_query_kernel(const bf16* __res
   for (int j = 0; j < QOB; ++j) o[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   // V^T A operand of output block j (dims 128 wave + 16 j ..) of a tile: lane a
   // of group g passes &V[4g + a/4][128 wave + 16 j + 4(a%4)].
-  const int vofs = (4 * grp + l16 / 4) * kQRow + 4 * (l16 % 4) + (kDim / W) * wave;
+  const int vofs = (4 * grp + l16 / 4) * kQRow + 4 * (l16 % 4) + DW * part + (DW / W) * wave;
 
   // This wavefront's sub-tile of the round: dequantise it into its tile, score
   // it against the 16 heads, publish the masked scores and the slot bits.
@@ -1167,7 +1174,7 @@ __global__ __launch_bounds__(W * kWave) void dsv4_query_kernel(const bf16* __res
   if (g.sink && mx != -INFINITY) L += fast_exp2(sk - mx);
   const float sc = l != l ? __builtin_nanf("") : (L > 0.f ? w / L : 0.f);
   if (l16 < nh) {
-    bf16* orow = g.out + (query * a.heads + h0 + l16) * kDim + (kDim / W) * wave + 4 * grp;
+    bf16* orow = g.out + (query * a.heads + h0 + l16) * kDim + DW * part + (DW / W) * wave + 4 * grp;
 #pragma unroll
     for (int j = 0; j < QOB; ++j) {
       *reinterpret_cast<uint2*>(orow + 16 * j) =
@@ -1353,18 +1360,19 @@ bool mfma_enabled() {
 }
 
 // The per-query kernel takes a call when there are at least 64 (query, head
-// group) workgroups: each latent row is then fetched once per query and no
-// partial leaves the CU.  With fewer, one workgroup's sequential sub-tiles
-// (about 3 us each) outweigh that, and the split kernel + merge, whose splits
-// spread a query over many CUs, is faster (measured: nq 32 x H 64 15.2-18.7 us
-// per call against 18.3-21.4; nq 1 and nq 32 x H 8 8.9-11 us against 12-16).
+// group) workgroups (measured per call, nq 32 x H 64: 13.5-13.6 us with two
+// workgroups per (query, 16 heads) against 18.3-21.4 for the split kernel and
+// its merge), or when the slot list is one round of 8 sub-tiles but more than
+// one split tile (33-128 slots: no merge launch; the 128-slot window at nq 1
+// and at nq 32 x H 8: 8.7-9.1 us against 8.8-9.8).  Longer lists at fewer
+// workgroups stay on the split kernel (12 sub-tiles at nq 1: 12.1-12.7 us
+// per-query against 8.8-9.5 split).
 // CSAHCA_DSV4_QUERY=0 / =1 forces the choice (read per call).
 bool use_query_kernel(int64_t nq, int64_t heads, int64_t total_slots) {
   const char* e = std::getenv("CSAHCA_DSV4_QUERY");
   if (e && (e[0] == '0' || e[0] == '1')) return e[0] == '1';
-  (void)total_slots;
   const int64_t groups = ceil_div(std::max<int64_t>(1, heads), kQHeads);
-  return nq * groups >= 64;
+  return nq * groups >= 64 || (total_slots > kMfmaSlots && total_slots <= 8 * kQSub);
 }
 
 // Wavefronts per workgroup of the per-query kernel (4 or 8; a round covers
@@ -1377,6 +1385,16 @@ int query_waves(int64_t total_slots) {
   const char* e = std::getenv("CSAHCA_DSV4_QWAVES");
   if (e && (e[0] == '4' || e[0] == '8') && e[1] == 0) return e[0] - '0';
   return total_slots <= 8 * kQSub ? 8 : 4;
+}
+
+// Workgroups per (query, 16 heads) of the per-query kernel: 2 (each writing
+// half the output dims) where twice the workgroups still fit one per CU,
+// else 1.  CSAHCA_DSV4_QPARTS=1/2 forces either.
+int query_dim_parts(int64_t nq, int64_t groups) {
+  const char* e = std::getenv("CSAHCA_DSV4_QPARTS");
+  if (e && (e[0] == '1' || e[0] == '2') && e[1] == 0) return e[0] - '0';
+  const int ncu = device_cu_count();
+  return ncu > 0 && 2 * ceil_div(nq, 8) * 8 * groups <= ncu ? 2 : 1;
 }
 
 struct Dsv4Call {
@@ -1448,12 +1466,14 @@ int dsv4_run(const Dsv4Call& c) {
     qa.nsub = static_cast<int>(ceil_div(total, kQSub));
     qa.sink = c.sink;
     qa.out = static_cast<bf16*>(c.out);
-    const int64_t blocks = ceil_div(c.nq, 8) * 8 * qa.groups;  // query q's groups: blocks q%8 + 8 (g + G q/8)
+    const int ds = query_dim_parts(c.nq, qa.groups);
+    // query q's (group, part) pairs x: blocks q%8 + 8 (x + G DS q/8)
+    const int64_t blocks = ceil_div(c.nq, 8) * 8 * qa.groups * ds;
     CSAHCA_REQUIRE(blocks <= INT32_MAX, "too many DSV4 work items");
-    if (query_waves(total) == 8)
-      return launch("dsv4_query_kernel", dsv4_query_kernel<8>, dim3(static_cast<uint32_t>(blocks)), dim3(8 * kWave), 0,
-                    stream, static_cast<const bf16*>(c.q), a, qa);
-    return launch("dsv4_query_kernel", dsv4_query_kernel<4>, dim3(static_cast<uint32_t>(blocks)), dim3(4 * kWave), 0,
+    const bool w8 = query_waves(total) == 8;
+    auto kfn = w8 ? (ds == 2 ? dsv4_query_kernel<8, 2> : dsv4_query_kernel<8, 1>)
+                  : (ds == 2 ? dsv4_query_kernel<4, 2> : dsv4_query_kernel<4, 1>);
+    return launch("dsv4_query_kernel", kfn, dim3(static_cast<uint32_t>(blocks)), dim3((w8 ? 8 : 4) * kWave), 0,
                   stream, static_cast<const bf16*>(c.q), a, qa);
   }
   if (use_mfma) {

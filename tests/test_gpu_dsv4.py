@@ -234,9 +234,12 @@ def test_query_kernel_matches_split_kernel_and_oracle(ratio, nq, heads, top_k, e
     (0, 2, 16, 600, 0),    # 38 sub-tiles
 ])
 @pytest.mark.parametrize("waves", ["4", "8"])
-def test_query_kernel_wavefront_counts(ratio, nq, heads, top_k, extra_top_k, waves, monkeypatch):
+@pytest.mark.parametrize("parts", ["1", "2"])
+def test_query_kernel_wavefront_counts(ratio, nq, heads, top_k, extra_top_k, waves, parts, monkeypatch):
     """The per-query kernel with 4 and with 8 wavefronts per workgroup
-    (CSAHCA_DSV4_QWAVES) against the oracle, with ragged lengths and a -1 slot."""
+    (CSAHCA_DSV4_QWAVES), and with one or two workgroups per (query, 16 heads)
+    each writing its share of the output dims (CSAHCA_DSV4_QPARTS), against
+    the oracle, with ragged lengths and a -1 slot."""
     page = 256 if ratio == 128 else 64
     c = make_dsv4_case(compress_ratio=ratio, num_queries=nq, heads=heads, num_tokens=1024, top_k=top_k,
                        page_size=page, extra_tokens=1024, extra_top_k=extra_top_k, seed=7 + heads + top_k,
@@ -244,8 +247,32 @@ def test_query_kernel_wavefront_counts(ratio, nq, heads, top_k, extra_top_k, wav
     c.token_indices[0, min(5, top_k - 1)] = -1
     monkeypatch.setenv("CSAHCA_DSV4_QUERY", "1")
     monkeypatch.setenv("CSAHCA_DSV4_QWAVES", waves)
+    monkeypatch.setenv("CSAHCA_DSV4_QPARTS", parts)
     for sink in (True, False):
-        assert_close(gpu_out(c, sink=sink), oracle_out(c, sink=sink), what=f"waves={waves} sink={sink}")
+        assert_close(gpu_out(c, sink=sink), oracle_out(c, sink=sink), what=f"waves={waves} parts={parts} sink={sink}")
+
+
+@pytest.mark.parametrize("ratio,nq,heads,top_k,extra_top_k", [
+    (4, 7, 70, 96, 40),     # 5 head groups (the last with 6 heads), 7 queries
+    (128, 32, 64, 64, 64),  # the benchmark's grouped-head shape class
+    (0, 9, 16, 128, 0),     # 9 queries: the grid's XCD mapping wraps
+])
+def test_query_kernel_dim_parts_give_the_same_bits(ratio, nq, heads, top_k, extra_top_k, monkeypatch):
+    """Two workgroups per (query, 16 heads), each writing half the output dims,
+    run every output block's MFMA chain exactly as one workgroup does: the
+    outputs are identical to the one-workgroup launch."""
+    page = 256 if ratio == 128 else 64
+    c = make_dsv4_case(compress_ratio=ratio, num_queries=nq, heads=heads, num_tokens=1024, top_k=top_k,
+                       page_size=page, extra_tokens=1024, extra_top_k=extra_top_k, seed=3 + nq + heads,
+                       device=DEV)
+    c.token_indices[0, 3] = -1
+    monkeypatch.setenv("CSAHCA_DSV4_QUERY", "1")
+    outs = {}
+    for parts in ("1", "2"):
+        monkeypatch.setenv("CSAHCA_DSV4_QPARTS", parts)
+        outs[parts] = gpu_out(c, sink=True)
+    assert torch.equal(outs["1"], outs["2"])
+    assert_close(outs["2"], oracle_out(c, sink=True), what="parts=2")
 
 
 @pytest.mark.parametrize("route", ["1", "0"])
