@@ -1387,14 +1387,16 @@ int query_waves(int64_t total_slots) {
   return total_slots <= 8 * kQSub ? 8 : 4;
 }
 
-// Workgroups per (query, 16 heads) of the per-query kernel: 2 (each writing
-// half the output dims) where twice the workgroups still fit one per CU,
-// else 1.  CSAHCA_DSV4_QPARTS=1/2 forces either.
+// Workgroups per (query, 16 heads) of the per-query kernel, each writing its
+// share of the output dims: the most of 4, 2 and 1 at which the workgroups
+// still fit one per CU.  CSAHCA_DSV4_QPARTS=1/2/4 forces a count.
 int query_dim_parts(int64_t nq, int64_t groups) {
   const char* e = std::getenv("CSAHCA_DSV4_QPARTS");
-  if (e && (e[0] == '1' || e[0] == '2') && e[1] == 0) return e[0] - '0';
+  if (e && (e[0] == '1' || e[0] == '2' || e[0] == '4') && e[1] == 0) return e[0] - '0';
   const int ncu = device_cu_count();
-  return ncu > 0 && 2 * ceil_div(nq, 8) * 8 * groups <= ncu ? 2 : 1;
+  const int64_t base = ceil_div(nq, 8) * 8 * groups;
+  if (ncu <= 0) return 1;
+  return 4 * base <= ncu ? 4 : 2 * base <= ncu ? 2 : 1;
 }
 
 struct Dsv4Call {
@@ -1471,8 +1473,8 @@ int dsv4_run(const Dsv4Call& c) {
     const int64_t blocks = ceil_div(c.nq, 8) * 8 * qa.groups * ds;
     CSAHCA_REQUIRE(blocks <= INT32_MAX, "too many DSV4 work items");
     const bool w8 = query_waves(total) == 8;
-    auto kfn = w8 ? (ds == 2 ? dsv4_query_kernel<8, 2> : dsv4_query_kernel<8, 1>)
-                  : (ds == 2 ? dsv4_query_kernel<4, 2> : dsv4_query_kernel<4, 1>);
+    auto kfn = w8 ? (ds == 4 ? dsv4_query_kernel<8, 4> : ds == 2 ? dsv4_query_kernel<8, 2> : dsv4_query_kernel<8, 1>)
+                  : (ds == 4 ? dsv4_query_kernel<4, 4> : ds == 2 ? dsv4_query_kernel<4, 2> : dsv4_query_kernel<4, 1>);
     return launch("dsv4_query_kernel", kfn, dim3(static_cast<uint32_t>(blocks)), dim3((w8 ? 8 : 4) * kWave), 0,
                   stream, static_cast<const bf16*>(c.q), a, qa);
   }

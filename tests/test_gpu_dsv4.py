@@ -234,7 +234,7 @@ def test_query_kernel_matches_split_kernel_and_oracle(ratio, nq, heads, top_k, e
     (0, 2, 16, 600, 0),    # 38 sub-tiles
 ])
 @pytest.mark.parametrize("waves", ["4", "8"])
-@pytest.mark.parametrize("parts", ["1", "2"])
+@pytest.mark.parametrize("parts", ["1", "2", "4"])
 def test_query_kernel_wavefront_counts(ratio, nq, heads, top_k, extra_top_k, waves, parts, monkeypatch):
     """The per-query kernel with 4 and with 8 wavefronts per workgroup
     (CSAHCA_DSV4_QWAVES), and with one or two workgroups per (query, 16 heads)
@@ -268,11 +268,12 @@ def test_query_kernel_dim_parts_give_the_same_bits(ratio, nq, heads, top_k, extr
     c.token_indices[0, 3] = -1
     monkeypatch.setenv("CSAHCA_DSV4_QUERY", "1")
     outs = {}
-    for parts in ("1", "2"):
+    for parts in ("1", "2", "4"):
         monkeypatch.setenv("CSAHCA_DSV4_QPARTS", parts)
         outs[parts] = gpu_out(c, sink=True)
     assert torch.equal(outs["1"], outs["2"])
-    assert_close(outs["2"], oracle_out(c, sink=True), what="parts=2")
+    assert torch.equal(outs["1"], outs["4"])
+    assert_close(outs["4"], oracle_out(c, sink=True), what="parts=4")
 
 
 @pytest.mark.parametrize("route", ["1", "0"])
