@@ -69,11 +69,12 @@ def parse_args():
     ap.add_argument("--no-hca", action="store_true")
     ap.add_argument("--no-block", action="store_true")
     ap.add_argument("--no-large-batch", action="store_true")
-    ap.add_argument("--no-sweep-subset", action="store_true")
+    ap.add_argument("--no-sweep", "--no-sweep-subset", dest="no_sweep_subset", action="store_true",
+                    help="leave out the config-2 grid (B {1,8,32} x S {8K,32K,128K} x k {8,32}, iid, "
+                         "planted-scattered and planted-clustered keys), which the line carries as 'sweep'")
     ap.add_argument("--sweep", action="store_true",
-                    help="also run the whole batch x context x top-k sweep: B {1,8,32} x S {8K,32K,128K} x k {8,32}, "
-                         "iid, planted-scattered and planted-clustered keys (rows on stderr; --sweep-out FILE "
-                         "also writes them as JSON)")
+                    help="run the config-2 grid even with --no-sweep (rows on stderr; --sweep-out FILE also "
+                         "writes them as JSON)")
     ap.add_argument("--sweep-out", type=Path, default=None)
     ap.add_argument("--dsv4-case", default=None, metavar="cR_nqN_hH",
                     help="run only this DSV4 case (e.g. c4_nq32_h64), --steps eager calls over 16 rotated caches, "
@@ -323,6 +324,40 @@ def csa_bench(args, B=1, H=8, S=32768, D=128, chunk=64, top_k=8, copies=None, se
     return res
 
 
+STEP_KERNEL_SOURCES = ("csa_step.hip", "csa_device.hpp", "common.hpp", "hca_device.hpp")
+
+
+def step_kernel_sources_sha256() -> str:
+    """sha256 over the decode-step kernel's sources (csahca_amd/csrc), in the
+    order of STEP_KERNEL_SOURCES."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for name in STEP_KERNEL_SOURCES:
+        h.update((ROOT / "csahca_amd" / "csrc" / name).read_bytes())
+    return h.hexdigest()
+
+
+def step_traffic_record():
+    """(HBM bytes per launch of csa_step_kernel, note) from profiles/traffic.json:
+    the scaled FETCH_SIZE + WRITE_SIZE of a rocprofv3 --pmc run of the headline
+    leg (profiles/csa_step_kernel_B1H8S32768k8_traffic.md), which no bench run
+    can measure from inside.  The record names the sha256 of the kernel
+    sources it was measured on; when they differ from this tree's, the figure
+    is stale and the line carries null."""
+    tfile = ROOT / "profiles" / "traffic.json"
+    try:
+        rec = json.loads(tfile.read_text())["csa_step_kernel"]
+    except (OSError, ValueError, KeyError, TypeError):
+        return None, "no traffic record (profiles/traffic.json)"
+    src = rec.get("sources_sha256")
+    if src != step_kernel_sources_sha256():
+        return None, "profiles/traffic.json was measured on other kernel sources; not used"
+    return rec.get("hbm_bytes_per_launch"), (
+        "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes over this leg, scaled by a plain copy's counters "
+        f"({rec.get('source')}); measured on these kernel sources (sha256 {src[:16]})")
+
+
 def kernel_bytes(name, r):
     """Algorithmic HBM bytes per launch of each CSA kernel for workload r."""
     B, H, D, C, k = r["B"], r["H"], r["D"], r["S"] // r["chunk"], min(r["top_k"], r["S"] // r["chunk"])
@@ -345,8 +380,10 @@ def step_flops(r):
     return r["B"] * r["H"] * (2 * r["D"] * C + 4 * r["D"] * min(r["top_k"], C) * r["chunk"])
 
 
-SWEEP_SUBSET = [(B, S, k, v) for B in (8, 32) for S in (32768, 131072) for k in (8, 32)
-                for v in ("iid", "scattered")]
+# Every point of BASELINE config 2: B {1, 8, 32} x S {8K, 32K, 128K} x top-k {8, 32},
+# iid, planted-scattered and planted-clustered keys.
+SWEEP_GRID = [(B, S, k, v) for B in (1, 8, 32) for S in (8192, 32768, 131072) for k in (8, 32)
+              for v in ("iid", "scattered", "clustered")]
 
 
 def sweep_rows(args, points, steps):
@@ -555,6 +592,38 @@ def dsv4_bench(steps=256, copies=64):
                             "roofline": roofline(nbytes, flops, ms, {"time_base": "graph replay period per call, "
                                                                      f"{copies} rotated caches"})}
                 log(f"dsv4 {key}: {out[key]}")
+        del caches, ecaches, c
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    # Independent sequences: every query draws its own slots uniformly over the
+    # pools (as hybrid_attention/dsv4_benchmark.py:40-47,66-73 draws them), so
+    # no two queries share rows -- beside the SWA-window leg above, whose
+    # queries' windows overlap.  Pools of 65,536 SWA tokens (pages of 64) and
+    # 16,384 C4 / 512 C128 entries (pages of 16 / 1); 128 SWA slots and 64
+    # extra slots per query; nq 32.
+    for ratio in (0, 4, 128):
+        c = make_dsv4_bench_case(compress_ratio=ratio, num_queries=32, heads=64, num_tokens=65536, top_k=128,
+                                 page_size=64, extra_tokens=65536 // max(ratio, 1), extra_top_k=64,
+                                 extra_page_size=max(1, 64 // max(ratio, 1)), seed=100 + ratio, device=dev)
+        caches = [c.cache] + [c.cache.clone() for _ in range(copies - 1)]
+        ecaches = ([c.extra_cache] + [c.extra_cache.clone() for _ in range(copies - 1)]) if ratio else None
+        for H in (8, 64):
+            q = c.q[:, :H].contiguous()
+            sink = c.attn_sink[:H].contiguous()
+            ms, ms_eager = _dsv4_time(native, q, caches, c.token_indices, c.topk_lengths, ecaches,
+                                      c.extra_token_indices if ratio else None,
+                                      c.extra_topk_lengths if ratio else None, sink, c.page_size,
+                                      c.extra_page_size if ratio else 1, scale, steps)
+            slots = 128 + (64 if ratio else 0)
+            nq = 32
+            nbytes = nq * slots * 584 + nq * H * 1024 * 2 + nq * slots * 4 + H * 4
+            key = f"c{ratio}_nq32_h{H}_independent_slots"
+            out[key] = {"ms_per_call": round(ms, 5), "ms_per_query": round(ms / nq, 5),
+                        "ms_per_call_eager": round(ms_eager, 5),
+                        "query_heads_per_s": round(nq * H / (ms / 1e3), 1),
+                        "roofline": roofline(nbytes, 2048 * slots * H * nq, ms,
+                                             {"time_base": f"graph replay period per call, {copies} rotated caches"})}
+            log(f"dsv4 {key}: {out[key]}")
         del caches, ecaches, c
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
@@ -969,13 +1038,7 @@ def main():
     ms = r["ms_per_step_eager"] if args.no_graph else r["ms_per_step_graph"]
     kern = r["kernels"]
     log("csa kernels:", json.dumps(kern))
-    traffic = None
-    tfile = ROOT / "profiles" / "traffic.json"
-    if tfile.exists():
-        try:
-            traffic = json.loads(tfile.read_text()).get("csa_step_kernel", {}).get("hbm_bytes_per_launch")
-        except (ValueError, AttributeError):
-            traffic = None
+    traffic, traffic_note = step_traffic_record()
     if args.route == "fused":
         # One kernel per step: its period in the timed graph is the time base.
         dom, dom_bytes, dom_us = "csa_step_kernel", r["step_bytes"], ms * 1e3
@@ -985,7 +1048,7 @@ def main():
         dom = max(kern, key=lambda n: kern[n]["total_ms"])
         dom_bytes, dom_us = kernel_bytes(dom, r), kern[dom]["avg_us"]
         base = "per-dispatch HIP events (eager pass)"
-        traffic = None
+        traffic, traffic_note = None, "the traffic record covers the fused step kernel only"
     achieved = dom_bytes / (dom_us * 1e-6) / 1e9
     line = {
         "metric": METRIC,
@@ -1009,6 +1072,7 @@ def main():
         "tokens_per_s": round(1e3 / ms, 1),
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": traffic,
+                     "traffic_source": traffic_note,
                      "bytes_per_launch": dom_bytes, "avg_launch_us": round(dom_us, 3), "time_base": base,
                      "kernel_us_events": round(kern[dom]["avg_us"], 3) if dom in kern else None,
                      "trace_window": r["trace_window"]},
@@ -1026,7 +1090,7 @@ def main():
         "kernels_avg_us": {n: round(v["avg_us"], 3) for n, v in kern.items()},
     }
     if not args.no_sweep_subset:
-        line["sweep_subset"] = sweep_rows(args, SWEEP_SUBSET, steps=max(args.steps, 20))
+        line["sweep"] = sweep_rows(args, SWEEP_GRID, steps=max(args.steps, 20))
     if not args.no_large_batch:
         line["large_batch"] = large_batch_bench()
     if not args.no_hca:
@@ -1036,9 +1100,7 @@ def main():
     if not args.no_dsv4:
         line["dsv4"] = dsv4_bench()
     if args.sweep:
-        points = [(B, S, k, v) for B in (1, 8, 32) for S in (8192, 32768, 131072) for k in (8, 32)
-                  for v in ("iid", "scattered", "clustered")]
-        rows = sweep_rows(args, points, steps=max(args.steps, 20))
+        rows = line["sweep"] if "sweep" in line else sweep_rows(args, SWEEP_GRID, steps=max(args.steps, 20))
         if args.sweep_out is not None:
             args.sweep_out.parent.mkdir(parents=True, exist_ok=True)
             args.sweep_out.write_text(json.dumps(rows, indent=1) + "\n")

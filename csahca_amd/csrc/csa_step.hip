@@ -85,7 +85,7 @@ constexpr int kStepScoreUnroll = 8;   // summary rows per lane per batch of load
 constexpr int kStepAttendUnroll = 4;  // K/V row loads per lane per batch
 constexpr int kRegMergeP = 8;         // partials per head merged from registers
 constexpr size_t kStepLds = 64 * 1024;
-constexpr uint32_t kSpinLimit = 1u << 20;
+constexpr uint32_t kSpinLimit = 1u << 20;  // polls per bounded wait (each with a short sleep)
 constexpr uint32_t kPoisonEpoch = 0xffffffffu;  // a head whose exchange timed out (see above)
 
 // This launch's tag for a head whose epoch word reads `epoch` (never the
@@ -125,6 +125,8 @@ struct StepParams {
                      // workgroups on one XCD when colo_bh is a multiple of 8); zero: head b / P
   float score_scale;
   float qscale;
+  uint32_t spin_limit;  // polls before a wait gives up (kSpinLimit; smaller only under the test switch)
+  int32_t mute_p;       // test switch: workgroup mute_p of head 0 publishes nothing (-1: none)
 };
 
 // Wait (bounded) until *p carries `tag`; returns its value bits.  On time-out
@@ -132,12 +134,12 @@ struct StepParams {
 // computes from the word (the head's output becomes NaN and the head is
 // poisoned), so a lost partner never yields a plausible-looking result.
 __device__ __forceinline__ uint32_t wait_tagged(const uint64_t* p, uint64_t w, uint32_t tag, uint32_t* status,
-                                                bool& bad) {
+                                                uint32_t spin_limit, bool& bad) {
   uint32_t it = 0;
   while (static_cast<uint32_t>(w >> 32) != tag) {
     __builtin_amdgcn_s_sleep(1);
     w = get_raw(p);
-    if (++it > kSpinLimit) {
+    if (++it > spin_limit) {
       __hip_atomic_fetch_or(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       bad = true;
       break;
@@ -178,6 +180,9 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
   const uint32_t cb = a.colo_bh;
   const int64_t h = cb ? block % cb : block / P;
   const int p = static_cast<int>(cb ? block / cb : block % P);
+  // Test switch only (the host sets mute_p = -1 otherwise): this workgroup
+  // publishes no key and no partial, so its partners' bounded waits expire.
+  const bool mute = h == 0 && p == a.mute_p;
   const int64_t Cs = a.Cs;
   // Chunks in play: the host's count, or the device's (its load overlaps the
   // summary loads of phase A, which are laid out over the Cs rows), or the
@@ -301,10 +306,11 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
         const int64_t c = base + grp + SRPL * (col / (SLPR / US));
         if (c < c1 && c < C) {
           const uint32_t key = order_key(ssum * a.score_scale);
-          if (P > 1)
-            put_tagged(kg + c, tag, key);
-          else
+          if (P > 1) {
+            if (!mute) put_tagged(kg + c, tag, key);
+          } else {
             keys_l[c] = key;
+          }
         }
       }
     };
@@ -359,7 +365,7 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
 #pragma unroll
       for (int j = 0; j < B8; ++j) {
         const int64_t i = i0 + j * NT;
-        if (i < C) keys_l[i] = wait_tagged(kg + i, w[j], tag, a.status, bad);
+        if (i < C) keys_l[i] = wait_tagged(kg + i, w[j], tag, a.status, a.spin_limit, bad);
       }
     }
   }
@@ -459,10 +465,12 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
   // until it carries this launch's tag: no arrival counter, so no atomic round
   // trip between the last partial and the merge.
   uint64_t* pp = a.part + h * a.part_stride + p * static_cast<int64_t>(D + 2);
-  if (d < D) put_tagged(pp + 2 + d, tag, __float_as_uint(A));
-  if (tid == 0) {
-    put_tagged(pp, tag, __float_as_uint(M));
-    put_tagged(pp + 1, tag, __float_as_uint(Lsum));
+  if (!mute) {
+    if (d < D) put_tagged(pp + 2 + d, tag, __float_as_uint(A));
+    if (tid == 0) {
+      put_tagged(pp, tag, __float_as_uint(M));
+      put_tagged(pp + 1, tag, __float_as_uint(Lsum));
+    }
   }
   CSAHCA_STAMP(5);
   if (p != 0) return;
@@ -505,7 +513,7 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
     poll(wf);
     for (uint32_t it = 0;; ++it) {
       if (bad || ready(wf)) break;
-      if (it >= kSpinLimit) {
+      if (it >= a.spin_limit) {
         __hip_atomic_fetch_or(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         bad = true;
         break;
@@ -559,7 +567,7 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
       const int i = i0 + j * NT;
       if (i < nw) {
         bool late = false;
-        const uint32_t v = wait_tagged(ph + i, w[j], tag, a.status, late);
+        const uint32_t v = wait_tagged(ph + i, w[j], tag, a.status, a.spin_limit, late);
         pb[i] = late ? __builtin_nanf("") : __uint_as_float(v);  // a lost word poisons what uses it
       }
     }
@@ -734,6 +742,19 @@ int env_step_wide() {
 int env_step_colocate() {
   const char* s = std::getenv("CSAHCA_STEP_COLOCATE");
   return s ? (std::atoi(s) != 0 ? 1 : 0) : -1;
+}
+
+// CSAHCA_STEP_TEST_TIMEOUT=n (> 0), a test switch for the exchange's
+// time-out path (read per call): in a launch with P > 1 the last workgroup of
+// head 0 publishes neither keys nor partial, and every bounded wait gives up
+// after n polls, so head 0's partners time out -- status bit set, head 0's
+// output NaN, head 0 poisoned -- while every workgroup still exits.  0 / unset:
+// off.
+uint32_t env_step_test_timeout() {
+  const char* s = std::getenv("CSAHCA_STEP_TEST_TIMEOUT");
+  if (s == nullptr) return 0;
+  const long long n = std::atoll(s);
+  return n > 0 ? static_cast<uint32_t>(std::min<long long>(n, kSpinLimit)) : 0;
 }
 
 HybridKernelFn hybrid_kernel_for(int dtype, int m) {
@@ -949,6 +970,11 @@ int decode_step_impl(const void* q, const void* k_cache, const void* v_cache, co
     pr.colo_bh = colo ? static_cast<uint32_t>(bh) : 0u;
     pr.score_scale = 1.0f / sqrtf(static_cast<float>(head_dim));
     pr.qscale = kLog2e / sqrtf(static_cast<float>(head_dim));
+    // Test switch for the time-out path: the last workgroup of head 0 publishes
+    // nothing, and every wait gives up after the given number of polls.
+    const uint32_t test_polls = env_step_test_timeout();
+    pr.spin_limit = test_polls > 0 ? test_polls : kSpinLimit;
+    pr.mute_p = (test_polls > 0 && P > 1) ? static_cast<int32_t>(P - 1) : -1;
     if (hyb) {
       const int64_t hblocks = ceil_div(hybrid->items, static_cast<int64_t>(hybrid->per_block));
       CSAHCA_REQUIRE(bh * P + hblocks <= INT32_MAX, "too many blocks in one call");
@@ -1030,9 +1056,18 @@ extern "C" int csahca_csa_decode_step_at(const void* q, const void* k_cache, con
                           stream_ptr);
 }
 
+namespace {
+int noalloc_status_word(const void** word);
+}
+
 extern "C" int csahca_csa_step_status(const void* workspace, uint32_t* status_out, void* stream_ptr) {
   clear_error();
-  CSAHCA_REQUIRE(workspace && status_out, "null pointer");
+  CSAHCA_REQUIRE(status_out, "null pointer");
+  // A null workspace names the allocation-free step's state on the current device.
+  if (workspace == nullptr) {
+    const int rc = noalloc_status_word(&workspace);
+    if (rc != CSAHCA_OK) return rc;
+  }
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
   hipError_t e = hipMemcpyAsync(status_out, workspace, sizeof(uint32_t), hipMemcpyDeviceToHost, stream);
   if (e != hipSuccess) return fail_hip(e, "csahca_csa_step_status");
@@ -1155,6 +1190,24 @@ int scratch_regions(StepRegions* rg) {
   rg->max_p = kFixedP;
   return CSAHCA_OK;
 }
+
+int noalloc_status_word(const void** word) {
+  StepRegions rg{};
+  const int rc = scratch_regions(&rg);
+  if (rc != CSAHCA_OK) return rc;
+  *word = rg.status;
+  return CSAHCA_OK;
+}
+
+// Zero-fills `words` 64-bit words (16 bytes per thread per store, grid-stride).
+__global__ __launch_bounds__(256) void scratch_zero_kernel(uint64_t* p, int64_t words) {
+  const int64_t pairs = words / 2;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  uint4* p4 = reinterpret_cast<uint4*>(p);
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < pairs; i += stride)
+    p4[i] = make_uint4(0u, 0u, 0u, 0u);
+  if (blockIdx.x == 0 && threadIdx.x == 0 && (words & 1)) p[words - 1] = 0;
+}
 }  // namespace
 
 extern "C" int csahca_csa_decode_step_noalloc(const void* q, const void* k_cache, const void* v_cache,
@@ -1178,6 +1231,21 @@ extern "C" int csahca_csa_decode_step_noalloc(const void* q, const void* k_cache
   return decode_step_impl(q, k_cache, v_cache, summary, out, out_indices, dtype, batch, heads, seq_len, head_dim,
                           num_chunks, nullptr, nullptr, chunk_size, top_k, nullptr, 0, stream_ptr, nullptr, 0,
                           nullptr, &rg);
+}
+
+// Zero the allocation-free step's state on the current device (status word,
+// epochs, keys and partials), on `stream`, with a fill kernel (capturable).
+// The caller must order it after every earlier allocation-free call and before
+// every later one (the same stream does).  This is how a head slot poisoned by
+// an exchange time-out is cleared.
+extern "C" int csahca_csa_step_noalloc_reset(void* stream_ptr) {
+  clear_error();
+  StepRegions rg{};
+  const int rc = scratch_regions(&rg);
+  if (rc != CSAHCA_OK) return rc;
+  uint64_t* base = reinterpret_cast<uint64_t*>(rg.status);
+  return launch("scratch_zero_kernel", scratch_zero_kernel, dim3(1024), dim3(256), 0,
+                static_cast<hipStream_t>(stream_ptr), base, kFixedWords);
 }
 
 #ifdef CSAHCA_STEP_TIMELINE

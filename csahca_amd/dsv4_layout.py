@@ -11,8 +11,9 @@ page ``loc // page_size`` at row ``loc % page_size``.  A nope value decodes as
 
 ``pack_dsv4_cache`` is a vectorised torch restatement of the reference's
 per-token packing loop (dsv4_correctness.py:24-59) that runs on CPU or GPU
-tensors and produces the same bytes; ``dequant_dsv4_cache`` mirrors
-dsv4_correctness.py:62-88.
+tensors and produces the same bytes (the input builder of tests and bench;
+the decode kernels read the format directly, and the checker's decoder of it
+lives with the oracle).
 """
 from __future__ import annotations
 
@@ -84,26 +85,3 @@ def pack_dsv4_cache(k_tokens: torch.Tensor, *, page_size: int) -> torch.Tensor:
     cache[:, :data_end] = rows.reshape(pages, data_end)
     cache[:, data_end:data_end + page_size * SCALE_BYTES_PER_TOKEN] = srows.reshape(pages, -1)
     return cache
-
-
-def dequant_dsv4_cache(cache: torch.Tensor, token_indices: torch.Tensor, *, page_size: int) -> torch.Tensor:
-    """Gather and decode token rows -> bf16 ``[..., 512]`` (dsv4_correctness.py:62-88)."""
-    raw = cache.contiguous().view(torch.uint8)
-    bpp = raw.shape[1]
-    flat_u8 = raw.reshape(-1)
-    loc = token_indices.to(torch.int64).reshape(-1).to(raw.device)
-    page = loc // page_size
-    in_page = loc % page_size
-    data_base = page * bpp + in_page * NOPE_ROPE_BYTES
-    scale_base = page * bpp + page_size * NOPE_ROPE_BYTES + in_page * SCALE_BYTES_PER_TOKEN
-    ar = torch.arange(DIM_NOPE, device=raw.device)
-    nope = flat_u8[data_base[:, None] + ar[None, :]].view(torch.float8_e4m3fn).float()
-    sidx = scale_base[:, None] + torch.arange(NUM_SCALE_TILES, device=raw.device)[None, :]
-    scale = torch.exp2(flat_u8[sidx].to(torch.int32).float() - 127.0)
-    nope = nope * scale.repeat_interleave(TILE_SIZE, dim=1)
-    rope_bytes = flat_u8[(data_base + DIM_NOPE)[:, None] + torch.arange(DIM_ROPE * 2, device=raw.device)[None, :]]
-    rope = rope_bytes.contiguous().view(torch.bfloat16)
-    out = torch.empty((loc.numel(), HEAD_DIM), dtype=torch.bfloat16, device=raw.device)
-    out[:, :DIM_NOPE] = nope.to(torch.bfloat16)
-    out[:, DIM_NOPE:] = rope
-    return out.reshape(*token_indices.shape, HEAD_DIM)

@@ -62,6 +62,7 @@ _SIGNATURES = {
     "csahca_csa_decode_step_at": (_int, [_vp] * 7 + [_int] + [_i64] * 7 + [_vp, _sz, _vp]),
     "csahca_csa_step_status": (_int, [_vp, ctypes.POINTER(ctypes.c_uint32), _vp]),
     "csahca_csa_decode_step_noalloc": (_int, [_vp] * 6 + [_int] + [_i64] * 7 + [_vp]),
+    "csahca_csa_step_noalloc_reset": (_int, [_vp]),
     "csahca_hca_decode_workspace_bytes": (_sz, [_i64] * 5),
     "csahca_dsv4_pack_tokens": (_int, [_vp, _vp, _i64, _vp, _i64, _i64, _i64, _vp]),
     "csahca_hca_decode_forward": (_int, [_vp, _vp, _vp, _vp, _dbl, _vp, _int] + [_i64] * 5 + [_vp, _sz, _vp]),
@@ -122,12 +123,36 @@ def _ptr(t: torch.Tensor | None):
     return None if t is None else t.data_ptr()
 
 
+# torch's current-device and raw current-stream queries (one C call each; the
+# Stream object that torch.cuda.current_stream() builds costs several us).
+_current_device = torch._C._cuda_getDevice
+_raw_stream = torch._C._cuda_getCurrentRawStream
+
+
 def _stream() -> int:
-    return torch.cuda.current_stream().cuda_stream
+    return _raw_stream(_current_device())
 
 
 def _workspace(nbytes: int, device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=device)
+
+
+_SCRATCH_WS: dict = {}
+
+
+def _scratch_workspace(nbytes: int, dev: int, stream: int) -> torch.Tensor:
+    """A workspace whose contents do not outlive one call (split partials),
+    kept per (device, stream, size) instead of allocated per call.  Calls on
+    one stream run in order, so they can share it; calls on different streams
+    get different buffers.  Never freed while the process runs
+    (release_step_workspaces() drops them), because a captured graph keeps
+    the address it recorded."""
+    key = (dev, stream, nbytes)
+    ws = _SCRATCH_WS.get(key)
+    if ws is None:
+        ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=torch.device("cuda", dev))
+        _SCRATCH_WS[key] = ws
+    return ws
 
 
 def _defined(t) -> bool:
@@ -144,23 +169,26 @@ def _present(t) -> bool:
 # ---------------------------------------------------------------------------
 
 def _csa_checks(q, k_cache, v_cache, chunk_indices, chunk_size, tiled: bool, tile_size=None):
-    if not (q.is_cuda and k_cache.is_cuda and v_cache.is_cuda and chunk_indices.is_cuda):
+    """The reference's TORCH_CHECKs of the CSA ops; ``chunk_indices`` None
+    (the fused step, which selects its own) skips the checks of that tensor."""
+    have_idx = chunk_indices is not None
+    if not (q.is_cuda and k_cache.is_cuda and v_cache.is_cuda and (not have_idx or chunk_indices.is_cuda)):
         raise RuntimeError("all tensors must be CUDA tensors")
     _check(q.is_contiguous(), "q must be contiguous")
     _check(k_cache.is_contiguous(), "k_cache must be contiguous")
     _check(v_cache.is_contiguous(), "v_cache must be contiguous")
-    _check(chunk_indices.is_contiguous(), "chunk_indices must be contiguous")
+    _check(not have_idx or chunk_indices.is_contiguous(), "chunk_indices must be contiguous")
     _check(q.dim() == 3, "q must be [batch, heads, head_dim]")
     _check(k_cache.dim() == 4, "k_cache must be [batch, heads, seq, head_dim]")
     _check(v_cache.shape == k_cache.shape, "v_cache must match k_cache shape")
-    _check(chunk_indices.dim() == 3, "chunk_indices must be [batch, heads, top_k]")
+    _check(not have_idx or chunk_indices.dim() == 3, "chunk_indices must be [batch, heads, top_k]")
     _check(q.dtype == k_cache.dtype, "q and k_cache dtype must match")
     _check(q.dtype == v_cache.dtype, "q and v_cache dtype must match")
-    _check(chunk_indices.dtype in (torch.int32, torch.int64), "chunk_indices must be int32 or int64")
+    _check(not have_idx or chunk_indices.dtype in (torch.int32, torch.int64), "chunk_indices must be int32 or int64")
     B, H, D = q.shape
     _check(k_cache.shape[0] == B and k_cache.shape[1] == H and k_cache.shape[3] == D,
            "KV cache shape must match q")
-    _check(chunk_indices.shape[0] == B and chunk_indices.shape[1] == H,
+    _check(not have_idx or (chunk_indices.shape[0] == B and chunk_indices.shape[1] == H),
            "chunk_indices batch/head dimensions must match q")
     _check(chunk_size > 0, "chunk_size must be positive")
     if tiled:
@@ -194,14 +222,18 @@ def csa_decode_forward_tiled(q, k_cache, v_cache, chunk_indices, chunk_size, til
     _csa_checks(q, k_cache, v_cache, chunk_indices, chunk_size, tiled=True, tile_size=tile_size)
     B, H, D = q.shape
     S, top_k = k_cache.shape[2], chunk_indices.shape[2]
-    with torch.cuda.device(q.device):
-        out = torch.empty_like(q)
-        nbytes = lib().csahca_csa_decode_workspace_bytes(B, H, D, top_k, chunk_size, tile_size)
-        ws = _workspace(nbytes, q.device)
-        _rc(lib().csahca_csa_decode_forward_tiled(
-            _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(chunk_indices), _ptr(out), _DTYPES[q.dtype],
-            0 if chunk_indices.dtype == torch.int32 else 1, B, H, S, D, top_k, chunk_size, tile_size,
-            _ptr(ws), ws.numel(), _stream()))
+    dev = q.get_device()
+    if dev != _current_device():
+        with torch.cuda.device(dev):
+            return csa_decode_forward_tiled(q, k_cache, v_cache, chunk_indices, chunk_size, tile_size)
+    stream = _raw_stream(dev)
+    out = torch.empty_like(q)
+    nbytes = lib().csahca_csa_decode_workspace_bytes(B, H, D, top_k, chunk_size, tile_size)
+    ws = _scratch_workspace(nbytes, dev, stream)
+    _rc(lib().csahca_csa_decode_forward_tiled(
+        q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), chunk_indices.data_ptr(), out.data_ptr(),
+        _DTYPES[q.dtype], 0 if chunk_indices.dtype == torch.int32 else 1, B, H, S, D, top_k, chunk_size, tile_size,
+        ws.data_ptr(), ws.numel(), stream))
     return out
 
 
@@ -297,12 +329,20 @@ def _step_workspace(nbytes: int, device, signature: tuple) -> torch.Tensor:
     stream) and then reused by every call of that shape on that stream -- eager
     calls and replays of graphs captured on it alike.  Buffers live until
     release_step_workspaces(): a captured graph keeps their addresses."""
-    key = (device.index, _stream(), signature)
-    ws = _STEP_WS.get(key)
-    if ws is None:
-        ws = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
-        _STEP_WS[key] = ws
-    return ws
+    return _step_ws_get(nbytes, torch.device(device).index, _stream(), signature)[0]
+
+
+def _step_ws_get(nbytes, dev: int, stream: int, signature: tuple):
+    """(workspace, its size in bytes) for (device index, raw stream, shape);
+    ``nbytes`` may be a callable, evaluated only when the buffer is created."""
+    key = (dev, stream, signature)
+    hit = _STEP_WS.get(key)
+    if hit is None:
+        n = max(int(nbytes() if callable(nbytes) else nbytes), 256)
+        ws = torch.zeros(n, dtype=torch.uint8, device=torch.device("cuda", dev))
+        hit = (ws, n)
+        _STEP_WS[key] = hit
+    return hit
 
 
 def step_workspace_ready(device, stream, signature: tuple) -> bool:
@@ -313,9 +353,10 @@ def step_workspace_ready(device, stream, signature: tuple) -> bool:
 
 
 def release_step_workspaces() -> None:
-    """Drop every cached step workspace (only when no captured graph that used
-    one will be replayed again)."""
+    """Drop every cached step workspace and per-stream scratch workspace (only
+    when no captured graph that used one will be replayed again)."""
     _STEP_WS.clear()
+    _SCRATCH_WS.clear()
 
 
 def csa_decode_step(q, k_cache, v_cache, summary, chunk_size, top_k, tile_size: int = 0):
@@ -329,24 +370,27 @@ def csa_decode_step(q, k_cache, v_cache, summary, chunk_size, top_k, tile_size: 
     if tile_size and tile_size > 0:
         idx = csa_select_topk(q, summary, top_k)
         return csa_decode_forward_tiled(q, k_cache, v_cache, idx, chunk_size, int(tile_size)), idx
-    _csa_checks(q, k_cache, v_cache, torch.empty((q.shape[0], q.shape[1], 0), dtype=torch.int32, device=q.device),
-                chunk_size, tiled=False)
+    _csa_checks(q, k_cache, v_cache, None, chunk_size, tiled=False)
     _check(summary.is_cuda and summary.is_contiguous() and summary.dtype == torch.float32 and summary.dim() == 4,
            "summary must be a contiguous fp32 [batch, heads, chunks, head_dim] CUDA tensor")
     B, H, D = q.shape
     S = k_cache.shape[2]
-    _check(tuple(summary.shape[:2]) == (B, H) and summary.shape[3] == D, "summary shape must match q")
+    _check(summary.shape[0] == B and summary.shape[1] == H and summary.shape[3] == D, "summary shape must match q")
     C = summary.shape[2]
     _check(top_k >= 0, "top_k must be non-negative")
     k = min(top_k, C)
-    with torch.cuda.device(q.device):
-        out = torch.empty_like(q)
-        idx = torch.empty((B, H, k), dtype=torch.int32, device=q.device)
-        ws = _step_workspace(lib().csahca_csa_step_workspace_bytes(B, H, C, D, top_k, chunk_size), q.device,
-                             (B * H, C, D, k, chunk_size))
-        _rc(lib().csahca_csa_decode_step(_ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(summary), _ptr(out), _ptr(idx),
-                                         _DTYPES[q.dtype], B, H, S, D, C, chunk_size, top_k, _ptr(ws), ws.numel(),
-                                         _stream()))
+    dev = q.get_device()
+    if dev != _current_device():
+        with torch.cuda.device(dev):
+            return csa_decode_step(q, k_cache, v_cache, summary, chunk_size, top_k)
+    stream = _raw_stream(dev)
+    out = torch.empty_like(q)
+    idx = q.new_empty((B, H, k), dtype=torch.int32)
+    ws, nbytes = _step_ws_get(lambda: lib().csahca_csa_step_workspace_bytes(B, H, C, D, top_k, chunk_size), dev,
+                              stream, (B * H, C, D, k, chunk_size))
+    _rc((_LIB or lib()).csahca_csa_decode_step(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), summary.data_ptr(),
+                                    out.data_ptr(), idx.data_ptr(), _DTYPES[q.dtype], B, H, S, D, C, chunk_size,
+                                    top_k, ws.data_ptr(), nbytes, stream))
     return out, idx
 
 
@@ -392,8 +436,7 @@ def csa_decode_step_dev(q, k_cache, v_cache, summary, num_chunks, chunk_size, to
     growing cache can be captured in one HIP graph.  ``out`` / ``indices``
     may be given to write in place.  Returns ``(out, chunk_indices)``."""
     chunk_size, top_k = int(chunk_size), int(top_k)
-    _csa_checks(q, k_cache, v_cache, torch.empty((q.shape[0], q.shape[1], 0), dtype=torch.int32, device=q.device),
-                chunk_size, tiled=False)
+    _csa_checks(q, k_cache, v_cache, None, chunk_size, tiled=False)
     _check(summary.is_cuda and summary.is_contiguous() and summary.dtype == torch.float32 and summary.dim() == 4,
            "summary must be a contiguous fp32 [batch, heads, chunks, head_dim] CUDA tensor")
     _check(num_chunks.is_cuda and num_chunks.dtype == torch.int32 and num_chunks.numel() == 1,
@@ -514,8 +557,7 @@ def csa_decode_step_at(q, k_cache, v_cache, summary, token_pos, chunk_size, top_
     launch in place of csa_chunk_summary_at + csa_decode_step_dev.  Returns
     ``(out, chunk_indices)``."""
     chunk_size, top_k = int(chunk_size), int(top_k)
-    _csa_checks(q, k_cache, v_cache, torch.empty((q.shape[0], q.shape[1], 0), dtype=torch.int32, device=q.device),
-                chunk_size, tiled=False)
+    _csa_checks(q, k_cache, v_cache, None, chunk_size, tiled=False)
     _check(summary.is_cuda and summary.is_contiguous() and summary.dtype == torch.float32 and summary.dim() == 4,
            "summary must be a contiguous fp32 [batch, heads, chunks, head_dim] CUDA tensor")
     _check(token_pos.is_cuda and token_pos.dtype == torch.int64 and token_pos.numel() == 1,
@@ -547,7 +589,7 @@ def csa_step_status(device=None) -> dict:
     an exchange wait timed out, the affected heads returned NaN and stay poisoned
     until their workspace is released).  Synchronises the calling stream."""
     out = {}
-    for key, ws in _STEP_WS.items():
+    for key, (ws, _) in _STEP_WS.items():
         if device is not None and key[0] != torch.device(device).index:
             continue
         val = ctypes.c_uint32(0)
@@ -555,6 +597,24 @@ def csa_step_status(device=None) -> dict:
             _rc(lib().csahca_csa_step_status(_ptr(ws), ctypes.byref(val), _stream()))
         out[key] = val.value
     return out
+
+
+def csa_step_noalloc_status(device=None) -> int:
+    """Sticky status word of csa_decode_step_noalloc's static state on
+    ``device`` (default: the current one): 0 = healthy, bit 0 = an exchange
+    wait timed out and the affected head slots stay poisoned until
+    csa_step_noalloc_reset().  Synchronises the calling stream."""
+    val = ctypes.c_uint32(0)
+    with torch.cuda.device(device if device is not None else torch.cuda.current_device()):
+        _rc(lib().csahca_csa_step_status(None, ctypes.byref(val), _stream()))
+    return val.value
+
+
+def csa_step_noalloc_reset(device=None) -> None:
+    """Zero csa_decode_step_noalloc's static state on ``device`` (a fill kernel
+    on the current stream; allocates nothing), clearing poisoned head slots."""
+    with torch.cuda.device(device if device is not None else torch.cuda.current_device()):
+        _rc(lib().csahca_csa_step_noalloc_reset(_stream()))
 
 
 def hca_decode_forward(q, k_cache, v_cache, chunk_size, *, blend=None, csa_weight: float = 0.7):
@@ -597,8 +657,7 @@ def hybrid_decode_forward(q, k_cache, v_cache, *, csa_chunk_size: int, csa_top_k
                "seq length must be divisible by chunk_size")
         summary = csa_chunk_summary(k_cache, csa_chunk_size)
     csa_chunk_size, csa_top_k, hca_chunk_size = int(csa_chunk_size), int(csa_top_k), int(hca_chunk_size)
-    _csa_checks(q, k_cache, v_cache, torch.empty((q.shape[0], q.shape[1], 0), dtype=torch.int32, device=q.device),
-                csa_chunk_size, tiled=False)
+    _csa_checks(q, k_cache, v_cache, None, csa_chunk_size, tiled=False)
     _check(summary.is_cuda and summary.is_contiguous() and summary.dtype == torch.float32 and summary.dim() == 4,
            "summary must be a contiguous fp32 [batch, heads, chunks, head_dim] CUDA tensor")
     B, H, S, D = k_cache.shape
@@ -700,21 +759,27 @@ def dsv4_decode_forward_tiled(q, paged_k_cache_u8, token_indices, topk_lengths, 
         _check(ebpp % 4 == 0,
                "tiled DSV4 kernel requires extra_bytes_per_page divisible by 4 for vectorized loads")
         extra_slots = extra_token_indices.shape[1]
-    with torch.cuda.device(q.device):
-        out = torch.empty_like(q)
-        if nq == 0 or heads == 0:
-            return out
-        ws = _workspace(lib().csahca_dsv4_decode_workspace_bytes(nq, heads, token_indices.shape[1], extra_slots,
-                                                                  tile_size), q.device)
-        ec = extra_paged_k_cache_u8 if has_extra else None
-        _rc(lib().csahca_dsv4_decode_forward_tiled(
-            _ptr(q), _DTYPES[q.dtype], nq, heads, _ptr(paged_k_cache_u8), paged_k_cache_u8.shape[0],
-            paged_k_cache_u8.shape[1], page_size, _ptr(token_indices), token_indices.shape[1],
-            _ptr(_opt(topk_lengths)), _ptr(ec), ec.shape[0] if has_extra else 0,
-            ec.shape[1] if has_extra else 0, extra_page_size if has_extra else 1,
-            _ptr(extra_token_indices) if has_extra else None, extra_slots,
-            _ptr(_opt(extra_topk_lengths)) if has_extra else None, _ptr(_opt(attn_sink)), float(softmax_scale),
-            tile_size, _ptr(out), _ptr(ws), ws.numel(), _stream()))
+    dev = q.get_device()
+    if dev != _current_device():
+        with torch.cuda.device(dev):
+            return dsv4_decode_forward_tiled(q, paged_k_cache_u8, token_indices, topk_lengths, extra_paged_k_cache_u8,
+                                             extra_token_indices, extra_topk_lengths, attn_sink, page_size,
+                                             extra_page_size, tile_size, softmax_scale)
+    out = torch.empty_like(q)
+    if nq == 0 or heads == 0:
+        return out
+    stream = _raw_stream(dev)
+    ws = _scratch_workspace(lib().csahca_dsv4_decode_workspace_bytes(nq, heads, token_indices.shape[1], extra_slots,
+                                                                     tile_size), dev, stream)
+    ec = extra_paged_k_cache_u8 if has_extra else None
+    _rc(lib().csahca_dsv4_decode_forward_tiled(
+        q.data_ptr(), _DTYPES[q.dtype], nq, heads, paged_k_cache_u8.data_ptr(), paged_k_cache_u8.shape[0],
+        paged_k_cache_u8.shape[1], page_size, token_indices.data_ptr(), token_indices.shape[1],
+        _ptr(_opt(topk_lengths)), _ptr(ec), ec.shape[0] if has_extra else 0,
+        ec.shape[1] if has_extra else 0, extra_page_size if has_extra else 1,
+        _ptr(extra_token_indices) if has_extra else None, extra_slots,
+        _ptr(_opt(extra_topk_lengths)) if has_extra else None, _ptr(_opt(attn_sink)), float(softmax_scale),
+        tile_size, out.data_ptr(), ws.data_ptr(), ws.numel(), stream))
     return out
 
 

@@ -155,13 +155,15 @@ def make_dsv4_case(*, compress_ratio: int, num_queries: int = 7, heads: int = 8,
 
 def make_dsv4_bench_case(*, compress_ratio: int, num_queries: int = 1, heads: int = 8, num_tokens: int = 4096,
                          top_k: int = 64, page_size: int = 256, extra_tokens: int = 4096, extra_top_k: int = 0,
-                         q_dtype: torch.dtype = torch.bfloat16, seed: int = 0,
+                         extra_page_size: int | None = None, q_dtype: torch.dtype = torch.bfloat16, seed: int = 0,
                          device: str | torch.device = "cpu") -> Dsv4Case:
     """The inputs of the reference DSV4 benchmark harness
     (hybrid_attention/dsv4_benchmark.py:30-76) on a CPU generator: q, k_tokens,
     token_indices (uniform over the pool), full lengths, sink, then for
     compress_ratio 4/128 extra_tokens and extra_token_indices; extra page size
-    ``page_size // compress_ratio``; extra_top_k defaults to 512 (C4) / 128 (C128).
+    ``page_size // compress_ratio`` unless ``extra_page_size`` is given;
+    extra_top_k defaults to 512 (C4) / 128 (C128).  Every query draws its own
+    slots, independently of the others (a batch of independent sequences).
     Its published H100 cases are nq 1, H 8, top_k 64, page 256 with extra_top_k
     128 (C4) and 64 (C128) (docs/dsv4_abi_status.md:64-65)."""
     g = torch.Generator(device="cpu")
@@ -174,7 +176,7 @@ def make_dsv4_bench_case(*, compress_ratio: int, num_queries: int = 1, heads: in
     case = Dsv4Case(q=q, k_tokens=k_tokens, cache=None, token_indices=token_indices, topk_lengths=topk_lengths,
                     attn_sink=attn_sink, page_size=page_size)
     if compress_ratio:
-        eps = page_size // compress_ratio
+        eps = extra_page_size if extra_page_size is not None else page_size // compress_ratio
         if eps <= 0:
             raise ValueError("page_size // compress_ratio must be positive")
         etop = extra_top_k or (512 if compress_ratio == 4 else 128)

@@ -189,7 +189,9 @@ int csahca_csa_decode_step_at(const void* q, const void* k_cache, const void* v_
 /* Reads the step workspace's sticky status word (0 = healthy; bit 0 = a
  * workgroup hand-off timed out: the affected heads returned NaN and stay
  * poisoned until the workspace is zero-filled) into host memory; synchronises
- * the stream. */
+ * the stream.  workspace == NULL reads the status word of
+ * csahca_csa_decode_step_noalloc's static state on the current device (no
+ * reference counterpart). */
 int csahca_csa_step_status(const void* workspace, uint32_t* status_out, void* stream);
 
 /* csahca_csa_decode_step without a workspace.  No counterpart in the
@@ -203,11 +205,23 @@ int csahca_csa_step_status(const void* workspace, uint32_t* status_out, void* st
  * aligned tensors, 0 < top_k <= 1024; other shapes return CSAHCA_ERR_ARGUMENT.
  * Results equal csahca_csa_decode_step's bit for bit.  Every call on a device
  * shares that device's array, so calls that can overlap on one device (two
- * streams) race and must be serialised by the caller. */
+ * streams) race and must be serialised by the caller.  After an exchange
+ * time-out the affected head slots of the array are poisoned: every later call
+ * returns NaN for the heads that use them, and the sticky status bit stays set,
+ * until csahca_csa_step_noalloc_reset; csahca_csa_step_status(NULL, ...) reads
+ * that status word. */
 int csahca_csa_decode_step_noalloc(const void* q, const void* k_cache, const void* v_cache,
                                    const float* summary, void* out, int32_t* out_indices, int dtype,
                                    int64_t batch, int64_t heads, int64_t seq_len, int64_t head_dim,
                                    int64_t num_chunks, int64_t chunk_size, int64_t top_k, void* stream);
+
+/* Zero-fills csahca_csa_decode_step_noalloc's static state on the current
+ * device (status word, epochs, tagged words) with a kernel on `stream`
+ * (capturable; allocates nothing).  No counterpart in the reference: it is
+ * for the same callers as csahca_csa_decode_step_noalloc, to clear head slots
+ * poisoned by a time-out.  Order it after every earlier and before every later
+ * allocation-free call (one stream does). */
+int csahca_csa_step_noalloc_reset(void* stream);
 
 /* ------------------------------------------------------------------------- */
 /* HCA: dense attention over chunk summaries, and the CSA/HCA blend           */

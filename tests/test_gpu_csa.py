@@ -430,6 +430,46 @@ def test_fused_step_repeated_calls_rearm_counters():
     assert all(v == 0 for v in native.csa_step_status().values())
 
 
+def test_exchange_timeout_poisons_the_head_until_the_workspace_is_zeroed(monkeypatch):
+    """The fused step's time-out path, forced from the host: with
+    CSAHCA_STEP_TEST_TIMEOUT=n the last workgroup of head 0 publishes neither
+    keys nor partial and every bounded wait gives up after n polls, so every
+    workgroup still exits.  Head 0's output is NaN and the sticky status bit
+    is set, while the other heads keep the oracle's ids and outputs.  Later
+    calls on that workspace (switch off) keep head 0 NaN and the bit set; a
+    zero-filled workspace recovers."""
+    B, H, S, D, chunk, k = 1, 8, 32768, 128, 64, 8  # P = 8 workgroups per head
+    case = make_synthetic_case(batch=B, heads=H, seq_len=S, head_dim=D, chunk_size=chunk, top_k=k, seed=11)
+    q, kd, vd = case.q.to(DEV), case.k_cache.to(DEV), case.v_cache.to(DEV)
+    summ = extension.csa_chunk_summary(kd, chunk)
+    want, scores = oracle.select_topk(case.q, summ.cpu(), k)
+    ref = oracle.csa_attend(case.q, case.k_cache, case.v_cache, want, chunk, prob_dtype=oracle.F32)
+    native.release_step_workspaces()
+    monkeypatch.setenv("CSAHCA_STEP_TEST_TIMEOUT", "4096")
+    out, idx = native.csa_decode_step(q, kd, vd, summ, chunk, k)
+    torch.cuda.synchronize()
+    monkeypatch.delenv("CSAHCA_STEP_TEST_TIMEOUT")
+
+    def healthy_heads_match(o, i):
+        assert_indices(i[:, 1:], want[:, 1:], scores[:, 1:])
+        assert_close(o[:, 1:], ref[:, 1:], 2e-2, 1e-2, "heads 1..7")
+
+    assert torch.isnan(out[0, 0].float()).all()
+    healthy_heads_match(out, idx)
+    assert all(v & 1 for v in native.csa_step_status().values())
+    for _ in range(2):  # the head stays poisoned on this workspace
+        out2, idx2 = native.csa_decode_step(q, kd, vd, summ, chunk, k)
+        torch.cuda.synchronize()
+        assert torch.isnan(out2[0, 0].float()).all()
+        healthy_heads_match(out2, idx2)
+    assert all(v & 1 for v in native.csa_step_status().values())
+    native.release_step_workspaces()  # the next call zero-fills a new workspace
+    out3, idx3 = native.csa_decode_step(q, kd, vd, summ, chunk, k)
+    assert_indices(idx3, want, scores)
+    assert_close(out3, ref, 2e-2, 1e-2, "after a zero-filled workspace")
+    assert all(v == 0 for v in native.csa_step_status().values())
+
+
 def test_workgroups_per_head_override_is_bounded_by_residency(monkeypatch):
     """CSAHCA_STEP_WGS_PER_HEAD=64 at B32 H8 asks for 16384 workgroups that wait
     on each other, far more than the device holds at once; the library shrinks P
@@ -450,19 +490,24 @@ def test_workgroups_per_head_override_is_bounded_by_residency(monkeypatch):
     assert all(v == 0 for v in native.csa_step_status().values())
 
 
-GRID_REST = [  # BASELINE config 1 grid points beyond B = 1 (B32 S131072 has its own test below)
-    (8, 32768, 8), (8, 32768, 32), (8, 131072, 8), (8, 131072, 32),
-    (32, 8192, 8), (32, 8192, 32), (32, 32768, 8), (32, 32768, 32),
+GRID = [  # every point of the sweep B {1, 8, 32} x S {8192, 32768, 131072} x top-k {8, 32}
+    (B, S, k) for B in (1, 8, 32) for S in (8192, 32768, 131072) for k in (8, 32)
 ]
 
 
-@pytest.mark.parametrize("B,S,k", GRID_REST)
+@pytest.mark.parametrize("B,S,k", GRID)
 def test_sweep_grid_point_matches_oracle(B, S, k):
     """The fused decode step at a config-1 grid point (H8 D128 chunk 64, bf16
     N(0,1) drawn on the device) against the oracle: chunk summaries on the
     first and last head, selection from the device summaries (ids bit-exact up
     to 1e-5 score ties), and attention over the selected chunks' tokens, which
-    are gathered on the device so the oracle works on [B, H, k*64, D] copies."""
+    are gathered on the device so the oracle works on [B, H, k*64, D] copies.
+
+    The launch shape the host picks differs across the grid: P = 8 workgroups
+    per head with a head's workgroups on one XCD at B1 S32768 top-8; P = 1 and
+    the double-buffered instantiation at B32 top-8 (at S131072 over K and V of
+    2^32 elements, 8 GiB, each, so the byte offsets of the last heads pass
+    2^32); the 8-wavefront instantiation at B32 top-32."""
     H, D, chunk = 8, 128, 64
     g = torch.Generator(device=DEV).manual_seed(B * 31 + S // 1024 + k)
     q = torch.randn(B, H, D, device=DEV, generator=g).to(torch.bfloat16)

@@ -111,6 +111,35 @@ def test_noalloc_python_wrapper_matches():
     assert torch.equal(idx, want_idx) and torch.equal(out, want_out)
 
 
+def test_noalloc_timeout_poisons_until_reset(monkeypatch):
+    """After an exchange time-out (forced from the host with
+    CSAHCA_STEP_TEST_TIMEOUT: the last workgroup of head 0 publishes nothing,
+    waits give up after 4096 polls) the static state's head slot 0 is
+    poisoned: head 0 returns NaN on this and later calls, the status word read
+    through csahca_csa_step_status(NULL) keeps bit 0, and the other heads are
+    unaffected; csahca_csa_step_noalloc_reset clears it."""
+    q, k, v, summ = _inputs(1, 8, 32768, 128, torch.bfloat16, seed=12)
+    want_out, want_idx = _with_workspace(q, k, v, summ, 8)
+    out, idx = _outputs(q, summ, 8)
+    native.csa_step_noalloc_reset()
+    assert native.csa_step_noalloc_status() == 0
+    monkeypatch.setenv("CSAHCA_STEP_TEST_TIMEOUT", "4096")
+    _noalloc(q, k, v, summ, out, idx, 8)
+    torch.cuda.synchronize()
+    monkeypatch.delenv("CSAHCA_STEP_TEST_TIMEOUT")
+    for rep in range(2):
+        assert torch.isnan(out[0, 0].float()).all(), rep
+        assert torch.equal(out[0, 1:], want_out[0, 1:]) and torch.equal(idx[0, 1:], want_idx[0, 1:]), rep
+        assert native.csa_step_noalloc_status() & 1, rep
+        _noalloc(q, k, v, summ, out, idx, 8)
+        torch.cuda.synchronize()
+    native.csa_step_noalloc_reset()
+    _noalloc(q, k, v, summ, out, idx, 8)
+    torch.cuda.synchronize()
+    assert torch.equal(out, want_out) and torch.equal(idx, want_idx)
+    assert native.csa_step_noalloc_status() == 0
+
+
 @pytest.mark.parametrize("B,H,C,D,top_k,msg", [
     (257, 1, 8, 128, 4, "batch \\* heads exceeds 256"),
     (1, 8, 2049, 128, 4, "num_chunks exceeds 2048"),
