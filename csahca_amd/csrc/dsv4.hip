@@ -18,6 +18,7 @@
 #include <algorithm>
 #include <climits>
 #include <cstdlib>
+#include <type_traits>
 
 namespace csahca {
 namespace {
@@ -1183,6 +1184,283 @@ __global__ __launch_bounds__(W * kWave) void dsv4_query_kernel(const bf16* __res
   }
 }
 
+// ---------------------------------------------------------------------------
+// One-pass grouped-head kernel (dsv4_onepass_kernel): slot lists of at most
+// kOpMaxSlots slots.  A workgroup of kOpWaves wavefronts is one (query, 16
+// heads, dim part), as for dsv4_query_kernel, but nothing runs in rounds:
+//   1. every lane requests the indices of its two slots, the lengths, the
+//      query rows (staged in LDS) and the sink; then, as soon as the indices
+//      arrive, the latent rows of both its sub-tiles -- wavefront w owns
+//      sub-tiles w and w + kOpWaves of 16 slots, so the whole slot list is in
+//      flight after two dependent round trips;
+//   2. each wavefront reads its B operand of S^T = K Q^T (the 16 query rows)
+//      from LDS into registers once, then per sub-tile dequantises the rows
+//      straight into MFMA A operands -- the contraction runs over the dims in
+//      the order of the 16-byte row chunks a lane holds (chunk c = grp + 4 i
+//      of e4m3 gives the k-steps 2 i and 2 i + 1, rope chunk grp + 4 i the
+//      k-step 14 + i), and the query operand is read in the same order -- and
+//      writes the values of this workgroup's output dims to a row-major V
+//      tile in LDS;
+//   3. one exact softmax per head over the whole list: per-wavefront maxima
+//      through LDS, then p = 2^(s - M) (fp32 sums, bf16 operands for PV)
+//      written as P^T rows in LDS;
+//   4. O^T = V^T P^T on v_mfma_f32_16x16x16_bf16 for the wavefront's 16-dim
+//      output blocks over all sub-tiles (V^T through ds_read_b64_tr_b16), and
+//      the sink as a virtual token of logit sink[h] and value 0
+//      (csrc/dsv4_attention.cu:252-269).
+// Scores, probabilities and sums are those of the other MFMA kernels up to
+// fp32 summation order (the softmax subtracts the exact maximum).
+constexpr int kOpWaves = 8;
+constexpr int kOpSubs = 2;                                // 16-slot sub-tiles per wavefront
+constexpr int kOpMaxSlots = kOpWaves * kOpSubs * kQSub;   // 256
+constexpr int kOpProw = 272;  // P^T row stride in bf16 (136 dwords = 8 mod 64 banks)
+
+template <int DS>
+struct OnePassLayout {
+  static constexpr int DW = kDim / DS;                     // output dims of a workgroup
+  static constexpr int VROW = DW + 24;                     // V tile row in bf16 (dwords = 12 mod 64)
+  static constexpr int OB = DW / kOpWaves / 16;            // 16-dim output blocks per wavefront
+  static constexpr int TILE_BYTES = kOpMaxSlots * VROW * 2;
+  static constexpr int Q_BYTES = kQHeads * kQQRow * 2;     // query staging (aliases the V tiles)
+  static constexpr int R0 = TILE_BYTES > Q_BYTES ? TILE_BYTES : Q_BYTES;
+  static constexpr int MX = R0;                            // [waves][16] maxima
+  static constexpr int LS = MX + kOpWaves * 16 * 4;        // [waves][16] sums
+  static constexpr int PT = LS + kOpWaves * 16 * 4;        // [16 heads][kOpProw] bf16
+  static constexpr int BYTES = PT + kQHeads * kOpProw * 2;
+  static_assert(OB >= 1, "at least one 16-dim block per wavefront");
+  static_assert(BYTES <= 160 * 1024, "LDS of one workgroup");
+};
+
+template <int DS>
+__global__ __launch_bounds__(kOpWaves * kWave) void dsv4_onepass_kernel(const bf16* __restrict__ q, Dsv4Args a,
+                                                                        QueryArgs g) {
+  using Lay = OnePassLayout<DS>;
+  constexpr int NW = kOpWaves;
+  constexpr int NT = NW * kWave;
+  constexpr int DW = Lay::DW, VROW = Lay::VROW, OB = Lay::OB;
+  constexpr int QQU = kQHeads * (kDim / 8) / NT;  // 16-byte query units per thread
+  __shared__ __align__(16) uint8_t smem[Lay::BYTES];
+  uint16_t* vtile = reinterpret_cast<uint16_t*>(smem);
+  uint16_t* qlds = reinterpret_cast<uint16_t*>(smem);  // before the V tiles are written
+  float* mxs = reinterpret_cast<float*>(smem + Lay::MX);
+  float* lss = reinterpret_cast<float*>(smem + Lay::LS);
+  uint16_t* pt = reinterpret_cast<uint16_t*>(smem + Lay::PT);
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int lane = tid % kWave;
+  const int grp = lane / 16;
+  const int l16 = lane % 16;
+  const uint32_t blk = blockIdx.x;
+  const uint32_t r = blk / 8;
+  const uint32_t gx = static_cast<uint32_t>(g.groups) * DS;
+  const uint32_t hgx = r % gx;
+  const int hg = static_cast<int>(hgx / DS);
+  const int part = static_cast<int>(hgx % DS);
+  const int64_t query = static_cast<int64_t>(r / gx) * 8 + blk % 8;
+  if (query >= g.nq) return;
+  const int h0 = hg * kQHeads;
+  const int nh = min(kQHeads, a.heads - h0);
+  const int nsub = g.nsub;
+  const int total = a.topk_slots + a.extra_slots;
+
+  // ---- 1. indices, lengths, query rows, sink; then the rows -----------------
+  const void* anyp = static_cast<const void*>(q);
+  const int32_t len_raw = load_global_i32(a.lens ? static_cast<const void*>(a.lens + query) : anyp);
+  const int32_t elen_raw = load_global_i32(a.elens ? static_cast<const void*>(a.elens + query) : anyp);
+  const uint8_t* dummy = reinterpret_cast<const uint8_t*>(q + (query * a.heads + h0) * kDim);  // >= 1 KiB, in bounds
+  int32_t li[kOpSubs], le[kOpSubs];
+#pragma unroll
+  for (int j = 0; j < kOpSubs; ++j) {
+    const int s = (wave + NW * j) * kQSub + l16;
+    const int32_t* ip = a.topk_slots > 0 ? a.idx + query * a.topk_slots + min(s, a.topk_slots - 1)
+                                         : reinterpret_cast<const int32_t*>(dummy);
+    const int32_t* ep = a.extra_slots > 0
+                            ? a.eidx + query * a.extra_slots + min(max(s - a.topk_slots, 0), a.extra_slots - 1)
+                            : reinterpret_cast<const int32_t*>(dummy);
+    li[j] = load_global_i32(ip);
+    le[j] = load_global_i32(ep);
+  }
+  uint4 qw[QQU];
+#pragma unroll
+  for (int u = 0; u < QQU; ++u) {
+    const int e = tid + NT * u;
+    qw[u] = load_global_u4(q + (query * a.heads + h0 + min(e / (kDim / 8), nh - 1)) * kDim + 8 * (e % (kDim / 8)));
+  }
+  // (unconditional: a load under a branch would make the wait-count pass wait
+  // for every load in flight at the join)
+  const float sink_raw = load_global_raw<float>(g.sink ? static_cast<const void*>(g.sink + h0 + min(l16, nh - 1))
+                                                       : anyp);
+  asm volatile("" : "+v"(li[0]), "+v"(le[0]), "+v"(li[1]), "+v"(le[1]));
+  const int n_swa = a.lens ? max(0, min(len_raw, a.topk_slots)) : a.topk_slots;
+  const int n_extra = a.extra_slots > 0 ? (a.elens ? max(0, min(elen_raw, a.extra_slots)) : a.extra_slots) : 0;
+  QRows rw[kOpSubs];
+#pragma unroll
+  for (int j = 0; j < kOpSubs; ++j) {
+    const int s = (wave + NW * j) * kQSub + l16;
+    const bool in_swa = s < a.topk_slots;
+    const bool valid = s < total && (in_swa ? s < n_swa : s - a.topk_slots < n_extra);
+    const int32_t loc = valid ? (in_swa ? li[j] : le[j]) : -1;
+    const uint8_t* sr = nullptr;
+    const uint8_t* rr = loc >= 0 ? row_ptr(in_swa ? a.swa : a.extra, loc, &sr) : nullptr;
+    rw[j].ok = rr != nullptr;
+    const uint8_t* rp = rw[j].ok ? rr : dummy;
+    const uint8_t* sp = rw[j].ok ? sr : dummy;
+#pragma unroll
+    for (int i = 0; i < 7; ++i) rw[j].c[i] = load_global_u4(rp + 16 * (grp + 4 * i));
+#pragma unroll
+    for (int i = 0; i < 2; ++i) rw[j].c[7 + i] = load_global_u4(rp + kNope + 16 * (grp + 4 * i));
+    rw[j].sc = load_global_u2(sp);
+  }
+
+  // ---- 2. query operand into registers; per sub-tile dequant, V tile, QK ----
+#pragma unroll
+  for (int u = 0; u < QQU; ++u) {
+    const int e = tid + NT * u;
+    *reinterpret_cast<uint4*>(qlds + (e / (kDim / 8)) * kQQRow + 8 * (e % (kDim / 8))) =
+        e / (kDim / 8) < nh ? qw[u] : make_uint4(0u, 0u, 0u, 0u);
+  }
+  lds_barrier();
+  uint4 qb[16];  // B operand of k-step t: head l16, the dims of this lane group's chunk for t
+  {
+    const uint16_t* qrow = qlds + l16 * kQQRow;
+#pragma unroll
+    for (int t = 0; t < 14; ++t)
+      qb[t] = *reinterpret_cast<const uint4*>(qrow + 16 * (grp + 4 * (t >> 1)) + 8 * (t & 1));
+#pragma unroll
+    for (int t = 14; t < 16; ++t) qb[t] = *reinterpret_cast<const uint4*>(qrow + kNope + 8 * (grp + 4 * (t - 14)));
+  }
+  lds_barrier();  // the query staging is overwritten by the V tiles below
+
+  float x[kOpSubs][4];
+#pragma unroll
+  for (int j = 0; j < kOpSubs; ++j) {
+    const int u = wave + NW * j;  // global sub-tile (wave-uniform)
+    if (u >= nsub) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[j][e] = -INFINITY;
+      continue;
+    }
+    const QRows& w = rw[j];
+    const uint32_t valid16 = static_cast<uint32_t>(__ballot(w.ok) & 0xffffull);
+    const bool any255 = __ballot(w.ok && has_scale_255(w.sc)) != 0ull;
+    uint16_t* trow = vtile + (u * kQSub + l16) * VROW;  // dim d (of this part) of this slot at trow + d - DW part
+    f32x4_t sacc0 = f32x4_t{0.f, 0.f, 0.f, 0.f}, sacc1 = sacc0;
+    // The 7 e4m3 chunks, with the hardware conversion or (rare: a scale byte
+    // of 255 in the sub-tile) the software decode -- one branch around the
+    // whole sequence, so the common path's code is contiguous.
+    auto nope = [&](auto sw) {
+#pragma unroll
+      for (int i = 0; i < 7; ++i) {
+        const uint32_t sbyte = (i < 4 ? w.sc.x >> (8 * i) : w.sc.y >> (8 * (i - 4))) & 0xffu;
+        uint4 lo, hi;
+        if constexpr (decltype(sw)::value) {
+          lo = dequant8_bf16_sw(make_uint2(w.c[i].x, w.c[i].y), sbyte);
+          hi = dequant8_bf16_sw(make_uint2(w.c[i].z, w.c[i].w), sbyte);
+        } else {
+          lo = dequant8_bf16_hw(make_uint2(w.c[i].x, w.c[i].y), sbyte);
+          hi = dequant8_bf16_hw(make_uint2(w.c[i].z, w.c[i].w), sbyte);
+        }
+        if (!w.ok) lo = hi = make_uint4(0u, 0u, 0u, 0u);  // skipped slot: zero K and V
+        const int d = 16 * (grp + 4 * i);                 // nope dims d .. d + 15
+        if (d >= DW * part && d < DW * (part + 1)) {
+          *reinterpret_cast<uint4*>(trow + (d - DW * part)) = lo;
+          *reinterpret_cast<uint4*>(trow + (d - DW * part) + 8) = hi;
+        }
+        sacc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, lo),
+                                                        __builtin_bit_cast(bf16x8_t, qb[2 * i]), sacc0, 0, 0, 0);
+        sacc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, hi),
+                                                        __builtin_bit_cast(bf16x8_t, qb[2 * i + 1]), sacc1, 0, 0, 0);
+      }
+    };
+    if (!any255)
+      nope(std::false_type{});
+    else
+      nope(std::true_type{});
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint4 rope = w.ok ? w.c[7 + i] : make_uint4(0u, 0u, 0u, 0u);
+      const int d = kNope + 8 * (grp + 4 * i);  // rope dims d .. d + 7
+      if (d >= DW * part && d < DW * (part + 1)) *reinterpret_cast<uint4*>(trow + (d - DW * part)) = rope;
+      if (i == 0)
+        sacc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, rope),
+                                                        __builtin_bit_cast(bf16x8_t, qb[14]), sacc0, 0, 0, 0);
+      else
+        sacc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, rope),
+                                                        __builtin_bit_cast(bf16x8_t, qb[15]), sacc1, 0, 0, 0);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      x[j][e] = ((valid16 >> (4 * grp + e)) & 1u) ? (sacc0[e] + sacc1[e]) * a.qscale : -INFINITY;
+  }
+
+  // ---- 3. softmax over the whole slot list ----------------------------------
+  float mw = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < kOpSubs; ++j)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) mw = fmaxf(mw, x[j][e]);
+  mw = fmaxf(mw, __uint_as_float(lane_xor<16>(__float_as_uint(mw), lane)));
+  mw = fmaxf(mw, __uint_as_float(lane_xor<32>(__float_as_uint(mw), lane)));
+  if (grp == 0) mxs[wave * 16 + l16] = mw;
+  lds_barrier();  // maxima, and every V tile
+  float M = -INFINITY;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) M = fmaxf(M, mxs[w * 16 + l16]);
+  float ps = 0.f;
+#pragma unroll
+  for (int j = 0; j < kOpSubs; ++j) {
+    float p[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      p[e] = M == -INFINITY ? 0.f : fast_exp2(x[j][e] - M);
+      ps += p[e];
+    }
+    const int u = wave + NW * j;
+    if (u < nsub)
+      *reinterpret_cast<uint2*>(pt + l16 * kOpProw + u * kQSub + 4 * grp) =
+          make_uint2(bf16x2_nb(p[0], p[1]), bf16x2_nb(p[2], p[3]));
+  }
+  ps += __uint_as_float(lane_xor<16>(__float_as_uint(ps), lane));
+  ps += __uint_as_float(lane_xor<32>(__float_as_uint(ps), lane));
+  if (grp == 0) lss[wave * 16 + l16] = ps;
+  lds_barrier();  // P^T rows and sums
+
+  // ---- 4. O^T = V^T P^T over every sub-tile, then the sink -----------------
+  float L = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) L += lss[w * 16 + l16];
+  f32x4_t o[OB];
+#pragma unroll
+  for (int j = 0; j < OB; ++j) o[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // V^T A operand of block j (dims (DW / NW) wave + 16 j .. of this part) of
+  // sub-tile u: lane a of group g passes &V[16 u + 4 g + a / 4][... + 4 (a % 4)].
+  const uint16_t* vbase = vtile + (4 * grp + l16 / 4) * VROW + 4 * (l16 % 4) + (DW / NW) * wave;
+  const uint16_t* pbase = pt + l16 * kOpProw + 4 * grp;
+  for (int u = 0; u < nsub; ++u) {
+    const i16x4_t pb = __builtin_bit_cast(i16x4_t, *reinterpret_cast<const uint2*>(pbase + u * kQSub));
+    i16x4_t vt[OB];
+#pragma unroll
+    for (int j = 0; j < OB; ++j)
+      vt[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(vbase + u * kQSub * VROW + 16 * j));
+#pragma unroll
+    for (int j = 0; j < OB; ++j) o[j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt[j], pb, o[j], 0, 0, 0);
+  }
+  const float sk = g.sink ? sink_raw * kLog2e : -INFINITY;
+  const float mx = L > 0.f ? fmaxf(sk, M) : sk;
+  const float wgt = (L > 0.f && mx != -INFINITY) ? fast_exp2(M - mx) : 0.f;
+  float Lt = wgt * (L > 0.f ? L : 0.f);
+  if (g.sink && mx != -INFINITY) Lt += fast_exp2(sk - mx);
+  const float sc = L != L ? __builtin_nanf("") : (Lt > 0.f ? wgt / Lt : 0.f);
+  if (l16 < nh) {
+    bf16* orow = g.out + (query * a.heads + h0 + l16) * kDim + DW * part + (DW / NW) * wave + 4 * grp;
+#pragma unroll
+    for (int j = 0; j < OB; ++j)
+      *reinterpret_cast<uint2*>(orow + 16 * j) =
+          make_uint2(bf16x2_nb(o[j][0] * sc, o[j][1] * sc), bf16x2_nb(o[j][2] * sc, o[j][3] * sc));
+  }
+}
+
 constexpr int kMergeThreads = kDim / 4;  // 4 output columns per thread
 constexpr int kMergeChunk = 1024;        // tile weights staged in LDS per pass
 constexpr int kMergeFastTiles = 16;      // tiles merged straight from registers
@@ -1399,6 +1677,29 @@ int query_dim_parts(int64_t nq, int64_t groups) {
   return 4 * base <= ncu ? 4 : 2 * base <= ncu ? 2 : 1;
 }
 
+// The one-pass kernel takes every bf16 call with automatic tiling whose slot
+// list fits it (1 .. kOpMaxSlots slots).  CSAHCA_DSV4_ONEPASS=0 turns it off,
+// and so does CSAHCA_DSV4_QUERY=0 / 1, which forces the split / per-query
+// kernel (both read per call).
+bool use_onepass(int64_t total_slots) {
+  const char* e = std::getenv("CSAHCA_DSV4_ONEPASS");
+  if (e && e[0] == '0' && e[1] == 0) return false;
+  const char* f = std::getenv("CSAHCA_DSV4_QUERY");
+  if (f && (f[0] == '0' || f[0] == '1')) return false;
+  return total_slots > 0 && total_slots <= kOpMaxSlots;
+}
+
+// Dim parts of the one-pass kernel: 4 where the workgroups still fit one per
+// CU, else 2 (a part of all 512 dims would not fit the V tiles in LDS).
+// CSAHCA_DSV4_QPARTS=2/4 forces a count.
+int onepass_dim_parts(int64_t nq, int64_t groups) {
+  const char* e = std::getenv("CSAHCA_DSV4_QPARTS");
+  if (e && (e[0] == '2' || e[0] == '4') && e[1] == 0) return e[0] - '0';
+  const int ncu = device_cu_count();
+  const int64_t base = ceil_div(nq, 8) * 8 * groups;
+  return (ncu > 0 && 4 * base <= ncu) ? 4 : 2;
+}
+
 struct Dsv4Call {
   const void* q;
   int dtype;
@@ -1461,6 +1762,21 @@ int dsv4_run(const Dsv4Call& c) {
   a.num_tiles = static_cast<int>(tiles);
   a.qscale = static_cast<float>(c.softmax_scale) * kLog2e;
   hipStream_t stream = static_cast<hipStream_t>(c.stream);
+  if (use_mfma && reinterpret_cast<uintptr_t>(c.out) % 8 == 0 && use_onepass(total)) {
+    QueryArgs qa;
+    qa.nq = c.nq;
+    qa.groups = static_cast<int>(ceil_div(c.heads, kQHeads));
+    qa.nsub = static_cast<int>(ceil_div(total, kQSub));
+    qa.sink = c.sink;
+    qa.out = static_cast<bf16*>(c.out);
+    const int ds = onepass_dim_parts(c.nq, qa.groups);
+    // query q's (group, part) pairs x: blocks q%8 + 8 (x + G DS q/8)
+    const int64_t blocks = ceil_div(c.nq, 8) * 8 * qa.groups * ds;
+    CSAHCA_REQUIRE(blocks <= INT32_MAX, "too many DSV4 work items");
+    auto kfn = ds == 4 ? dsv4_onepass_kernel<4> : dsv4_onepass_kernel<2>;
+    return launch("dsv4_onepass_kernel", kfn, dim3(static_cast<uint32_t>(blocks)), dim3(kOpWaves * kWave), 0,
+                  stream, static_cast<const bf16*>(c.q), a, qa);
+  }
   if (use_mfma && reinterpret_cast<uintptr_t>(c.out) % 8 == 0 && use_query_kernel(c.nq, c.heads, total)) {
     QueryArgs qa;
     qa.nq = c.nq;

@@ -150,13 +150,13 @@ def test_unaligned_bytes_per_page_scalar_path():
     assert_close(gpu_out(c), oracle_out(c))
 
 
-@pytest.mark.parametrize("path", ["valu-f32", "query-bf16", "split-bf16"])
+@pytest.mark.parametrize("path", ["valu-f32", "onepass-bf16", "query-bf16", "split-bf16"])
 def test_e4m3_and_scale_decode_exhaustive(path, monkeypatch):
     """Single valid slot, no sink: out = the dequantised row exactly (softmax
     weight 1).  Rows cover all 256 e4m3 codes (NaN codes excluded) under many
-    scale bytes.  fp32 queries take the VALU kernel; bf16 queries the per-query
-    MFMA kernel or the split MFMA kernel + merge (both round the probability
-    1.0 and the bf16 row exactly)."""
+    scale bytes.  fp32 queries take the VALU kernel; bf16 queries the one-pass
+    kernel, the per-query MFMA kernel or the split MFMA kernel + merge (all
+    round the probability 1.0 and the bf16 row exactly)."""
     codes = np.array([b for b in range(256) if (b & 0x7F) != 0x7F], dtype=np.uint8)
     ps = 4
     bpp = dsv4_layout.bytes_per_page(ps)
@@ -174,7 +174,7 @@ def test_e4m3_and_scale_decode_exhaustive(path, monkeypatch):
         cache[page, ps * 576 + r * 8:ps * 576 + r * 8 + 7] = [sb + 3 * j for j in range(7)]
     locs = np.arange(n, dtype=np.int32)
     want = oracle.dequant_dsv4_cache(cache, locs, page_size=ps).astype(np.float64)
-    if path != "valu-f32":
+    if path in ("query-bf16", "split-bf16"):
         monkeypatch.setenv("CSAHCA_DSV4_QUERY", "1" if path == "query-bf16" else "0")
     q = torch.zeros(n, 1, 512, dtype=torch.float32 if path == "valu-f32" else torch.bfloat16, device=DEV)
     idx = torch.from_numpy(locs.reshape(n, 1)).to(DEV)
@@ -276,13 +276,84 @@ def test_query_kernel_dim_parts_give_the_same_bits(ratio, nq, heads, top_k, extr
     assert_close(outs["4"], oracle_out(c, sink=True), what="parts=4")
 
 
-@pytest.mark.parametrize("route", ["1", "0"])
+ONEPASS = [
+    # ratio, nq, heads, top_k, extra_top_k
+    (0, 1, 8, 128, 0),       # SWA window: 8 sub-tiles, one per wavefront
+    (4, 1, 8, 128, 64),      # 12 sub-tiles: wavefronts 0..3 take two
+    (128, 1, 64, 128, 64),   # 4 head groups of one query on one XCD
+    (4, 3, 24, 96, 40),      # second head group holds 8 heads
+    (4, 7, 70, 96, 40),      # 5 head groups, the last with 6 heads; 7 queries
+    (4, 2, 8, 5, 3),         # 8 slots: one partial sub-tile, seven idle wavefronts
+    (4, 9, 16, 40, 9),       # 9 queries: the grid's XCD mapping wraps
+    (0, 2, 16, 256, 0),      # 256 slots: every wavefront takes two full sub-tiles
+    (4, 32, 64, 128, 64),    # the benchmark's grouped-head shape class (2 dim parts)
+    (128, 32, 8, 128, 64),   # 4 dim parts
+]
+
+
+@pytest.mark.parametrize("ratio,nq,heads,top_k,extra_top_k", ONEPASS)
+def test_onepass_kernel_matches_oracle_and_query_kernel(ratio, nq, heads, top_k, extra_top_k, monkeypatch):
+    """The one-pass kernel (the default route for bf16 queries with at most
+    256 slots) against the oracle and against the per-query kernel
+    (CSAHCA_DSV4_QUERY=1), with ragged lengths, a -1 slot, a slot whose page is
+    past the cache, and with and without the sink."""
+    page = 256 if ratio == 128 else 64
+    c = make_dsv4_case(compress_ratio=ratio, num_queries=nq, heads=heads, num_tokens=1024, top_k=top_k,
+                       page_size=page, extra_tokens=1024, extra_top_k=extra_top_k, seed=41 + heads + top_k + nq,
+                       device=DEV)
+    c.token_indices[0, min(5, top_k - 1)] = -1
+    c.token_indices[-1, 0] = 10_000_000
+    for sink in (True, False):
+        ref = oracle_out(c, sink=sink)
+        got = gpu_out(c, sink=sink)
+        assert_close(got, ref, what=f"onepass sink={sink}")
+        monkeypatch.setenv("CSAHCA_DSV4_QUERY", "1")
+        assert_close(got, gpu_out(c, sink=sink).float().cpu().numpy().astype(np.float64), what="vs query kernel")
+        monkeypatch.delenv("CSAHCA_DSV4_QUERY")
+
+
+@pytest.mark.parametrize("ratio,nq,heads,top_k,extra_top_k", [(4, 7, 70, 96, 40), (128, 32, 64, 64, 64),
+                                                               (0, 9, 16, 128, 0)])
+def test_onepass_dim_parts_give_the_same_bits(ratio, nq, heads, top_k, extra_top_k, monkeypatch):
+    """Two or four workgroups per (query, 16 heads) (CSAHCA_DSV4_QPARTS), each
+    writing its share of the output dims, run the same scores, softmax and
+    output-block MFMA chains: identical outputs."""
+    page = 256 if ratio == 128 else 64
+    c = make_dsv4_case(compress_ratio=ratio, num_queries=nq, heads=heads, num_tokens=1024, top_k=top_k,
+                       page_size=page, extra_tokens=1024, extra_top_k=extra_top_k, seed=5 + nq + heads,
+                       device=DEV)
+    c.token_indices[0, 3] = -1
+    outs = {}
+    for parts in ("2", "4"):
+        monkeypatch.setenv("CSAHCA_DSV4_QPARTS", parts)
+        outs[parts] = gpu_out(c, sink=True)
+    assert torch.equal(outs["2"], outs["4"])
+    assert_close(outs["2"], oracle_out(c, sink=True), what="parts=2")
+
+
+def test_onepass_takes_lists_up_to_256_slots(monkeypatch):
+    """257 slots leave the one-pass kernel for the per-query kernel; both sides
+    of the boundary match the oracle, and CSAHCA_DSV4_ONEPASS=0 routes a
+    256-slot list to the per-query kernel with the same result."""
+    for top_k in (256, 257):
+        c = make_dsv4_case(compress_ratio=0, num_queries=4, heads=16, num_tokens=1024, top_k=top_k, page_size=64,
+                           seed=top_k, device=DEV)
+        ref = oracle_out(c)
+        got = gpu_out(c)
+        assert_close(got, ref, what=f"top_k={top_k}")
+        monkeypatch.setenv("CSAHCA_DSV4_ONEPASS", "0")
+        assert_close(gpu_out(c), ref, what=f"top_k={top_k} onepass off")
+        monkeypatch.delenv("CSAHCA_DSV4_ONEPASS")
+
+
+@pytest.mark.parametrize("route", ["onepass", "1", "0"])
 def test_scale_byte_255_gives_nan_like_the_reference(route, monkeypatch):
     """A scale byte of 255 is 2^128 = inf in the reference's fp32 dequant, so
     every score of that query is NaN (q . k meets inf) and so is its output;
     queries whose rows have no such byte stay finite and correct.  The MFMA
     kernels decode such sub-tiles in software."""
-    monkeypatch.setenv("CSAHCA_DSV4_QUERY", route)
+    if route != "onepass":
+        monkeypatch.setenv("CSAHCA_DSV4_QUERY", route)
     c = make_dsv4_case(compress_ratio=0, num_queries=3, heads=8, num_tokens=256, top_k=32, page_size=64, seed=9)
     cache = c.cache.clone()
     loc = int(c.token_indices[1, 3])
