@@ -259,6 +259,20 @@ __device__ __forceinline__ uint64_t get_raw(const uint64_t* p) {
   return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Launch epochs of a tagged exchange: an epoch word per exchange group holds
+// the tag of the last completed launch; kPoisonEpoch marks a group whose
+// exchange timed out (every later launch on it skips its waits and writes NaN
+// until the words are zero-filled again).
+constexpr uint32_t kPoisonEpoch = 0xffffffffu;
+
+// This launch's tag for a group whose epoch word reads `epoch` (never the
+// poison value; after 2^32 - 2 launches the sequence restarts at 1, and every
+// exchanged word is rewritten by each launch, so no stale word carries it).
+__device__ __forceinline__ uint32_t launch_tag(uint32_t epoch) {
+  const uint32_t t = epoch + 1u;
+  return t == kPoisonEpoch ? 1u : t;
+}
+
 // Value of lane (lane ^ off), off in {1, 2, 4, 8, 16, 32} (a constant once the
 // caller's loop is unrolled): DPP / row-swap moves, no LDS round trip.  The
 // whole wavefront must be active.

@@ -86,15 +86,6 @@ constexpr int kStepAttendUnroll = 4;  // K/V row loads per lane per batch
 constexpr int kRegMergeP = 8;         // partials per head merged from registers
 constexpr size_t kStepLds = 64 * 1024;
 constexpr uint32_t kSpinLimit = 1u << 20;  // polls per bounded wait (each with a short sleep)
-constexpr uint32_t kPoisonEpoch = 0xffffffffu;  // a head whose exchange timed out (see above)
-
-// This launch's tag for a head whose epoch word reads `epoch` (never the
-// poison value; after 2^32 - 2 launches the sequence restarts at 1, and every
-// exchanged word is rewritten by each launch, so no stale word carries it).
-__device__ __forceinline__ uint32_t launch_tag(uint32_t epoch) {
-  const uint32_t t = epoch + 1u;
-  return t == kPoisonEpoch ? 1u : t;
-}
 
 struct StepParams {
   const void* q;
