@@ -220,6 +220,7 @@ def csa_bench(args, B=1, H=8, S=32768, D=128, chunk=64, top_k=8, copies=None, se
     import torch
 
     from csahca_amd import native
+    from csahca_amd.tracing import op_range
 
     steps = args.steps if steps is None else steps
     warmup = args.warmup if warmup is None else warmup
@@ -280,7 +281,7 @@ def csa_bench(args, B=1, H=8, S=32768, D=128, chunk=64, top_k=8, copies=None, se
             native.device_clock_stamp(stamps, 1)
 
         graph = capture(s, [timed_steps])
-        with torch.cuda.stream(s):
+        with torch.cuda.stream(s), op_range(f"csahca.bench.steps_B{B}_S{S}_k{top_k}"):
             graph.replay()
         torch.cuda.synchronize()
         t = stamps.cpu().tolist()
@@ -291,7 +292,7 @@ def csa_bench(args, B=1, H=8, S=32768, D=128, chunk=64, top_k=8, copies=None, se
     if eager_pass or args.no_graph:
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        with torch.cuda.stream(s):
+        with torch.cuda.stream(s), op_range(f"csahca.bench.eager_B{B}_S{S}_k{top_k}"):
             run(steps)
         torch.cuda.synchronize()
         res["ms_per_step_eager"] = (time.perf_counter() - t0) * 1e3 / steps
@@ -534,7 +535,10 @@ def _dsv4_time(native, q, caches, idx, lens, ecaches, eidx, elens, sink, ps, eps
             call(copies - 1 - j)
     g = capture(s, [lambda j=j: call(j) for j in range(copies)])
     reps = max(1, steps // copies)
-    ms_graph = replay_timed(s, g, reps) / (reps * copies)
+    from csahca_amd.tracing import op_range
+
+    with op_range("csahca.bench.dsv4"):
+        ms_graph = replay_timed(s, g, reps) / (reps * copies)
     del g
     torch.cuda.synchronize()
     with torch.cuda.stream(s):

@@ -1,9 +1,17 @@
 """Build libcsahca.so (gfx950) in-tree with hipcc.
 
     python -m csahca_amd.build          # compile every source, link the library
+    python -m csahca_amd.build --sanitized   # also the host-sanitized variant
 
 Each HIP source compiles to an object under csahca_amd/_build/ and the objects
 link into csahca_amd/libcsahca.so, which csahca_amd.native loads with ctypes.
+Beside it: libcsahca_timeline.so (the decode step with phase stamps) and, on
+request, csahca_amd/_build/asan/libcsahca_asan.so -- the same sources with
+AddressSanitizer and UndefinedBehaviorSanitizer on the host side only (the
+argument checks, workspace sizing and launch set-up of every entry point; the
+device code is compiled as usual), for the CPU ABI tests
+(tests/test_abi_sanitized.py), which load it through CSAHCA_LIBRARY with the
+ASan runtime preloaded.
 """
 from __future__ import annotations
 
@@ -25,6 +33,12 @@ TIMELINE_SOURCE = "csa_step.hip"
 ARCH = os.environ.get("CSAHCA_OFFLOAD_ARCH", "gfx950")
 
 SOURCES = ["status.cpp", "csa.hip", "csa_step.hip", "dsv4.hip", "dsv4_pack.hip", "hca.hip", "block.hip"]
+ASAN_BUILD = BUILD / "asan"
+LIB_ASAN = ASAN_BUILD / "libcsahca_asan.so"
+# Host-side sanitizers only: each -fsanitize= applies to the host compilation
+# (-Xarch_host), the device code objects are the product's.
+SANITIZE_FLAGS = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+                  "-Xarch_host", "-fno-omit-frame-pointer", "-Xarch_host", "-fno-sanitize-recover=undefined"]
 
 COMMON_FLAGS = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
@@ -42,9 +56,9 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
 
 
-def _link(cc: str, objs, out: Path, verbose: bool) -> None:
+def _link(cc: str, objs, out: Path, verbose: bool, extra=()) -> None:
     tmp = out.with_suffix(".so.tmp")
-    cmd = [cc, "-shared", "-o", str(tmp)] + [str(o) for o in objs] + [f"--offload-arch={ARCH}"]
+    cmd = [cc, "-shared", "-o", str(tmp)] + [str(o) for o in objs] + [f"--offload-arch={ARCH}"] + list(extra)
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -53,25 +67,21 @@ def _link(cc: str, objs, out: Path, verbose: bool) -> None:
     os.replace(tmp, out)
 
 
-def build(verbose: bool = False, jobs: int | None = None) -> Path:
-    """Compile all sources (always) and link the shared library, and beside it
-    the phase-timeline variant (the decode step built with its stamps)."""
-    cc = hipcc()
-    BUILD.mkdir(exist_ok=True)
-    procs = []
-    objs = []
-    units = [(name, SRC / name, BUILD / (name.rsplit(".", 1)[0] + ".o"), []) for name in SOURCES]
-    tl_obj = BUILD / "csa_step_timeline.o"
-    units.append((TIMELINE_SOURCE + " (timeline)", SRC / TIMELINE_SOURCE, tl_obj, ["-DCSAHCA_STEP_TIMELINE"]))
-    for name, src, obj, extra in units:
-        if not extra:
-            objs.append(obj)
-        cmd = [cc, "-x", "hip", "-c", str(src), "-o", str(obj)] + COMMON_FLAGS + extra
-        if verbose:
-            print(" ".join(cmd), flush=True)
-        procs.append((name, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)))
-    failed = []
-    for name, p in procs:
+def _compile(cc: str, units, verbose: bool, jobs: int) -> None:
+    """Run the hipcc compile commands of `units` (name, source, object, extra
+    flags), at most `jobs` at a time; raise with the output of any failure."""
+    pending = list(units)
+    running, failed = [], []
+    while pending or running:
+        while pending and len(running) < jobs:
+            name, src, obj, extra = pending.pop(0)
+            obj.parent.mkdir(parents=True, exist_ok=True)
+            cmd = [cc, "-x", "hip", "-c", str(src), "-o", str(obj)] + COMMON_FLAGS + extra
+            if verbose:
+                print(" ".join(cmd), flush=True)
+            running.append((name, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
+                                                   text=True)))
+        name, p = running.pop(0)
         out, _ = p.communicate()
         if p.returncode != 0:
             failed.append((name, out))
@@ -80,11 +90,32 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     if failed:
         msg = "\n".join(f"--- {n} ---\n{o}" for n, o in failed)
         raise RuntimeError(f"hipcc failed:\n{msg}")
+
+
+def build(verbose: bool = False, jobs: int | None = None, sanitized: bool = False) -> Path:
+    """Compile all sources (always) and link the shared library, and beside it
+    the phase-timeline variant (the decode step built with its stamps); with
+    `sanitized`, also the host-sanitized variant (LIB_ASAN)."""
+    cc = hipcc()
+    BUILD.mkdir(exist_ok=True)
+    jobs = jobs or max(1, min(16, os.cpu_count() or 1))
+    objs = []
+    units = [(name, SRC / name, BUILD / (name.rsplit(".", 1)[0] + ".o"), []) for name in SOURCES]
+    objs = [u[2] for u in units]
+    tl_obj = BUILD / "csa_step_timeline.o"
+    units.append((TIMELINE_SOURCE + " (timeline)", SRC / TIMELINE_SOURCE, tl_obj, ["-DCSAHCA_STEP_TIMELINE"]))
+    asan_objs = [ASAN_BUILD / (name.rsplit(".", 1)[0] + ".o") for name in SOURCES]
+    if sanitized:
+        units += [(name + " (sanitized)", SRC / name, obj, ["-Xarch_host", "-O1", "-Xarch_host", "-g"] + SANITIZE_FLAGS)
+                  for name, obj in zip(SOURCES, asan_objs)]
+    _compile(cc, units, verbose, jobs)
     _link(cc, objs, LIB, verbose)
     step_obj = BUILD / (TIMELINE_SOURCE.rsplit(".", 1)[0] + ".o")
     _link(cc, [tl_obj if o == step_obj else o for o in objs], LIB_TIMELINE, verbose)
+    if sanitized:
+        _link(cc, asan_objs, LIB_ASAN, verbose, SANITIZE_FLAGS)
     return LIB
 
 
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    print(build(verbose="-v" in sys.argv, sanitized="--sanitized" in sys.argv))

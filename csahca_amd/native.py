@@ -16,15 +16,22 @@ New ops next to them: ``csa_chunk_summary``, ``csa_select_topk``,
 ``hca_decode_forward`` and ``hybrid_decode_forward``.
 
 There is no CPU fallback: without the built library every op raises.
+With CSAHCA_ROCTX=1 at import every op runs inside a roctx range named after
+it (csahca_amd.tracing).
 """
 from __future__ import annotations
 
 import ctypes
+import os
 from pathlib import Path
 
 import torch
 
-_LIB_PATH = Path(__file__).resolve().parent / "libcsahca.so"
+from .tracing import traced
+
+# CSAHCA_LIBRARY names another build of the library to load (the host-sanitized
+# variant for the sanitizer tests); by default the in-tree libcsahca.so.
+_LIB_PATH = Path(os.environ.get("CSAHCA_LIBRARY") or Path(__file__).resolve().parent / "libcsahca.so")
 _LIB = None
 
 _DTYPES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2, torch.float64: 3}
@@ -199,6 +206,7 @@ def _csa_checks(q, k_cache, v_cache, chunk_indices, chunk_size, tiled: bool, til
     _check(q.dtype in _FLOATING, f"unsupported dtype {q.dtype}")
 
 
+@traced
 def csa_decode_forward(q, k_cache, v_cache, chunk_indices, chunk_size):
     """Sparse decode over explicit chunk ids (reference op csa_decode_forward)."""
     chunk_size = int(chunk_size)
@@ -216,6 +224,7 @@ def csa_decode_forward(q, k_cache, v_cache, chunk_indices, chunk_size):
     return out
 
 
+@traced
 def csa_decode_forward_tiled(q, k_cache, v_cache, chunk_indices, chunk_size, tile_size):
     """Split-KV sparse decode (reference op csa_decode_forward_tiled)."""
     chunk_size, tile_size = int(chunk_size), int(tile_size)
@@ -241,6 +250,7 @@ def csa_auto_tile_size(batch: int, heads: int, top_k: int, chunk_size: int) -> i
     return int(lib().csahca_csa_auto_tile_size(batch, heads, top_k, chunk_size))
 
 
+@traced
 def csa_chunk_summary(k_cache, chunk_size, *, out=None, chunk_begin: int = 0, num_chunks: int | None = None):
     """fp32 chunk means of K (chunk_mean, hybrid_attention/reference.py:40-45).
 
@@ -270,6 +280,7 @@ def csa_chunk_summary(k_cache, chunk_size, *, out=None, chunk_begin: int = 0, nu
     return out
 
 
+@traced
 def csa_chunk_summary_at(k_cache, summary, chunk_size, token_pos):
     """Recompute in place the summary of the chunk that the token at
     ``token_pos`` (a one-element int64 CUDA tensor, read on the device)
@@ -293,6 +304,7 @@ def csa_chunk_summary_at(k_cache, summary, chunk_size, token_pos):
     return summary
 
 
+@traced
 def csa_select_topk(q, summary, top_k):
     """Top-k chunk ids by q . summary / sqrt(D) (select_topk_chunks scoring,
     hybrid_attention/reference.py:51-56).  int32 ``[B, H, min(top_k, C)]``, best
@@ -359,6 +371,7 @@ def release_step_workspaces() -> None:
     _SCRATCH_WS.clear()
 
 
+@traced
 def csa_decode_step(q, k_cache, v_cache, summary, chunk_size, top_k, tile_size: int = 0):
     """One CSA decode step from cached summaries in one launch: select the top-k
     chunks (as csa_select_topk), then attend over their tokens (as
@@ -399,6 +412,7 @@ NOALLOC_MAX_CHUNKS = 2048    # summary rows per head
 NOALLOC_MAX_HEAD_DIM = 256
 
 
+@traced
 def csa_decode_step_noalloc(q, k_cache, v_cache, summary, chunk_size, top_k, *, out, indices):
     """csa_decode_step through the library's allocation-free entry point: the
     exchange state lives in a static per-device array, so neither the library
@@ -427,6 +441,7 @@ def csa_decode_step_noalloc(q, k_cache, v_cache, summary, chunk_size, top_k, *, 
     return out, indices
 
 
+@traced
 def csa_decode_step_dev(q, k_cache, v_cache, summary, num_chunks, chunk_size, top_k, *, out=None, indices=None):
     """csa_decode_step with the chunk count in device memory: ``summary`` holds
     ``max_chunks`` rows per head and the step selects among the first
@@ -480,6 +495,7 @@ def block_linear_supported(x: torch.Tensor, weight: torch.Tensor) -> bool:
             and x.data_ptr() % 16 == 0 and weight.data_ptr() % 16 == 0)
 
 
+@traced
 def block_linear(x, weight, *, norm_weight=None, eps: float = 1e-6, activation=None, residual=None, base=None,
                  alpha: float = 1.0, out=None, advance_pos=None):
     """Decode-step product ``base + alpha * (act(x' @ weight.T) + residual)`` for
@@ -519,6 +535,7 @@ def block_linear(x, weight, *, norm_weight=None, eps: float = 1e-6, activation=N
     return out
 
 
+@traced
 def block_qkv(hidden, w_qkv, q, k_cache, v_cache, token_pos, *, norm_weight=None, eps: float = 1e-6,
               num_chunks=None, chunk_size: int = 64):
     """QKV projection of a decode step over a growing cache: RMSNorm(hidden)
@@ -548,6 +565,7 @@ def block_qkv(hidden, w_qkv, q, k_cache, v_cache, token_pos, *, norm_weight=None
     return q
 
 
+@traced
 def csa_decode_step_at(q, k_cache, v_cache, summary, token_pos, chunk_size, top_k, *, out=None, indices=None):
     """The decode step of the token at ``token_pos`` (one-element int64 CUDA
     tensor, read on the device) just appended to a growing cache: the chunks in
@@ -617,6 +635,7 @@ def csa_step_noalloc_reset(device=None) -> None:
         _rc(lib().csahca_csa_step_noalloc_reset(_stream()))
 
 
+@traced
 def hca_decode_forward(q, k_cache, v_cache, chunk_size, *, blend=None, csa_weight: float = 0.7):
     """hca_reference (hybrid_attention/reference.py:87-92) on the GPU: dense
     attention over the chunk means of K and V, both rounded to the storage
@@ -645,6 +664,7 @@ def hca_decode_forward(q, k_cache, v_cache, chunk_size, *, blend=None, csa_weigh
     return out
 
 
+@traced
 def hybrid_decode_forward(q, k_cache, v_cache, *, csa_chunk_size: int, csa_top_k: int, hca_chunk_size: int,
                           csa_weight: float = 0.7, summary=None):
     """hybrid_reference (hybrid_attention/reference.py:95-108) on the GPU: the
@@ -737,6 +757,7 @@ def _opt(t):
     return t if _present(t) else None
 
 
+@traced
 def dsv4_decode_forward_tiled(q, paged_k_cache_u8, token_indices, topk_lengths, extra_paged_k_cache_u8,
                               extra_token_indices, extra_topk_lengths, attn_sink, page_size, extra_page_size,
                               tile_size, softmax_scale):
@@ -783,6 +804,7 @@ def dsv4_decode_forward_tiled(q, paged_k_cache_u8, token_indices, topk_lengths, 
     return out
 
 
+@traced
 def dsv4_swa_decode_forward(q, paged_k_cache_u8, token_indices, topk_lengths, attn_sink, page_size,
                             softmax_scale):
     """Reference op dsv4_swa_decode_forward (SWA slots only)."""
@@ -804,6 +826,7 @@ def dsv4_swa_decode_forward(q, paged_k_cache_u8, token_indices, topk_lengths, at
     return out
 
 
+@traced
 def dsv4_sparse_decode_forward(q, paged_k_cache_u8, token_indices, topk_lengths, extra_paged_k_cache_u8,
                                extra_token_indices, extra_topk_lengths, attn_sink, page_size, extra_page_size,
                                softmax_scale):
@@ -884,6 +907,7 @@ class profile_launches:
         return False
 
 
+@traced
 def dsv4_pack_tokens(k_tokens, page_size, *, cache=None, locs=None):
     """pack_dsv4_cache (hybrid_attention/dsv4_correctness.py:24-59) on the GPU:
     quantise [T, 512] bf16 tokens into the paged FP8 layout.  Without ``cache``

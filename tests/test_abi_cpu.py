@@ -262,3 +262,54 @@ def test_reference_module_name_resolves_to_native_ops(monkeypatch):
                  "dsv4_sparse_decode_forward", "dsv4_decode_forward_tiled"):
         assert getattr(mod, name) is getattr(native, name)
     sys.modules.pop("hybrid_attention_cuda", None)
+
+
+def test_workspace_sizes_over_the_shape_range(lib):
+    """Every *_workspace_bytes function over ordinary and extreme shapes:
+    negative sizes give 0, sizes grow with the shape, and no shape makes the
+    host arithmetic misbehave (the sanitized build runs this under UBSan)."""
+    big = 1 << 40
+    for B, H, C, D, k, chunk in [(1, 8, 512, 128, 8, 64), (32, 8, 2048, 128, 32, 64), (1, 1, 1, 64, 1, 1),
+                                 (0, 8, 512, 128, 8, 64), (1, 8, 0, 128, 8, 64), (-1, 8, 512, 128, 8, 64)]:
+        n = lib.csahca_csa_step_workspace_bytes(B, H, C, D, k, chunk)
+        assert (n == 0) == (B < 0)
+        t = lib.csahca_csa_decode_workspace_bytes(B, H, D, k, chunk, 8)
+        assert t >= 0
+    assert lib.csahca_csa_step_workspace_bytes(1, 8, 512, 128, 8, 0) == 0
+    assert lib.csahca_csa_step_workspace_bytes(32, 8, 2048, 128, 32, 64) > \
+        lib.csahca_csa_step_workspace_bytes(1, 8, 512, 128, 8, 64)
+    for nq, H, T, E, tile in [(1, 8, 128, 0, 0), (32, 64, 128, 64, 0), (32, 64, 600, 64, 16), (0, 8, 128, 0, 0),
+                              (-1, 8, 128, 0, 0)]:
+        n = lib.csahca_dsv4_decode_workspace_bytes(nq, H, T, E, tile)
+        assert (n == 0) == (nq <= 0)  # no query, or a negative size: no workspace
+    assert lib.csahca_hca_decode_workspace_bytes(1, 8, 32768, 128, 256) >= 8 * 128 * (1 + 128) * 4
+    assert lib.csahca_csa_select_workspace_bytes(32, 8, 2048) == 32 * 8 * 2048 * 4
+    for f in (lib.csahca_csa_auto_tile_size,):
+        assert f(1, 8, 8, 64) > 0 and f(32, 8, 32, 64) > 0
+    # sizes far past any device: the functions still return without faulting
+    lib.csahca_csa_select_workspace_bytes(big, 8, 2048)
+    lib.csahca_dsv4_decode_workspace_bytes(1 << 20, 64, 1 << 16, 64, 0)
+
+
+def test_roctx_ranges_only_when_asked():
+    """Without CSAHCA_ROCTX the ops are the undecorated functions; with
+    CSAHCA_ROCTX=1 at import each op is wrapped in a roctx range named after
+    it, and ranges open and close (depth 0 after the pop) without a profiler."""
+    import subprocess
+    import sys
+
+    from csahca_amd import tracing
+
+    assert not hasattr(native.csa_decode_step, "__wrapped__")
+    code = ("from csahca_amd import native, tracing\n"
+            "assert tracing.ENABLED and native.csa_decode_step.__wrapped__.__name__ == 'csa_decode_step'\n"
+            "assert native.dsv4_decode_forward_tiled.__wrapped__ is not None\n"
+            "d = tracing.push('csahca.test'); assert d >= 0, d\n"
+            "assert tracing.pop() >= 0\n"
+            "with tracing.op_range('csahca.block'): pass\n"
+            "print('ok')\n")
+    env = dict(__import__("os").environ, CSAHCA_ROCTX="1")
+    r = subprocess.run([sys.executable, "-c", code], cwd=ROOT, env=env, capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0 and "ok" in r.stdout, r.stderr[-2000:]
+    with tracing.op_range("csahca.noop"):  # disabled: no library needed
+        pass
