@@ -176,6 +176,32 @@ __device__ __forceinline__ uint32_t wave_sort_desc(uint32_t x, int lane) {
   return merge_desc<32>(x, lane);
 }
 
+// The k-th largest (k <= 8) of one value per lane, in every lane: each block
+// of 8 lanes is sorted descending (6 stages, as wave_sort_desc's first
+// three merges but with every block descending), then three levels merge
+// blocks 8, 16 and 32 lanes apart: lane i of a block takes the larger of its
+// value and lane 7 - i of the partner block (a mirrored permute), which leaves
+// the top 8 of both blocks as a bitonic sequence, and a 3-stage merge sorts
+// it descending again.  18 stages against the full sort's 21; afterwards
+// every block holds the wavefront's top 8 in descending order.
+__device__ __forceinline__ uint32_t wave_top8_desc(uint32_t x, int lane) {
+  x ^= lane_bit_mask<1>(lane);
+  x = merge_desc<1>(x, lane);
+  x ^= lane_bit_mask<1>(lane) ^ lane_bit_mask<2>(lane);
+  x = merge_desc<2>(x, lane);
+  x ^= lane_bit_mask<2>(lane);
+  x = merge_desc<4>(x, lane);
+  uint32_t p = dpp_mov<0x140>(x);  // row_mirror: lane ^ 15 (the block 8 lanes away, mirrored)
+  x = x > p ? x : p;
+  x = merge_desc<4>(x, lane);
+  p = dpp_mov<0x141>(lane_xor<16>(x, lane));  // half_row_mirror after the row swap: lane ^ 16 ^ 7
+  x = x > p ? x : p;
+  x = merge_desc<4>(x, lane);
+  p = dpp_mov<0x141>(lane_xor<32>(x, lane));  // lane ^ 32 ^ 7
+  x = x > p ? x : p;
+  return merge_desc<4>(x, lane);
+}
+
 // ---------------------------------------------------------------------------
 // Top-k for k <= 64, executed by ONE wavefront.  On gfx950 every dependent
 // hop between the vector and the scalar unit (a compare whose mask feeds a
@@ -187,11 +213,14 @@ __device__ __forceinline__ uint32_t wave_sort_desc(uint32_t x, int lane) {
 //      distinct lanes: chunks at a common stride of at least M, and any
 //      contiguous run of at most 63 chunks; their maxima then sit in
 //      different lanes and step 2 finds a tight threshold;
-//   2. the 64 lane maxima are sorted by a bitonic network of lane permutes
-//      (no LDS) and t = the k-th largest lane maximum: at least k keys are
-//      >= t and every key of the answer is >= t;
+//   2. t = the k-th largest of the 64 lane maxima, from a network of lane
+//      permutes (no LDS): the top-8 network for k <= 8, else the full
+//      bitonic sort.  At least k keys are >= t and every key of the answer is
+//      >= t;
 //   3. keys >= t are compacted into LDS as unique composites
-//      (key << 32 | ~position), ballot + mbcnt giving the slots;
+//      (key << 32 | ~position) in one pass: each lane counts its candidates,
+//      one ballot per bit of the counts and mbcnt give every lane its first
+//      slot (no scalar count carried from key to key);
 //   4. with n <= 64 candidates, lane j ranks composite j by counting the
 //      larger composites from broadcast reads (16 per batch, one LDS wait
 //      each); composite order is exactly the declared order (larger key
@@ -216,22 +245,31 @@ __device__ bool wave_topk_regs(const uint32_t* keys, int C, int k, uint32_t* scr
   uint32_t mx = 0;
 #pragma unroll
   for (int j = 0; j < M; ++j) mx = v[j] > mx ? v[j] : mx;
-  const uint32_t t =
-      static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(wave_sort_desc(mx, lane)), k - 1));
+  const uint32_t srt = k <= 8 ? wave_top8_desc(mx, lane) : wave_sort_desc(mx, lane);
+  const uint32_t t = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(srt), k - 1));
   if (t == 0u) return false;
   wave_lds_sync();  // the clears above land before any compacted store
-  int n = 0;
+  // Positions past C hold key 0 < t, so no bound check is needed.
+  int cnt = 0;
+#pragma unroll
+  for (int j = 0; j < M; ++j) cnt += v[j] >= t ? 1 : 0;
+  // This lane's first slot = the candidates of the lanes below it, bit by bit
+  // of the counts (0 .. M); n = all candidates.
+  int slot = 0, n = 0;
+#pragma unroll
+  for (int b = 0; (1 << b) <= M; ++b) {
+    const unsigned long long bal = __ballot((cnt >> b) & 1);
+    slot += lanes_below(bal) << b;
+    n += __popcll(bal) << b;
+  }
 #pragma unroll
   for (int j = 0; j < M; ++j) {
-    // Positions past C hold key 0 < t, so no bound check is needed.  Lanes
-    // without a candidate (or past 64 candidates) store to the dummy slot.
+    // Keys below t (and candidates past 64) store to the dummy slot.
     const bool take = v[j] >= t;
-    const unsigned long long bal = __ballot(take);
-    int slot = n + lanes_below(bal) + (take ? 0 : kWave);
-    slot = slot < kWave ? slot : kWave;
+    const int sj = take && slot < kWave ? slot : kWave;
     const uint32_t pos = static_cast<uint32_t>(kWave * j + ((lane - j) & (kWave - 1)));
-    cand[slot] = (static_cast<unsigned long long>(v[j]) << 32) | static_cast<uint32_t>(~pos);
-    n += __popcll(bal);
+    cand[sj] = (static_cast<unsigned long long>(v[j]) << 32) | static_cast<uint32_t>(~pos);
+    slot += take ? 1 : 0;
   }
   if (n > kWave) return false;
   wave_lds_sync();
