@@ -1185,14 +1185,15 @@ __global__ __launch_bounds__(W * kWave) void dsv4_query_kernel(const bf16* __res
 }
 
 // ---------------------------------------------------------------------------
-// One-pass grouped-head kernel (dsv4_onepass_kernel): slot lists of at most
-// kOpMaxSlots slots.  A workgroup of kOpWaves wavefronts is one (query, 16
-// heads, dim part), as for dsv4_query_kernel, but nothing runs in rounds:
-//   1. every lane requests the indices of its two slots, the lengths, the
+// One-pass grouped-head kernel (dsv4_onepass_kernel<NW, SUBS, DS>): slot
+// lists of at most NW * SUBS * 16 slots.  A workgroup of NW wavefronts is one
+// (query, 16 heads, dim part), as for dsv4_query_kernel, but nothing runs in
+// rounds:
+//   1. every lane requests the indices of its SUBS slots, the lengths, the
 //      query rows (staged in LDS) and the sink; then, as soon as the indices
-//      arrive, the latent rows of both its sub-tiles -- wavefront w owns
-//      sub-tiles w and w + kOpWaves of 16 slots, so the whole slot list is in
-//      flight after two dependent round trips;
+//      arrive, the latent rows of its sub-tiles -- wavefront w owns sub-tiles
+//      w, w + NW, ... of 16 slots, so the whole slot list is in flight after
+//      two dependent round trips;
 //   2. each wavefront reads its B operand of S^T = K Q^T (the 16 query rows)
 //      from LDS into registers once, then per sub-tile dequantises the rows
 //      straight into MFMA A operands -- the contraction runs over the dims in
@@ -1204,44 +1205,54 @@ __global__ __launch_bounds__(W * kWave) void dsv4_query_kernel(const bf16* __res
 //   3. one exact softmax per head over the whole list: per-wavefront maxima
 //      through LDS, then p = 2^(s - M) (fp32 sums, bf16 operands for PV)
 //      written as P^T rows in LDS;
-//   4. O^T = V^T P^T on v_mfma_f32_16x16x16_bf16 for the wavefront's 16-dim
-//      output blocks over all sub-tiles (V^T through ds_read_b64_tr_b16), and
-//      the sink as a virtual token of logit sink[h] and value 0
-//      (csrc/dsv4_attention.cu:252-269).
+//   4. O^T = V^T P^T on v_mfma_f32_16x16x16_bf16 for the workgroup's 16-dim
+//      output blocks (dealt to the wavefronts round-robin) over all sub-tiles
+//      (V^T through ds_read_b64_tr_b16), and the sink as a virtual token of
+//      logit sink[h] and value 0 (csrc/dsv4_attention.cu:252-269).
+// Two shapes: 12 wavefronts with one sub-tile each (lists of up to 192 slots:
+// every wavefront's QK is one sub-tile, so no wavefront serialises two; the
+// query staging has LDS of its own) and 8 wavefronts with two each (up to
+// 256; the V tiles then take the staging's LDS once the operand is read).
 // Scores, probabilities and sums are those of the other MFMA kernels up to
-// fp32 summation order (the softmax subtracts the exact maximum).
-constexpr int kOpWaves = 8;
-constexpr int kOpSubs = 2;                                // 16-slot sub-tiles per wavefront
-constexpr int kOpMaxSlots = kOpWaves * kOpSubs * kQSub;   // 256
-constexpr int kOpProw = 272;  // P^T row stride in bf16 (136 dwords = 8 mod 64 banks)
+// fp32 summation order (the softmax subtracts the exact maximum).  Each output
+// block's MFMA chain is the same in every shape and dim-part count; the
+// softmax sum adds per-wavefront partial sums, so the two shapes can differ in
+// its last bits.
+constexpr int kOpMaxSlots = 256;  // the largest list of the one-pass shapes
+constexpr int kOpProw = 272;      // P^T row stride in bf16 (136 dwords = 8 mod 64 banks)
 
-template <int DS>
+template <int NW, int SUBS, int DS>
 struct OnePassLayout {
+  static constexpr int SLOTS = NW * SUBS * kQSub;          // capacity
   static constexpr int DW = kDim / DS;                     // output dims of a workgroup
   static constexpr int VROW = DW + 24;                     // V tile row in bf16 (dwords = 12 mod 64)
-  static constexpr int OB = DW / kOpWaves / 16;            // 16-dim output blocks per wavefront
-  static constexpr int TILE_BYTES = kOpMaxSlots * VROW * 2;
-  static constexpr int Q_BYTES = kQHeads * kQQRow * 2;     // query staging (aliases the V tiles)
-  static constexpr int R0 = TILE_BYTES > Q_BYTES ? TILE_BYTES : Q_BYTES;
+  static constexpr int NB = DW / 16;                       // 16-dim output blocks of the workgroup
+  static constexpr int OB = (NB + NW - 1) / NW;            // blocks per wavefront (at most)
+  static constexpr int TILE_BYTES = SLOTS * VROW * 2;
+  static constexpr int Q_BYTES = kQHeads * kQQRow * 2;     // query staging
+  static constexpr int SMALL = NW * 16 * 4 * 2 + kQHeads * kOpProw * 2;  // maxima, sums, P^T
+  static constexpr bool ALIAS = TILE_BYTES + Q_BYTES + SMALL > 160 * 1024;  // staging inside the V tiles
+  static constexpr int QS = ALIAS ? 0 : TILE_BYTES;        // query staging offset
+  static constexpr int R0 = ALIAS ? (TILE_BYTES > Q_BYTES ? TILE_BYTES : Q_BYTES) : TILE_BYTES + Q_BYTES;
   static constexpr int MX = R0;                            // [waves][16] maxima
-  static constexpr int LS = MX + kOpWaves * 16 * 4;        // [waves][16] sums
-  static constexpr int PT = LS + kOpWaves * 16 * 4;        // [16 heads][kOpProw] bf16
+  static constexpr int LS = MX + NW * 16 * 4;              // [waves][16] sums
+  static constexpr int PT = LS + NW * 16 * 4;              // [16 heads][kOpProw] bf16
   static constexpr int BYTES = PT + kQHeads * kOpProw * 2;
-  static_assert(OB >= 1, "at least one 16-dim block per wavefront");
+  static_assert(SLOTS <= kOpMaxSlots, "P^T rows hold kOpMaxSlots slots");
   static_assert(BYTES <= 160 * 1024, "LDS of one workgroup");
 };
 
-template <int DS>
-__global__ __launch_bounds__(kOpWaves * kWave) void dsv4_onepass_kernel(const bf16* __restrict__ q, Dsv4Args a,
-                                                                        QueryArgs g) {
-  using Lay = OnePassLayout<DS>;
-  constexpr int NW = kOpWaves;
+template <int NW, int SUBS, int DS>
+__global__ __launch_bounds__(NW * kWave) void dsv4_onepass_kernel(const bf16* __restrict__ q, Dsv4Args a,
+                                                                   QueryArgs g) {
+  using Lay = OnePassLayout<NW, SUBS, DS>;
   constexpr int NT = NW * kWave;
-  constexpr int DW = Lay::DW, VROW = Lay::VROW, OB = Lay::OB;
-  constexpr int QQU = kQHeads * (kDim / 8) / NT;  // 16-byte query units per thread
+  constexpr int DW = Lay::DW, VROW = Lay::VROW, NB = Lay::NB, OB = Lay::OB;
+  constexpr int QUNITS = kQHeads * (kDim / 8);              // 16-byte query units of the workgroup
+  constexpr int QQU = (QUNITS + NT - 1) / NT;               // per thread
   __shared__ __align__(16) uint8_t smem[Lay::BYTES];
   uint16_t* vtile = reinterpret_cast<uint16_t*>(smem);
-  uint16_t* qlds = reinterpret_cast<uint16_t*>(smem);  // before the V tiles are written
+  uint16_t* qlds = reinterpret_cast<uint16_t*>(smem + Lay::QS);
   float* mxs = reinterpret_cast<float*>(smem + Lay::MX);
   float* lss = reinterpret_cast<float*>(smem + Lay::LS);
   uint16_t* pt = reinterpret_cast<uint16_t*>(smem + Lay::PT);
@@ -1269,9 +1280,9 @@ __global__ __launch_bounds__(kOpWaves * kWave) void dsv4_onepass_kernel(const bf
   const int32_t len_raw = load_global_i32(a.lens ? static_cast<const void*>(a.lens + query) : anyp);
   const int32_t elen_raw = load_global_i32(a.elens ? static_cast<const void*>(a.elens + query) : anyp);
   const uint8_t* dummy = reinterpret_cast<const uint8_t*>(q + (query * a.heads + h0) * kDim);  // >= 1 KiB, in bounds
-  int32_t li[kOpSubs], le[kOpSubs];
+  int32_t li[SUBS], le[SUBS];
 #pragma unroll
-  for (int j = 0; j < kOpSubs; ++j) {
+  for (int j = 0; j < SUBS; ++j) {
     const int s = (wave + NW * j) * kQSub + l16;
     const int32_t* ip = a.topk_slots > 0 ? a.idx + query * a.topk_slots + min(s, a.topk_slots - 1)
                                          : reinterpret_cast<const int32_t*>(dummy);
@@ -1284,19 +1295,20 @@ __global__ __launch_bounds__(kOpWaves * kWave) void dsv4_onepass_kernel(const bf
   uint4 qw[QQU];
 #pragma unroll
   for (int u = 0; u < QQU; ++u) {
-    const int e = tid + NT * u;
+    const int e = min(tid + NT * u, QUNITS - 1);  // (units past the last re-read it; not stored)
     qw[u] = load_global_u4(q + (query * a.heads + h0 + min(e / (kDim / 8), nh - 1)) * kDim + 8 * (e % (kDim / 8)));
   }
   // (unconditional: a load under a branch would make the wait-count pass wait
   // for every load in flight at the join)
   const float sink_raw = load_global_raw<float>(g.sink ? static_cast<const void*>(g.sink + h0 + min(l16, nh - 1))
                                                        : anyp);
-  asm volatile("" : "+v"(li[0]), "+v"(le[0]), "+v"(li[1]), "+v"(le[1]));
+#pragma unroll
+  for (int j = 0; j < SUBS; ++j) asm volatile("" : "+v"(li[j]), "+v"(le[j]));
   const int n_swa = a.lens ? max(0, min(len_raw, a.topk_slots)) : a.topk_slots;
   const int n_extra = a.extra_slots > 0 ? (a.elens ? max(0, min(elen_raw, a.extra_slots)) : a.extra_slots) : 0;
-  QRows rw[kOpSubs];
+  QRows rw[SUBS];
 #pragma unroll
-  for (int j = 0; j < kOpSubs; ++j) {
+  for (int j = 0; j < SUBS; ++j) {
     const int s = (wave + NW * j) * kQSub + l16;
     const bool in_swa = s < a.topk_slots;
     const bool valid = s < total && (in_swa ? s < n_swa : s - a.topk_slots < n_extra);
@@ -1317,8 +1329,9 @@ __global__ __launch_bounds__(kOpWaves * kWave) void dsv4_onepass_kernel(const bf
 #pragma unroll
   for (int u = 0; u < QQU; ++u) {
     const int e = tid + NT * u;
-    *reinterpret_cast<uint4*>(qlds + (e / (kDim / 8)) * kQQRow + 8 * (e % (kDim / 8))) =
-        e / (kDim / 8) < nh ? qw[u] : make_uint4(0u, 0u, 0u, 0u);
+    if (e < QUNITS)
+      *reinterpret_cast<uint4*>(qlds + (e / (kDim / 8)) * kQQRow + 8 * (e % (kDim / 8))) =
+          e / (kDim / 8) < nh ? qw[u] : make_uint4(0u, 0u, 0u, 0u);
   }
   lds_barrier();
   uint4 qb[16];  // B operand of k-step t: head l16, the dims of this lane group's chunk for t
@@ -1330,11 +1343,11 @@ __global__ __launch_bounds__(kOpWaves * kWave) void dsv4_onepass_kernel(const bf
 #pragma unroll
     for (int t = 14; t < 16; ++t) qb[t] = *reinterpret_cast<const uint4*>(qrow + kNope + 8 * (grp + 4 * (t - 14)));
   }
-  lds_barrier();  // the query staging is overwritten by the V tiles below
+  if constexpr (Lay::ALIAS) lds_barrier();  // the query staging is overwritten by the V tiles below
 
-  float x[kOpSubs][4];
+  float x[SUBS][4];
 #pragma unroll
-  for (int j = 0; j < kOpSubs; ++j) {
+  for (int j = 0; j < SUBS; ++j) {
     const int u = wave + NW * j;  // global sub-tile (wave-uniform)
     if (u >= nsub) {
 #pragma unroll
@@ -1397,7 +1410,7 @@ __global__ __launch_bounds__(kOpWaves * kWave) void dsv4_onepass_kernel(const bf
   // ---- 3. softmax over the whole slot list ----------------------------------
   float mw = -INFINITY;
 #pragma unroll
-  for (int j = 0; j < kOpSubs; ++j)
+  for (int j = 0; j < SUBS; ++j)
 #pragma unroll
     for (int e = 0; e < 4; ++e) mw = fmaxf(mw, x[j][e]);
   mw = fmaxf(mw, __uint_as_float(lane_xor<16>(__float_as_uint(mw), lane)));
@@ -1409,7 +1422,7 @@ __global__ __launch_bounds__(kOpWaves * kWave) void dsv4_onepass_kernel(const bf
   for (int w = 0; w < NW; ++w) M = fmaxf(M, mxs[w * 16 + l16]);
   float ps = 0.f;
 #pragma unroll
-  for (int j = 0; j < kOpSubs; ++j) {
+  for (int j = 0; j < SUBS; ++j) {
     float p[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -1433,18 +1446,23 @@ __global__ __launch_bounds__(kOpWaves * kWave) void dsv4_onepass_kernel(const bf
   f32x4_t o[OB];
 #pragma unroll
   for (int j = 0; j < OB; ++j) o[j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  // V^T A operand of block j (dims (DW / NW) wave + 16 j .. of this part) of
-  // sub-tile u: lane a of group g passes &V[16 u + 4 g + a / 4][... + 4 (a % 4)].
-  const uint16_t* vbase = vtile + (4 * grp + l16 / 4) * VROW + 4 * (l16 % 4) + (DW / NW) * wave;
+  // V^T A operand of output block b (dims 16 b .. of this part) of sub-tile
+  // u: lane a of group g passes &V[16 u + 4 g + a / 4][16 b + 4 (a % 4)].
+  // This wavefront's blocks are wave, wave + NW, ... (< NB; wave-uniform).
+  const uint16_t* vbase = vtile + (4 * grp + l16 / 4) * VROW + 4 * (l16 % 4) + 16 * wave;
   const uint16_t* pbase = pt + l16 * kOpProw + 4 * grp;
-  for (int u = 0; u < nsub; ++u) {
-    const i16x4_t pb = __builtin_bit_cast(i16x4_t, *reinterpret_cast<const uint2*>(pbase + u * kQSub));
-    i16x4_t vt[OB];
+  if (wave < NB) {
+    for (int u = 0; u < nsub; ++u) {
+      const i16x4_t pb = __builtin_bit_cast(i16x4_t, *reinterpret_cast<const uint2*>(pbase + u * kQSub));
+      i16x4_t vt[OB];
 #pragma unroll
-    for (int j = 0; j < OB; ++j)
-      vt[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(vbase + u * kQSub * VROW + 16 * j));
+      for (int j = 0; j < OB; ++j)
+        if (wave + NW * j < NB)
+          vt[j] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)(vbase + u * kQSub * VROW + 16 * NW * j));
 #pragma unroll
-    for (int j = 0; j < OB; ++j) o[j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt[j], pb, o[j], 0, 0, 0);
+      for (int j = 0; j < OB; ++j)
+        if (wave + NW * j < NB) o[j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt[j], pb, o[j], 0, 0, 0);
+    }
   }
   const float sk = g.sink ? sink_raw * kLog2e : -INFINITY;
   const float mx = L > 0.f ? fmaxf(sk, M) : sk;
@@ -1453,11 +1471,12 @@ __global__ __launch_bounds__(kOpWaves * kWave) void dsv4_onepass_kernel(const bf
   if (g.sink && mx != -INFINITY) Lt += fast_exp2(sk - mx);
   const float sc = L != L ? __builtin_nanf("") : (Lt > 0.f ? wgt / Lt : 0.f);
   if (l16 < nh) {
-    bf16* orow = g.out + (query * a.heads + h0 + l16) * kDim + DW * part + (DW / NW) * wave + 4 * grp;
+    bf16* orow = g.out + (query * a.heads + h0 + l16) * kDim + DW * part + 16 * wave + 4 * grp;
 #pragma unroll
     for (int j = 0; j < OB; ++j)
-      *reinterpret_cast<uint2*>(orow + 16 * j) =
-          make_uint2(bf16x2_nb(o[j][0] * sc, o[j][1] * sc), bf16x2_nb(o[j][2] * sc, o[j][3] * sc));
+      if (wave + NW * j < NB)
+        *reinterpret_cast<uint2*>(orow + 16 * NW * j) =
+            make_uint2(bf16x2_nb(o[j][0] * sc, o[j][1] * sc), bf16x2_nb(o[j][2] * sc, o[j][3] * sc));
   }
 }
 
@@ -1773,9 +1792,14 @@ int dsv4_run(const Dsv4Call& c) {
     // query q's (group, part) pairs x: blocks q%8 + 8 (x + G DS q/8)
     const int64_t blocks = ceil_div(c.nq, 8) * 8 * qa.groups * ds;
     CSAHCA_REQUIRE(blocks <= INT32_MAX, "too many DSV4 work items");
-    auto kfn = ds == 4 ? dsv4_onepass_kernel<4> : dsv4_onepass_kernel<2>;
-    return launch("dsv4_onepass_kernel", kfn, dim3(static_cast<uint32_t>(blocks)), dim3(kOpWaves * kWave), 0,
-                  stream, static_cast<const bf16*>(c.q), a, qa);
+    // 12 wavefronts with one sub-tile each for lists of up to 192 slots, else
+    // 8 with two (CSAHCA_DSV4_OPWAVES=8 / 12 forces either where it fits).
+    const char* ew = std::getenv("CSAHCA_DSV4_OPWAVES");
+    const bool w12 = ew ? (std::atoi(ew) == 12 && total <= 12 * kQSub) : total <= 12 * kQSub;
+    auto kfn = w12 ? (ds == 4 ? dsv4_onepass_kernel<12, 1, 4> : dsv4_onepass_kernel<12, 1, 2>)
+                   : (ds == 4 ? dsv4_onepass_kernel<8, 2, 4> : dsv4_onepass_kernel<8, 2, 2>);
+    return launch("dsv4_onepass_kernel", kfn, dim3(static_cast<uint32_t>(blocks)), dim3((w12 ? 12 : 8) * kWave),
+                  0, stream, static_cast<const bf16*>(c.q), a, qa);
   }
   if (use_mfma && reinterpret_cast<uintptr_t>(c.out) % 8 == 0 && use_query_kernel(c.nq, c.heads, total)) {
     QueryArgs qa;

@@ -145,6 +145,18 @@ def _workspace(nbytes: int, device) -> torch.Tensor:
 
 
 _SCRATCH_WS: dict = {}
+_WS_BYTES: dict = {}
+
+
+def _ws_bytes(fn_name: str, *args) -> int:
+    """A workspace-size query of the library, memoised per (function, shape):
+    the sizes are pure functions of their arguments."""
+    key = (fn_name,) + args
+    n = _WS_BYTES.get(key)
+    if n is None:
+        n = int(getattr(lib(), fn_name)(*args))
+        _WS_BYTES[key] = n
+    return n
 
 
 def _scratch_workspace(nbytes: int, dev: int, stream: int) -> torch.Tensor:
@@ -237,7 +249,7 @@ def csa_decode_forward_tiled(q, k_cache, v_cache, chunk_indices, chunk_size, til
             return csa_decode_forward_tiled(q, k_cache, v_cache, chunk_indices, chunk_size, tile_size)
     stream = _raw_stream(dev)
     out = torch.empty_like(q)
-    nbytes = lib().csahca_csa_decode_workspace_bytes(B, H, D, top_k, chunk_size, tile_size)
+    nbytes = _ws_bytes("csahca_csa_decode_workspace_bytes", B, H, D, top_k, chunk_size, tile_size)
     ws = _scratch_workspace(nbytes, dev, stream)
     _rc(lib().csahca_csa_decode_forward_tiled(
         q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), chunk_indices.data_ptr(), out.data_ptr(),
@@ -790,8 +802,8 @@ def dsv4_decode_forward_tiled(q, paged_k_cache_u8, token_indices, topk_lengths, 
     if nq == 0 or heads == 0:
         return out
     stream = _raw_stream(dev)
-    ws = _scratch_workspace(lib().csahca_dsv4_decode_workspace_bytes(nq, heads, token_indices.shape[1], extra_slots,
-                                                                     tile_size), dev, stream)
+    ws = _scratch_workspace(_ws_bytes("csahca_dsv4_decode_workspace_bytes", nq, heads, token_indices.shape[1],
+                                      extra_slots, tile_size), dev, stream)
     ec = extra_paged_k_cache_u8 if has_extra else None
     _rc(lib().csahca_dsv4_decode_forward_tiled(
         q.data_ptr(), _DTYPES[q.dtype], nq, heads, paged_k_cache_u8.data_ptr(), paged_k_cache_u8.shape[0],

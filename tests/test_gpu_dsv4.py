@@ -331,6 +331,26 @@ def test_onepass_dim_parts_give_the_same_bits(ratio, nq, heads, top_k, extra_top
     assert_close(outs["2"], oracle_out(c, sink=True), what="parts=2")
 
 
+@pytest.mark.parametrize("ratio,nq,heads,top_k,extra_top_k", [(4, 3, 24, 128, 64), (0, 9, 16, 128, 0),
+                                                               (4, 2, 8, 5, 3), (128, 32, 64, 128, 64)])
+@pytest.mark.parametrize("waves", ["8", "12"])
+def test_onepass_shapes_match_the_oracle(ratio, nq, heads, top_k, extra_top_k, waves, monkeypatch):
+    """Lists of up to 192 slots run with 12 wavefronts of one sub-tile each by
+    default; CSAHCA_DSV4_OPWAVES=8 forces the 8-wavefront shape (two sub-tiles
+    each).  Both against the oracle, with ragged lengths and a -1 slot, and with
+    two and four dim parts."""
+    page = 256 if ratio == 128 else 64
+    c = make_dsv4_case(compress_ratio=ratio, num_queries=nq, heads=heads, num_tokens=1024, top_k=top_k,
+                       page_size=page, extra_tokens=1024, extra_top_k=extra_top_k, seed=13 + nq + heads,
+                       device=DEV)
+    c.token_indices[0, min(3, top_k - 1)] = -1
+    monkeypatch.setenv("CSAHCA_DSV4_OPWAVES", waves)
+    for parts in ("2", "4"):
+        monkeypatch.setenv("CSAHCA_DSV4_QPARTS", parts)
+        for sink in (True, False):
+            assert_close(gpu_out(c, sink=sink), oracle_out(c, sink=sink), what=f"waves={waves} parts={parts}")
+
+
 def test_onepass_takes_lists_up_to_256_slots(monkeypatch):
     """257 slots leave the one-pass kernel for the per-query kernel; both sides
     of the boundary match the oracle, and CSAHCA_DSV4_ONEPASS=0 routes a
