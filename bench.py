@@ -265,17 +265,19 @@ def csa_bench(args, B=1, H=8, S=32768, D=128, chunk=64, top_k=8, copies=None, se
         # the steps on the device, back to back, and the graph's own launch --
         # including a freshly captured graph's first-launch setup -- falls
         # before the first stamp.  Step i reads copy (c0 + i) mod copies.  An
-        # untimed pre-roll over the copies outside the timed window (at most
-        # PRE_ROLL steps, each copy once) opens the graph: the device idles
-        # while the host captures, and the pre-roll brings it back to the
-        # steady state of a decode loop before the first stamp.
+        # untimed pre-roll of PRE_ROLL steps over the copies outside the timed
+        # window (cycling over them; the timed copies are not touched, so they
+        # are as cold as before) opens the graph: the device idles while the
+        # host captures, and the pre-roll brings it back to the steady state
+        # of a decode loop before the first stamp.
         c0 = cursor
-        npre = min(PRE_ROLL, copies - steps) if copies > steps else 0
+        spare = copies - steps
+        npre = PRE_ROLL if spare > 0 else 0
         stamps = torch.zeros(2, dtype=torch.int64, device=q.device)
 
         def timed_steps():
             for i in range(npre):
-                step((c0 + steps + i) % copies)
+                step((c0 + steps + i % spare) % copies)
             native.device_clock_stamp(stamps, 0)
             for i in range(steps):
                 step((c0 + i) % copies)

@@ -49,6 +49,15 @@ COMMON_FLAGS = [
 ]
 
 
+# Per-source device flags.  csa_step.hip: the decode step's leading scalar
+# parameters (the StepLead fields: 8 arguments, 14 dwords) are preloaded into
+# SGPRs at wave launch, so its first loads need no argument load.  (Kernels
+# whose first parameter is a struct are unaffected: preloading stops there.)
+SOURCE_FLAGS = {
+    "csa_step.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=8"],
+}
+
+
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and Path(cand).exists():
@@ -100,13 +109,16 @@ def build(verbose: bool = False, jobs: int | None = None, sanitized: bool = Fals
     BUILD.mkdir(exist_ok=True)
     jobs = jobs or max(1, min(16, os.cpu_count() or 1))
     objs = []
-    units = [(name, SRC / name, BUILD / (name.rsplit(".", 1)[0] + ".o"), []) for name in SOURCES]
+    units = [(name, SRC / name, BUILD / (name.rsplit(".", 1)[0] + ".o"), list(SOURCE_FLAGS.get(name, [])))
+             for name in SOURCES]
     objs = [u[2] for u in units]
     tl_obj = BUILD / "csa_step_timeline.o"
-    units.append((TIMELINE_SOURCE + " (timeline)", SRC / TIMELINE_SOURCE, tl_obj, ["-DCSAHCA_STEP_TIMELINE"]))
+    units.append((TIMELINE_SOURCE + " (timeline)", SRC / TIMELINE_SOURCE, tl_obj,
+                  ["-DCSAHCA_STEP_TIMELINE"] + SOURCE_FLAGS.get(TIMELINE_SOURCE, [])))
     asan_objs = [ASAN_BUILD / (name.rsplit(".", 1)[0] + ".o") for name in SOURCES]
     if sanitized:
-        units += [(name + " (sanitized)", SRC / name, obj, ["-Xarch_host", "-O1", "-Xarch_host", "-g"] + SANITIZE_FLAGS)
+        units += [(name + " (sanitized)", SRC / name, obj,
+                   ["-Xarch_host", "-O1", "-Xarch_host", "-g"] + SANITIZE_FLAGS + SOURCE_FLAGS.get(name, []))
                   for name, obj in zip(SOURCES, asan_objs)]
     _compile(cc, units, verbose, jobs)
     _link(cc, objs, LIB, verbose)

@@ -152,17 +152,20 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
   constexpr int B8 = 8;                              // tagged key loads issued per batch
   constexpr int kGather = 24;                        // tagged partial loads per thread per batch
 
-  // LDS: top-k scratch | hist[256] | skey[k] | sidx[k] | sel[k] | count | comb |
-  //      keys[max(C, P*(D+2))] (the head's keys, later the gathered partials)
+  // LDS: keys[max(Cs, P*(D+2))] (the head's keys, later the gathered
+  //      partials; first, so that its address needs only preloaded arguments)
+  //      | top-k scratch (16-byte aligned) | hist[256] | skey[k] | sidx[k] |
+  //      sel[k] | count | comb
   extern __shared__ uint64_t smem64[];
-  uint32_t* tk_scratch = reinterpret_cast<uint32_t*>(smem64);
+  uint32_t* keys_l = reinterpret_cast<uint32_t*>(smem64);
+  const int64_t keys_words = max<int64_t>(a.Cs, a.P > 1 ? int64_t{a.P} * (D + 2) : 0);
+  uint32_t* tk_scratch = keys_l + ((keys_words + 3) & ~int64_t{3});
   uint32_t* hist = tk_scratch + kTopkScratchWords;
   uint32_t* skey = hist + 256;
   int32_t* sidx = reinterpret_cast<int32_t*>(skey + a.topk);
   int32_t* sel = sidx + a.topk;
   uint32_t* lcount = reinterpret_cast<uint32_t*>(sel + a.topk);
   float* comb = reinterpret_cast<float*>(lcount + 1);
-  uint32_t* keys_l = reinterpret_cast<uint32_t*>(comb + W * (D + 2));
 
   const int tid = threadIdx.x;
   const int wave = tid / kWave;
@@ -171,35 +174,39 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
   const uint32_t cb = a.colo_bh;
   const int64_t h = cb ? block % cb : block / P;
   const int p = static_cast<int>(cb ? block / cb : block % P);
-  // Test switch only (the host sets mute_p = -1 otherwise): this workgroup
-  // publishes no key and no partial, so its partners' bounded waits expire.
-  const bool mute = h == 0 && p == a.mute_p;
   const int64_t Cs = a.Cs;
-  // Chunks in play: the host's count, or the device's (its load overlaps the
-  // summary loads of phase A, which are laid out over the Cs rows), or the
-  // count implied by the device position of the token just appended.
-  // (POS: the position mode, a separate instantiation so that the count
-  // modes compile without it.)
-  int64_t C = POS ? Cs : (a.c_dev ? min<int64_t>(max<int32_t>(*a.c_dev, 0), Cs) : a.C);
-  // Position mode: the count is set in phase A, after its loads are issued
-  // (the position is requested with them).
+  // Loads that depend on nothing are issued together, unconditionally, and
+  // consumed only after the summary rows are requested, so phase A costs one
+  // memory round trip: this launch's tag for the head (epoch + 1; every head
+  // has an epoch word, read even when P = 1), the device count or position,
+  // q in the summary lane layout, and the summary rows.  (They need only the
+  // preloaded arguments and the block index.)
+  const uint32_t epoch = __hip_atomic_load(&a.epoch[h], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // Chunks in play: the host's count, or the device's, or the count implied
+  // by the device position of the token just appended (POS: the position
+  // mode, a separate instantiation so that the count modes compile without
+  // it).  The device count and the position are requested here, with an
+  // unconditional load (the epoch word stands in for an absent count), and
+  // applied in phase A where the keys are published, after its row loads.
+  int64_t C = Cs;  // the count modes set it in phase A (count_from_device)
+  const bool c_on_dev = !POS && a.c_dev != nullptr;
+  int32_t c_raw = 0;
+  if constexpr (!POS)
+    c_raw = load_global_raw<int32_t>(c_on_dev ? a.c_dev : reinterpret_cast<const int32_t*>(a.epoch + h));
+  auto count_from_device = [&]() {
+    int32_t v = c_raw;
+    asm volatile("" : "+v"(v));  // consumed only here, after the row loads
+    C = c_on_dev ? min<int64_t>(max<int32_t>(v, 0), Cs) : a.C;
+  };
   int64_t pos_raw = 0;
   if constexpr (POS) pos_raw = load_global_raw<int64_t>(a.pos_dev);
   const T* __restrict__ q = static_cast<const T*>(a.q) + h * D;
   CSAHCA_STAMP(0);
 
-  // Loads that depend on nothing are issued together, unconditionally, and
-  // consumed only after the summary rows are requested, so phase A costs one
-  // memory round trip: this launch's tag for the head (epoch + 1; every head
-  // has an epoch word, read even when P = 1), q in the summary lane layout,
-  // and the summary rows.
-  const uint32_t epoch = __hip_atomic_load(&a.epoch[h], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-
   // ---- A: order keys of this workgroup's chunk range ----------------------
   {
     const int grp = lane / SLPR, col = lane % SLPR;
     const float* __restrict__ sb = a.summary + h * Cs * D + col * 4;
-    uint64_t* kg = a.keys + h * a.key_stride;
     // This workgroup's rows: 32-bit division whenever Cs * P fits (every
     // practical shape); a 64-bit division is a long scalar sequence on the
     // critical path of the step.
@@ -239,6 +246,11 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
       // hoisting its use above the row loads.
       uint32_t ep = epoch;
       asm volatile("" : "+v"(ep));
+      uint64_t* kg = a.keys + h * a.key_stride;
+      // Test switch only (the host sets mute_p = -1 otherwise): this workgroup
+      // publishes no key and no partial, so its partners' bounded waits expire.
+      const bool mute = h == 0 && p == a.mute_p;
+      if constexpr (!POS) count_from_device();
       if constexpr (POS) {
         // The token at pos was just appended: n = pos + 1 tokens, C complete
         // chunks.  If it completes chunk C - 1 and this block of rows holds
@@ -309,12 +321,21 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
       // Batch by batch: the rows, then q -- the newest load, so waiting for it
       // covers them all: one round trip per batch (one batch per wavefront in
       // the latency-bound shapes; with two workgroups on a CU, one waits while
-      // the other computes).
-      for (int64_t blk = c0; blk < c1; blk += kScoreStride) {
+      // the other computes).  The first batch is requested before the loop,
+      // so that what the compiler hoists into the loop's preheader (the key
+      // words' address and other non-preloaded arguments, with the wait for
+      // their loads) comes after it.
+      if (c0 < c1) {
         uint4 rs[US];
-        issue_rows(blk, rs);
-        const uint4 q4 = load_q4();
-        score_rows(blk, rs, q4);
+        issue_rows(c0, rs);
+        uint4 q4 = load_q4();
+        for (int64_t blk = c0;;) {
+          score_rows(blk, rs, q4);
+          blk += kScoreStride;
+          if (blk >= c1) break;
+          issue_rows(blk, rs);
+          q4 = load_q4();
+        }
       }
     } else {
       // Several batches, double-buffered: batch i + 1 is requested before batch
@@ -338,6 +359,8 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
     }
   }
 
+  // (A workgroup with no summary rows scored none.)
+  if constexpr (!POS) count_from_device();
   CSAHCA_STAMP(1);
   // ---- B: gather the head's keys, top-k -----------------------------------
   const uint32_t tag = launch_tag(epoch);
@@ -456,6 +479,7 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
   // until it carries this launch's tag: no arrival counter, so no atomic round
   // trip between the last partial and the merge.
   uint64_t* pp = a.part + h * a.part_stride + p * static_cast<int64_t>(D + 2);
+  const bool mute = h == 0 && p == a.mute_p;  // the test switch of phase A
   if (!mute) {
     if (d < D) put_tagged(pp + 2 + d, tag, __float_as_uint(A));
     if (tid == 0) {
@@ -595,8 +619,51 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
     __hip_atomic_store(&a.epoch[h], LL != LL ? kPoisonEpoch : tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Every argument of the step, requested from the kernel-argument segment in
+// one batch at entry.  Left to itself the compiler loads each argument where
+// it is first used: the head/workgroup division waited for one scalar load,
+// the pointers of phase A for a second one issued after it -- two dependent
+// round trips before the first summary load.
+__device__ __forceinline__ void step_args_at_entry(const StepParams& a) {
+  asm volatile("" ::"s"(a.q), "s"(a.summary), "s"(a.kcache), "s"(a.vcache), "s"(a.out), "s"(a.idx_out),
+               "s"(a.status), "s"(a.epoch), "s"(a.keys), "s"(a.part), "s"(a.key_stride), "s"(a.part_stride));
+  asm volatile("" ::"s"(a.S), "s"(a.C), "s"(a.Cs), "s"(a.c_dev), "s"(a.pos_dev), "s"(a.summary_out),
+               "s"(a.chunk), "s"(a.chunk_shift), "s"(a.topk), "s"(a.P), "s"(a.colo_bh), "s"(a.score_scale),
+               "s"(a.qscale), "s"(a.spin_limit), "s"(a.mute_p));
+}
+
+// The arguments phase A needs first also lead the kernel's parameter list as
+// scalars (StepLead), which the library is built to preload into SGPRs at
+// wave launch (-amdgpu-kernarg-preload-count): the summary and q addresses
+// and the epoch word are requested without waiting for any argument load.
+struct StepLead {
+  const float* summary;
+  const void* q;
+  uint32_t* epoch;
+  int64_t Cs;
+  const int32_t* c_dev;
+  const int64_t* pos_dev;
+  uint32_t colo_bh;
+  int32_t P;
+};
+
+__host__ __device__ inline StepLead step_lead_of(const StepParams& a) {
+  return StepLead{a.summary, a.q, a.epoch, a.Cs, a.c_dev, a.pos_dev, a.colo_bh, a.P};
+}
+
 template <typename T, int D, int TOPK_M, bool POS, bool PIPE = false, int W = kStepWaves>
-__global__ __launch_bounds__(W * kWave) void csa_step_kernel(StepParams a) {
+__global__ __launch_bounds__(W * kWave) void csa_step_kernel(const float* summary, const void* q, uint32_t* epoch,
+                                                             int64_t Cs, const int32_t* c_dev,
+                                                             const int64_t* pos_dev, uint32_t colo_bh, int32_t P,
+                                                             StepParams a) {
+  a.summary = summary;
+  a.q = q;
+  a.epoch = epoch;
+  a.Cs = Cs;
+  a.c_dev = c_dev;
+  a.pos_dev = pos_dev;
+  a.colo_bh = colo_bh;
+  a.P = P;
   csa_step_body<T, D, TOPK_M, POS, PIPE, W>(a, blockIdx.x);
 }
 
@@ -662,7 +729,8 @@ int64_t env_wgs_per_head() {
   return s ? std::max<int64_t>(0, std::atoll(s)) : 0;
 }
 
-using StepKernelFn = void (*)(StepParams);
+using StepKernelFn = void (*)(const float*, const void*, uint32_t*, int64_t, const int32_t*, const int64_t*, uint32_t,
+                              int32_t, StepParams);
 using HybridKernelFn = void (*)(StepParams, HcaPart, uint32_t);
 
 // The instantiation of the step kernel a call launches (m: top-k register rows).
@@ -895,9 +963,11 @@ int decode_step_impl(const void* q, const void* k_cache, const void* v_cache, co
   }
   P = std::min<int64_t>({P, rg.max_p, ceil_div(num_chunks, 8), ceil_div(k * chunk_size, 16)});
   P = std::max<int64_t>(1, P);
-  // keys region: the head's C keys, later (P > 1) the P gathered partials
+  // keys region (first, its size rounded to 16 bytes): the head's C keys,
+  // later (P > 1) the P gathered partials
   auto lds_for = [&](int64_t np) {
-    return lds_base + static_cast<size_t>(std::max<int64_t>(num_chunks, np > 1 ? np * (head_dim + 2) : 0)) * 4;
+    const int64_t words = std::max<int64_t>(num_chunks, np > 1 ? np * (head_dim + 2) : 0);
+    return lds_base + static_cast<size_t>((words + 3) & ~int64_t{3}) * 4;
   };
   size_t lds = lds_for(P);
   if (k > 0 && k <= kStepMaxK && fused_dtype && fused_dim && aligned && ncu > 0 && lds <= kStepLds) {
@@ -975,8 +1045,9 @@ int decode_step_impl(const void* q, const void* k_cache, const void* v_cache, co
     }
     if (wide) {
       const StepKernelFn wf = step_kernel_wide(dtype, head_dim, m);
+      const StepLead ld = step_lead_of(pr);
       return launch("csa_step_kernel", wf, dim3(static_cast<uint32_t>(bh)), dim3(kWideWaves * kWave), lds, stream,
-                    pr);
+                    ld.summary, ld.q, ld.epoch, ld.Cs, ld.c_dev, ld.pos_dev, ld.colo_bh, ld.P, pr);
     }
     StepKernelFn run = sfn;
     // (only where some wavefront has more than one batch of rows to walk)
@@ -986,8 +1057,9 @@ int decode_step_impl(const void* q, const void* k_cache, const void* v_cache, co
     if (pos_dev == nullptr && bh * P <= ncu && batches) {
       if (const StepKernelFn pf = step_kernel_pipelined(dtype, head_dim, m)) run = pf;
     }
+    const StepLead ld = step_lead_of(pr);
     return launch("csa_step_kernel", run, dim3(static_cast<uint32_t>(bh * P)), dim3(kStepThreads), lds, stream,
-                  pr);
+                  ld.summary, ld.q, ld.epoch, ld.Cs, ld.c_dev, ld.pos_dev, ld.colo_bh, ld.P, pr);
   }
   if (fixed != nullptr)
     return fail(CSAHCA_ERR_ARGUMENT,
