@@ -55,6 +55,7 @@ COMMON_FLAGS = [
 # whose first parameter is a struct are unaffected: preloading stops there.)
 SOURCE_FLAGS = {
     "csa_step.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=8"],
+    "dsv4.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=9"],
 }
 
 

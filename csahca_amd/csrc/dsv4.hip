@@ -1243,8 +1243,24 @@ struct OnePassLayout {
 };
 
 template <int NW, int SUBS, int DS>
-__global__ __launch_bounds__(NW * kWave) void dsv4_onepass_kernel(const bf16* __restrict__ q, Dsv4Args a,
+__global__ __launch_bounds__(NW * kWave) void dsv4_onepass_kernel(const int32_t* idx, const int32_t* eidx,
+                                                                   const int32_t* lens, const int32_t* elens,
+                                                                   int32_t topk_slots, int32_t extra_slots,
+                                                                   int32_t groups, int32_t nq, int32_t heads,
+                                                                   const bf16* __restrict__ q, Dsv4Args a,
                                                                    QueryArgs g) {
+  // The leading scalars repeat what the slot-index loads need (the library
+  // preloads them into SGPRs at wave launch); the copies in a and g are the
+  // same values.
+  a.idx = idx;
+  a.eidx = eidx;
+  a.lens = lens;
+  a.elens = elens;
+  a.topk_slots = topk_slots;
+  a.extra_slots = extra_slots;
+  a.heads = heads;
+  g.groups = groups;
+  g.nq = nq;
   using Lay = OnePassLayout<NW, SUBS, DS>;
   constexpr int NT = NW * kWave;
   constexpr int DW = Lay::DW, VROW = Lay::VROW, NB = Lay::NB, OB = Lay::OB;
@@ -1276,19 +1292,20 @@ __global__ __launch_bounds__(NW * kWave) void dsv4_onepass_kernel(const bf16* __
   const int total = a.topk_slots + a.extra_slots;
 
   // ---- 1. indices, lengths, query rows, sink; then the rows -----------------
-  const void* anyp = static_cast<const void*>(q);
+  // The index and length loads need only the preloaded arguments: an absent
+  // list or length reads the query's first index of the other list instead
+  // (the list is never empty here), not the query rows.
+  const int32_t* anyi = a.topk_slots > 0 ? a.idx + query * a.topk_slots : a.eidx + query * a.extra_slots;
+  const void* anyp = static_cast<const void*>(anyi);
   const int32_t len_raw = load_global_i32(a.lens ? static_cast<const void*>(a.lens + query) : anyp);
   const int32_t elen_raw = load_global_i32(a.elens ? static_cast<const void*>(a.elens + query) : anyp);
-  const uint8_t* dummy = reinterpret_cast<const uint8_t*>(q + (query * a.heads + h0) * kDim);  // >= 1 KiB, in bounds
   int32_t li[SUBS], le[SUBS];
 #pragma unroll
   for (int j = 0; j < SUBS; ++j) {
     const int s = (wave + NW * j) * kQSub + l16;
-    const int32_t* ip = a.topk_slots > 0 ? a.idx + query * a.topk_slots + min(s, a.topk_slots - 1)
-                                         : reinterpret_cast<const int32_t*>(dummy);
-    const int32_t* ep = a.extra_slots > 0
-                            ? a.eidx + query * a.extra_slots + min(max(s - a.topk_slots, 0), a.extra_slots - 1)
-                            : reinterpret_cast<const int32_t*>(dummy);
+    const int32_t* ip = a.topk_slots > 0 ? a.idx + query * a.topk_slots + min(s, a.topk_slots - 1) : anyi;
+    const int32_t* ep =
+        a.extra_slots > 0 ? a.eidx + query * a.extra_slots + min(max(s - a.topk_slots, 0), a.extra_slots - 1) : anyi;
     li[j] = load_global_i32(ip);
     le[j] = load_global_i32(ep);
   }
@@ -1302,6 +1319,14 @@ __global__ __launch_bounds__(NW * kWave) void dsv4_onepass_kernel(const bf16* __
   // for every load in flight at the join)
   const float sink_raw = load_global_raw<float>(g.sink ? static_cast<const void*>(g.sink + h0 + min(l16, nh - 1))
                                                        : anyp);
+  // The rows of invalid slots re-read a query row (>= 1 KiB, in bounds).
+  const uint8_t* dummy = reinterpret_cast<const uint8_t*>(q + (query * a.heads + h0) * kDim);
+  // The cache views the row addresses need, requested now, while the slot
+  // indices are in flight (left to itself the compiler loads them where the
+  // addresses are formed: one more dependent round trip after the indices).
+  asm volatile("" ::"s"(a.swa.base), "s"(a.swa.num_pages), "s"(a.swa.bpp), "s"(a.swa.page_size),
+               "s"(a.swa.page_shift), "s"(a.extra.base), "s"(a.extra.num_pages), "s"(a.extra.bpp),
+               "s"(a.extra.page_size), "s"(a.extra.page_shift));
 #pragma unroll
   for (int j = 0; j < SUBS; ++j) asm volatile("" : "+v"(li[j]), "+v"(le[j]));
   const int n_swa = a.lens ? max(0, min(len_raw, a.topk_slots)) : a.topk_slots;
@@ -1799,7 +1824,8 @@ int dsv4_run(const Dsv4Call& c) {
     auto kfn = w12 ? (ds == 4 ? dsv4_onepass_kernel<12, 1, 4> : dsv4_onepass_kernel<12, 1, 2>)
                    : (ds == 4 ? dsv4_onepass_kernel<8, 2, 4> : dsv4_onepass_kernel<8, 2, 2>);
     return launch("dsv4_onepass_kernel", kfn, dim3(static_cast<uint32_t>(blocks)), dim3((w12 ? 12 : 8) * kWave),
-                  0, stream, static_cast<const bf16*>(c.q), a, qa);
+                  0, stream, a.idx, a.eidx, a.lens, a.elens, a.topk_slots, a.extra_slots, qa.groups,
+                  static_cast<int32_t>(qa.nq), a.heads, static_cast<const bf16*>(c.q), a, qa);
   }
   if (use_mfma && reinterpret_cast<uintptr_t>(c.out) % 8 == 0 && use_query_kernel(c.nq, c.heads, total)) {
     QueryArgs qa;
