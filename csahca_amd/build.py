@@ -56,6 +56,7 @@ COMMON_FLAGS = [
 SOURCE_FLAGS = {
     "csa_step.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=8"],
     "dsv4.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=9"],
+    "block.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=8"],
 }
 
 

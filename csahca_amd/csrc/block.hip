@@ -66,7 +66,22 @@ __device__ __forceinline__ float round_t(float v) {
 }
 
 template <typename T, int KV, int BB, int EPI>
-__global__ __launch_bounds__(kGemvThreads) void block_gemv_kernel(GemvArgs a) {
+// The leading scalars repeat the arguments of the kernel's one batch of loads
+// (x, the weights, the norm weight, the residual and base rows, the sizes);
+// the library preloads them into SGPRs at wave launch, so the weight stream
+// is requested without waiting for an argument load.  The copies in `a` are
+// the same values.
+__global__ __launch_bounds__(kGemvThreads) void block_gemv_kernel(const void* x_, const void* w_, const void* norm,
+                                                                  const void* res, const void* base, int32_t B,
+                                                                  int32_t N, int32_t K, GemvArgs a) {
+  a.x = x_;
+  a.w = w_;
+  a.norm = norm;
+  a.res = res;
+  a.base = base;
+  a.B = B;
+  a.N = N;
+  a.K = K;
   constexpr int RW = kRowsPerWave;
   constexpr int NV = BB * RW;  // outputs of a wavefront
   const int lane = threadIdx.x % kWave;
@@ -206,8 +221,10 @@ template <typename T, int KV, int BB>
 int launch_gemv_epi(int epi, const GemvArgs& a, dim3 grid, hipStream_t stream) {
   const dim3 block(kGemvThreads);
   return epi == kEpiQkv
-             ? launch("block_gemv_kernel", block_gemv_kernel<T, KV, BB, kEpiQkv>, grid, block, 0, stream, a)
-             : launch("block_gemv_kernel", block_gemv_kernel<T, KV, BB, kEpiGeneral>, grid, block, 0, stream, a);
+             ? launch("block_gemv_kernel", block_gemv_kernel<T, KV, BB, kEpiQkv>, grid, block, 0, stream, a.x, a.w,
+                      a.norm, a.res, a.base, a.B, a.N, a.K, a)
+             : launch("block_gemv_kernel", block_gemv_kernel<T, KV, BB, kEpiGeneral>, grid, block, 0, stream, a.x,
+                      a.w, a.norm, a.res, a.base, a.B, a.N, a.K, a);
 }
 
 template <typename T, int KV>
