@@ -57,6 +57,8 @@ SOURCE_FLAGS = {
     "csa_step.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=8"],
     "dsv4.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=9"],
     "block.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=8"],
+    "csa.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"],
+    "hca.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"],
 }
 
 

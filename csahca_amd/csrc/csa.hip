@@ -26,12 +26,16 @@ namespace {
 // ---------------------------------------------------------------------------
 // Split-KV sparse attention (vectorised path).
 // ---------------------------------------------------------------------------
+// Parameter order: what the chunk-id load, the K/V row addresses and q need
+// comes first (14 dwords, preloaded into SGPRs at wave launch: the library
+// builds this file with -amdgpu-kernarg-preload-count), the outputs after;
+// the chunk shift is formed here from the chunk size.
 template <typename T, typename IdxT, int D, int U>
 __global__ __launch_bounds__(64) void csa_attend_vec_kernel(
-    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v,
-    const IdxT* __restrict__ idx, float* __restrict__ part_ml, float* __restrict__ part_acc,
-    int64_t seq_len, int top_k, int chunk, int chunk_shift, int tile, int num_tiles,
-    float qscale) {
+    const IdxT* __restrict__ idx, int64_t seq_len, const T* __restrict__ k, const T* __restrict__ v,
+    const T* __restrict__ q, int num_tiles, int top_k, int tile, int chunk, float* __restrict__ part_ml,
+    float* __restrict__ part_acc, float qscale) {
+  const int chunk_shift = (chunk & (chunk - 1)) == 0 ? __builtin_ctz(static_cast<uint32_t>(chunk)) : -1;
   using L = AttendLayout<T, D>;
   constexpr int VEC = L::VEC, LPR = L::LPR, RPL = L::RPL;
   const int lane = threadIdx.x;
@@ -539,8 +543,8 @@ int launch_attend(const void* q, const void* k, const void* v, const void* idx, 
   if (aligned && D == DD && (DD / VEC) <= kWave) {                                           \
     return launch("csa_attend_vec_kernel",                                                   \
                   csa_attend_vec_kernel<T, IdxT, (DD / VEC <= kWave ? DD : VEC), 4>, grid,   \
-                  dim3(kWave), 0, stream, qp, kp, vp, ip, part_ml, part_acc, S, top_k, chunk, \
-                  cshift, tile, num_tiles, qscale);                                          \
+                  dim3(kWave), 0, stream, ip, S, kp, vp, qp, num_tiles, top_k, tile, chunk,    \
+                  part_ml, part_acc, qscale);                                                \
   }
   CSAHCA_ATTEND_VEC(64)
   CSAHCA_ATTEND_VEC(128)

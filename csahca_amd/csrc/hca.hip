@@ -32,14 +32,17 @@ namespace {
 
 constexpr int kHcaProbChunk = 2048;  // probabilities staged in LDS per pass
 
+// Parameter order: the inputs of the first loads (q, K, V and the sizes that
+// place them) lead, so they fit the 14 dwords preloaded into SGPRs at wave
+// launch (the library builds this file with -amdgpu-kernarg-preload-count);
+// the outputs and the scale, needed at the end, follow.
 template <typename T, bool kVec>
 __global__ __launch_bounds__(kHcaThreads) void hca_chunk_kernel(const T* __restrict__ q,
                                                               const T* __restrict__ k,
-                                                              const T* __restrict__ v,
+                                                              const T* __restrict__ v, int64_t S,
+                                                              int64_t C, int D, int chunk,
                                                               float* __restrict__ scores,
-                                                              float* __restrict__ means, int64_t S,
-                                                              int D, int chunk, int64_t C,
-                                                              float scale) {
+                                                              float* __restrict__ means, float scale) {
   hca_chunk_body<T, kVec>(q, k, v, scores, means, S, D, chunk, C, scale, blockIdx.x);
 }
 
@@ -202,9 +205,9 @@ extern "C" int csahca_hca_decode_forward(const void* q, const void* k_cache, con
     const T* vp = static_cast<const T*>(v_cache);
     const int rc =
         vec ? launch("hca_chunk_kernel", hca_chunk_kernel<T, true>, grid, dim3(kHcaThreads), lds, stream, qp,
-                     kp, vp, scores, means, seq_len, D, static_cast<int>(chunk_size), C, scale)
+                     kp, vp, seq_len, C, D, static_cast<int>(chunk_size), scores, means, scale)
             : launch("hca_chunk_kernel", hca_chunk_kernel<T, false>, grid, dim3(kHcaThreads), lds, stream, qp,
-                     kp, vp, scores, means, seq_len, D, static_cast<int>(chunk_size), C, scale);
+                     kp, vp, seq_len, C, D, static_cast<int>(chunk_size), scores, means, scale);
     if (rc != CSAHCA_OK) return rc;
     const int col_blocks = (D + kMergeCols - 1) / kMergeCols;
     CSAHCA_REQUIRE(bh * col_blocks <= INT32_MAX, "too many heads in one call");

@@ -825,16 +825,22 @@ def dsv4_swa_decode_forward(q, paged_k_cache_u8, token_indices, topk_lengths, at
         raise RuntimeError("q, paged_k_cache_u8, and token_indices must be CUDA tensors")
     _dsv4_common(q, paged_k_cache_u8, token_indices, topk_lengths, attn_sink, page_size, allow_empty=True)
     nq, heads = q.shape[0], q.shape[1]
-    with torch.cuda.device(q.device):
-        out = torch.empty_like(q)
-        if nq == 0 or heads == 0:
-            return out
-        ws = _workspace(lib().csahca_dsv4_decode_workspace_bytes(nq, heads, token_indices.shape[1], 0, 0), q.device)
-        _rc(lib().csahca_dsv4_swa_decode_forward(
-            _ptr(q), _DTYPES[q.dtype], nq, heads, _ptr(paged_k_cache_u8), paged_k_cache_u8.shape[0],
-            paged_k_cache_u8.shape[1], page_size, _ptr(token_indices), token_indices.shape[1],
-            _ptr(_opt(topk_lengths)), _ptr(_opt(attn_sink)), float(softmax_scale), _ptr(out), _ptr(ws),
-            ws.numel(), _stream()))
+    dev = q.get_device()
+    if dev != _current_device():
+        with torch.cuda.device(dev):
+            return dsv4_swa_decode_forward(q, paged_k_cache_u8, token_indices, topk_lengths, attn_sink, page_size,
+                                           softmax_scale)
+    out = torch.empty_like(q)
+    if nq == 0 or heads == 0:
+        return out
+    stream = _raw_stream(dev)
+    ws = _scratch_workspace(_ws_bytes("csahca_dsv4_decode_workspace_bytes", nq, heads, token_indices.shape[1], 0, 0),
+                            dev, stream)
+    _rc(lib().csahca_dsv4_swa_decode_forward(
+        q.data_ptr(), _DTYPES[q.dtype], nq, heads, paged_k_cache_u8.data_ptr(), paged_k_cache_u8.shape[0],
+        paged_k_cache_u8.shape[1], page_size, token_indices.data_ptr(), token_indices.shape[1],
+        _ptr(_opt(topk_lengths)), _ptr(_opt(attn_sink)), float(softmax_scale), out.data_ptr(), ws.data_ptr(),
+        ws.numel(), stream))
     return out
 
 
@@ -854,19 +860,25 @@ def dsv4_sparse_decode_forward(q, paged_k_cache_u8, token_indices, topk_lengths,
     _check(extra_page_size > 0, "extra_page_size must be positive")
     _check(extra_paged_k_cache_u8.shape[1] >= extra_page_size * (576 + 8),
            "extra_bytes_per_page is too small for DSV4 page layout")
-    with torch.cuda.device(q.device):
-        out = torch.empty_like(q)
-        if nq == 0 or heads == 0:
-            return out
-        ws = _workspace(lib().csahca_dsv4_decode_workspace_bytes(nq, heads, token_indices.shape[1],
-                                                                  extra_token_indices.shape[1], 0), q.device)
-        _rc(lib().csahca_dsv4_sparse_decode_forward(
-            _ptr(q), _DTYPES[q.dtype], nq, heads, _ptr(paged_k_cache_u8), paged_k_cache_u8.shape[0],
-            paged_k_cache_u8.shape[1], page_size, _ptr(token_indices), token_indices.shape[1],
-            _ptr(_opt(topk_lengths)), _ptr(extra_paged_k_cache_u8), extra_paged_k_cache_u8.shape[0],
-            extra_paged_k_cache_u8.shape[1], extra_page_size, _ptr(extra_token_indices),
-            extra_token_indices.shape[1], _ptr(_opt(extra_topk_lengths)), _ptr(_opt(attn_sink)),
-            float(softmax_scale), _ptr(out), _ptr(ws), ws.numel(), _stream()))
+    dev = q.get_device()
+    if dev != _current_device():
+        with torch.cuda.device(dev):
+            return dsv4_sparse_decode_forward(q, paged_k_cache_u8, token_indices, topk_lengths,
+                                              extra_paged_k_cache_u8, extra_token_indices, extra_topk_lengths,
+                                              attn_sink, page_size, extra_page_size, softmax_scale)
+    out = torch.empty_like(q)
+    if nq == 0 or heads == 0:
+        return out
+    stream = _raw_stream(dev)
+    ws = _scratch_workspace(_ws_bytes("csahca_dsv4_decode_workspace_bytes", nq, heads, token_indices.shape[1],
+                                      extra_token_indices.shape[1], 0), dev, stream)
+    _rc(lib().csahca_dsv4_sparse_decode_forward(
+        q.data_ptr(), _DTYPES[q.dtype], nq, heads, paged_k_cache_u8.data_ptr(), paged_k_cache_u8.shape[0],
+        paged_k_cache_u8.shape[1], page_size, token_indices.data_ptr(), token_indices.shape[1],
+        _ptr(_opt(topk_lengths)), extra_paged_k_cache_u8.data_ptr(), extra_paged_k_cache_u8.shape[0],
+        extra_paged_k_cache_u8.shape[1], extra_page_size, extra_token_indices.data_ptr(),
+        extra_token_indices.shape[1], _ptr(_opt(extra_topk_lengths)), _ptr(_opt(attn_sink)),
+        float(softmax_scale), out.data_ptr(), ws.data_ptr(), ws.numel(), stream))
     return out
 
 
