@@ -313,3 +313,22 @@ def test_roctx_ranges_only_when_asked():
     assert r.returncode == 0 and "ok" in r.stdout, r.stderr[-2000:]
     with tracing.op_range("csahca.noop"):  # disabled: no library needed
         pass
+
+
+def test_tensors_on_another_device_are_rejected():
+    """The bindings check that every CUDA tensor of a call is on the launching
+    device (the library addresses all of them from that device); CPU tensors
+    are left to the ops' own is_cuda checks and messages."""
+    from csahca_amd import native
+
+    class Fake:
+        def __init__(self, dev):
+            self.is_cuda = dev >= 0
+            self._dev = dev
+
+        def get_device(self):
+            return self._dev
+
+    native._same_device(0, Fake(0), None, Fake(-1))
+    with pytest.raises(RuntimeError, match="all tensors must be on the same device"):
+        native._same_device(0, Fake(0), Fake(1))
