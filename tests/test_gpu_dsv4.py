@@ -366,6 +366,23 @@ def test_onepass_takes_lists_up_to_256_slots(monkeypatch):
         monkeypatch.delenv("CSAHCA_DSV4_ONEPASS")
 
 
+def test_onepass_with_an_empty_swa_list_and_without_lengths():
+    """An empty SWA list with extra slots (the one-pass kernel's index loads
+    then read the extra list for their stand-in addresses) and calls without
+    length tensors, against the oracle."""
+    c = make_dsv4_case(compress_ratio=4, num_queries=3, heads=16, num_tokens=1024, top_k=16, page_size=64,
+                       extra_tokens=1024, extra_top_k=64, seed=77, device=DEV)
+    c.token_indices = c.token_indices[:, :0].contiguous()
+    c.topk_lengths = torch.zeros(3, dtype=torch.int32, device=c.topk_lengths.device)
+    for lengths in (True, False):
+        for sink in (True, False):
+            assert_close(gpu_out(c, sink=sink, lengths=lengths), oracle_out(c, sink=sink, lengths=lengths),
+                         what=f"empty SWA list, lengths={lengths} sink={sink}")
+    c = make_dsv4_case(compress_ratio=0, num_queries=5, heads=8, num_tokens=1024, top_k=100, page_size=64, seed=78,
+                       device=DEV)
+    assert_close(gpu_out(c, lengths=False), oracle_out(c, lengths=False), what="SWA only, no lengths")
+
+
 @pytest.mark.parametrize("route", ["onepass", "1", "0"])
 def test_scale_byte_255_gives_nan_like_the_reference(route, monkeypatch):
     """A scale byte of 255 is 2^128 = inf in the reference's fp32 dequant, so
