@@ -293,12 +293,17 @@ def csa_bench(args, B=1, H=8, S=32768, D=128, chunk=64, top_k=8, copies=None, se
         cursor = c0 + steps + npre
         del graph
     if eager_pass or args.no_graph:
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        with torch.cuda.stream(s), op_range(f"csahca.bench.eager_B{B}_S{S}_k{top_k}"):
-            run(steps)
-        torch.cuda.synchronize()
-        res["ms_per_step_eager"] = (time.perf_counter() - t0) * 1e3 / steps
+        # The median of 5 synchronised passes of `steps` eager steps each (one
+        # host hiccup in a 20-step pass moves its per-step figure by several us).
+        eager = []
+        for _ in range(5):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            with torch.cuda.stream(s), op_range(f"csahca.bench.eager_B{B}_S{S}_k{top_k}"):
+                run(steps)
+            torch.cuda.synchronize()
+            eager.append((time.perf_counter() - t0) * 1e3 / steps)
+        res["ms_per_step_eager"] = sorted(eager)[len(eager) // 2]
     if event_pass:
         with torch.cuda.stream(s), native.profile_launches() as prof:
             run(steps)
@@ -549,16 +554,22 @@ def _dsv4_time(native, q, caches, idx, lens, ecaches, eidx, elens, sink, ps, eps
         ms_graph = replay_timed(s, g, reps) / (reps * copies)
     del g
     torch.cuda.synchronize()
+    # Eager: the median of 5 timed loops of 50 calls (a host hiccup in one loop
+    # would otherwise move the figure by tens of percent).
+    eager = []
     with torch.cuda.stream(s):
         for _ in range(10):
             call(0)
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record(s)
-        for _ in range(50):
-            call(0)
-        end.record(s)
+        for _ in range(5):
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record(s)
+            for _ in range(50):
+                call(0)
+            end.record(s)
+            end.synchronize()
+            eager.append(start.elapsed_time(end) / 50)
     torch.cuda.synchronize()
-    return ms_graph, start.elapsed_time(end) / 50
+    return ms_graph, sorted(eager)[len(eager) // 2]
 
 
 def dsv4_bench(steps=256, copies=64):

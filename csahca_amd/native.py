@@ -187,6 +187,12 @@ def _present(t) -> bool:
 # CSA
 # ---------------------------------------------------------------------------
 
+# With one visible device every CUDA tensor is on it, so the device check
+# below runs only where there are several (device_count does not initialise
+# the GPU).
+_MULTI_DEVICE = torch.cuda.device_count() > 1
+
+
 def _same_device(dev: int, *tensors) -> None:
     """Every given CUDA tensor (None skipped; a CPU tensor is left to the
     caller's own is_cuda check and its message) lives on device ``dev``: the
@@ -206,7 +212,8 @@ def _csa_checks(q, k_cache, v_cache, chunk_indices, chunk_size, tiled: bool, til
     _check(k_cache.is_contiguous(), "k_cache must be contiguous")
     _check(v_cache.is_contiguous(), "v_cache must be contiguous")
     _check(not have_idx or chunk_indices.is_contiguous(), "chunk_indices must be contiguous")
-    _same_device(q.get_device(), k_cache, v_cache, chunk_indices)
+    if _MULTI_DEVICE:
+        _same_device(q.get_device(), k_cache, v_cache, chunk_indices)
     _check(q.dim() == 3, "q must be [batch, heads, head_dim]")
     _check(k_cache.dim() == 4, "k_cache must be [batch, heads, seq, head_dim]")
     _check(v_cache.shape == k_cache.shape, "v_cache must match k_cache shape")
@@ -296,7 +303,8 @@ def csa_chunk_summary(k_cache, chunk_size, *, out=None, chunk_begin: int = 0, nu
         _check(out.is_cuda and out.is_contiguous() and out.dtype == torch.float32 and out.dim() == 4
                and tuple(out.shape[:2]) == (B, H) and out.shape[3] == D,
                "summary must be a contiguous fp32 [batch, heads, chunks, head_dim] CUDA tensor")
-        _same_device(k_cache.get_device(), out)
+        if _MULTI_DEVICE:
+            _same_device(k_cache.get_device(), out)
         _rc(lib().csahca_csa_chunk_summary(_ptr(k_cache), _ptr(out), _DTYPES[k_cache.dtype], B, H, S, D,
                                            chunk_size, out.shape[2], int(chunk_begin), int(num_chunks),
                                            _stream()))
@@ -313,7 +321,8 @@ def csa_chunk_summary_at(k_cache, summary, chunk_size, token_pos):
     complete chunks."""
     chunk_size = int(chunk_size)
     _check(k_cache.is_cuda and summary.is_cuda and token_pos.is_cuda, "tensors must be CUDA tensors")
-    _same_device(k_cache.get_device(), summary, token_pos)
+    if _MULTI_DEVICE:
+        _same_device(k_cache.get_device(), summary, token_pos)
     _check(k_cache.is_contiguous() and k_cache.dim() == 4, "k_cache must be a contiguous [batch, heads, seq, head_dim]")
     _check(k_cache.dtype in _FLOATING, f"unsupported dtype {k_cache.dtype}")
     _check(chunk_size > 0, "chunk_size must be positive")
@@ -335,7 +344,8 @@ def csa_select_topk(q, summary, top_k):
     first; equal scores are ordered by ascending chunk id."""
     top_k = int(top_k)
     _check(q.is_cuda and summary.is_cuda, "q and summary must be CUDA tensors")
-    _same_device(q.get_device(), summary)
+    if _MULTI_DEVICE:
+        _same_device(q.get_device(), summary)
     _check(q.is_contiguous() and summary.is_contiguous(), "q and summary must be contiguous")
     _check(q.dim() == 3, "q must be [batch, heads, head_dim]")
     _check(summary.dim() == 4 and summary.dtype == torch.float32,
@@ -418,7 +428,8 @@ def csa_decode_step(q, k_cache, v_cache, summary, chunk_size, top_k, tile_size: 
     _check(top_k >= 0, "top_k must be non-negative")
     k = min(top_k, C)
     dev = q.get_device()
-    _same_device(dev, summary)
+    if _MULTI_DEVICE:
+        _same_device(dev, summary)
     if dev != _current_device():
         with torch.cuda.device(dev):
             return csa_decode_step(q, k_cache, v_cache, summary, chunk_size, top_k)
@@ -449,7 +460,8 @@ def csa_decode_step_noalloc(q, k_cache, v_cache, summary, chunk_size, top_k, *, 
     on one device race on the shared array.  Returns ``(out, indices)``."""
     chunk_size, top_k = int(chunk_size), int(top_k)
     _check(all(t.is_cuda for t in (q, k_cache, v_cache, summary, out, indices)), "all tensors must be CUDA tensors")
-    _same_device(q.get_device(), k_cache, v_cache, summary, out, indices)
+    if _MULTI_DEVICE:
+        _same_device(q.get_device(), k_cache, v_cache, summary, out, indices)
     _check(all(t.is_contiguous() for t in (q, k_cache, v_cache, summary, out, indices)), "tensors must be contiguous")
     _check(q.dim() == 3 and k_cache.dim() == 4 and k_cache.shape == v_cache.shape, "q [B, H, D], caches [B, H, S, D]")
     B, H, S, D = k_cache.shape
@@ -489,7 +501,8 @@ def csa_decode_step_dev(q, k_cache, v_cache, summary, num_chunks, chunk_size, to
     Cs = summary.shape[2]
     _check(top_k >= 0, "top_k must be non-negative")
     k = min(top_k, Cs)
-    _same_device(q.get_device(), summary, num_chunks, out, indices)
+    if _MULTI_DEVICE:
+        _same_device(q.get_device(), summary, num_chunks, out, indices)
     with torch.cuda.device(q.device):
         if out is None:
             out = torch.empty_like(q)
@@ -534,7 +547,8 @@ def block_linear(x, weight, *, norm_weight=None, eps: float = 1e-6, activation=N
     ``advance_pos`` (int64 CUDA tensor) is incremented by one after the
     product.  Returns ``out`` [batch, out_features]."""
     _check(x.is_cuda and weight.is_cuda, "x and weight must be CUDA tensors")
-    _same_device(x.get_device(), weight, norm_weight, residual, base, advance_pos, out)
+    if _MULTI_DEVICE:
+        _same_device(x.get_device(), weight, norm_weight, residual, base, advance_pos, out)
     _check(x.dim() == 2 and weight.dim() == 2 and weight.shape[1] == x.shape[1],
            "x must be [batch, in_features] and weight [out_features, in_features]")
     _check(x.dtype in _BLOCK_DTYPES and weight.dtype == x.dtype, "x and weight must both be bfloat16 or float16")
@@ -573,7 +587,8 @@ def block_qkv(hidden, w_qkv, q, k_cache, v_cache, token_pos, *, norm_weight=None
     [batch, H, capacity, D]); ``num_chunks`` (int32, optional) receives
     (token_pos + 1) // chunk_size.  Positions are read on the device."""
     _check(all(t.is_cuda for t in (hidden, w_qkv, q, k_cache, v_cache, token_pos)), "all tensors must be CUDA tensors")
-    _same_device(hidden.get_device(), w_qkv, q, k_cache, v_cache, token_pos, num_chunks, norm_weight)
+    if _MULTI_DEVICE:
+        _same_device(hidden.get_device(), w_qkv, q, k_cache, v_cache, token_pos, num_chunks, norm_weight)
     _check(hidden.dtype in _BLOCK_DTYPES and all(t.dtype == hidden.dtype for t in (w_qkv, q, k_cache, v_cache)),
            "hidden, w_qkv, q and the caches must share a bfloat16 or float16 dtype")
     _check(all(t.is_contiguous() for t in (hidden, w_qkv, q, k_cache, v_cache)), "tensors must be contiguous")
@@ -616,7 +631,8 @@ def csa_decode_step_at(q, k_cache, v_cache, summary, token_pos, chunk_size, top_
     Cs = summary.shape[2]
     _check(top_k >= 0, "top_k must be non-negative")
     k = min(top_k, Cs)
-    _same_device(q.get_device(), summary, token_pos, out, indices)
+    if _MULTI_DEVICE:
+        _same_device(q.get_device(), summary, token_pos, out, indices)
     with torch.cuda.device(q.device):
         if out is None:
             out = torch.empty_like(q)
@@ -686,7 +702,8 @@ def hca_decode_forward(q, k_cache, v_cache, chunk_size, *, blend=None, csa_weigh
     if blend is not None:
         _check(blend.is_cuda and blend.is_contiguous() and blend.dtype == q.dtype and blend.shape == q.shape,
                "blend must be a contiguous CUDA tensor shaped and typed like q")
-    _same_device(q.get_device(), k_cache, v_cache, blend)
+    if _MULTI_DEVICE:
+        _same_device(q.get_device(), k_cache, v_cache, blend)
     with torch.cuda.device(q.device):
         out = torch.empty_like(q)
         ws = _workspace(lib().csahca_hca_decode_workspace_bytes(B, H, S, D, chunk_size), q.device)
@@ -717,7 +734,8 @@ def hybrid_decode_forward(q, k_cache, v_cache, *, csa_chunk_size: int, csa_top_k
     C = summary.shape[2]
     _check(csa_top_k >= 0, "top_k must be non-negative")
     k = min(csa_top_k, C)
-    _same_device(q.get_device(), summary)
+    if _MULTI_DEVICE:
+        _same_device(q.get_device(), summary)
     with torch.cuda.device(q.device):
         out = torch.empty_like(q)
         csa_out = torch.empty_like(q)
@@ -746,7 +764,8 @@ def _dsv4_common(q, cache, token_indices, topk_lengths, attn_sink, page_size, al
     _check(token_indices.is_contiguous(), "token_indices must be contiguous")
     _check(not _defined(topk_lengths) or topk_lengths.is_contiguous(), "topk_lengths must be contiguous")
     _check(not _defined(attn_sink) or attn_sink.is_contiguous(), "attn_sink must be contiguous")
-    _same_device(q.get_device(), cache, token_indices, topk_lengths, attn_sink)
+    if _MULTI_DEVICE:
+        _same_device(q.get_device(), cache, token_indices, topk_lengths, attn_sink)
     _check(q.dim() == 3, "q must be [num_queries, heads, 512]")
     _check(q.shape[2] == _DSV4_HEAD_DIM, "q head_dim must be 512 for DSV4")
     _check(cache.dim() == 2, "paged_k_cache_u8 must be [num_pages, bytes_per_page]")
@@ -783,7 +802,8 @@ def _dsv4_extra_checks(extra_cache, extra_token_indices, extra_topk_lengths, nq,
     _check(not _present(extra_topk_lengths) or extra_topk_lengths.dtype == torch.int32,
            "extra_topk_lengths must be int32 when defined")
     _check(extra_token_indices.shape[0] == nq, "extra_token_indices query dimension must match q")
-    _same_device(dev, extra_cache, extra_token_indices, extra_topk_lengths)
+    if _MULTI_DEVICE:
+        _same_device(dev, extra_cache, extra_token_indices, extra_topk_lengths)
     _check(not _present(extra_topk_lengths) or extra_topk_lengths.numel() == nq,
            "extra_topk_lengths must have one value per query")
 
@@ -980,7 +1000,8 @@ def dsv4_pack_tokens(k_tokens, page_size, *, cache=None, locs=None):
         if locs is not None:
             _check(locs.is_cuda and locs.dtype == torch.int32 and locs.numel() == T, "locs must be int32 [tokens]")
             locs = locs.contiguous()
-        _same_device(k_tokens.get_device(), cache, locs)
+        if _MULTI_DEVICE:
+            _same_device(k_tokens.get_device(), cache, locs)
         _rc(lib().csahca_dsv4_pack_tokens(_ptr(k_tokens), _ptr(locs), T, _ptr(cache_u8), cache_u8.shape[0],
                                           cache_u8.shape[1], page_size, _stream()))
     return cache
