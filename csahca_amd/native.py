@@ -203,36 +203,60 @@ def _same_device(dev: int, *tensors) -> None:
 
 
 def _csa_checks(q, k_cache, v_cache, chunk_indices, chunk_size, tiled: bool, tile_size=None):
-    """The reference's TORCH_CHECKs of the CSA ops; ``chunk_indices`` None
-    (the fused step, which selects its own) skips the checks of that tensor."""
-    have_idx = chunk_indices is not None
-    if not (q.is_cuda and k_cache.is_cuda and v_cache.is_cuda and (not have_idx or chunk_indices.is_cuda)):
-        raise RuntimeError("all tensors must be CUDA tensors")
-    _check(q.is_contiguous(), "q must be contiguous")
-    _check(k_cache.is_contiguous(), "k_cache must be contiguous")
-    _check(v_cache.is_contiguous(), "v_cache must be contiguous")
-    _check(not have_idx or chunk_indices.is_contiguous(), "chunk_indices must be contiguous")
+    """The reference's TORCH_CHECKs of the CSA ops, in their order (the first
+    that fails raises its text); ``chunk_indices`` None (the fused step, which
+    selects its own) skips the checks of that tensor.  Each check is an inline
+    test, not a call: they run on every eager call."""
+    msg = _csa_check_error(q, k_cache, v_cache, chunk_indices, chunk_size, tiled, tile_size)
+    if msg is not None:
+        raise RuntimeError(msg)
     if _MULTI_DEVICE:
         _same_device(q.get_device(), k_cache, v_cache, chunk_indices)
-    _check(q.dim() == 3, "q must be [batch, heads, head_dim]")
-    _check(k_cache.dim() == 4, "k_cache must be [batch, heads, seq, head_dim]")
-    _check(v_cache.shape == k_cache.shape, "v_cache must match k_cache shape")
-    _check(not have_idx or chunk_indices.dim() == 3, "chunk_indices must be [batch, heads, top_k]")
-    _check(q.dtype == k_cache.dtype, "q and k_cache dtype must match")
-    _check(q.dtype == v_cache.dtype, "q and v_cache dtype must match")
-    _check(not have_idx or chunk_indices.dtype in (torch.int32, torch.int64), "chunk_indices must be int32 or int64")
+
+
+def _csa_check_error(q, k_cache, v_cache, chunk_indices, chunk_size, tiled, tile_size):
+    have_idx = chunk_indices is not None
+    if not (q.is_cuda and k_cache.is_cuda and v_cache.is_cuda and (not have_idx or chunk_indices.is_cuda)):
+        return "all tensors must be CUDA tensors"
+    if not q.is_contiguous():
+        return "q must be contiguous"
+    if not k_cache.is_contiguous():
+        return "k_cache must be contiguous"
+    if not v_cache.is_contiguous():
+        return "v_cache must be contiguous"
+    if have_idx and not chunk_indices.is_contiguous():
+        return "chunk_indices must be contiguous"
+    if q.dim() != 3:
+        return "q must be [batch, heads, head_dim]"
+    if k_cache.dim() != 4:
+        return "k_cache must be [batch, heads, seq, head_dim]"
+    if v_cache.shape != k_cache.shape:
+        return "v_cache must match k_cache shape"
+    if have_idx and chunk_indices.dim() != 3:
+        return "chunk_indices must be [batch, heads, top_k]"
+    if q.dtype != k_cache.dtype:
+        return "q and k_cache dtype must match"
+    if q.dtype != v_cache.dtype:
+        return "q and v_cache dtype must match"
+    if have_idx and chunk_indices.dtype not in (torch.int32, torch.int64):
+        return "chunk_indices must be int32 or int64"
     B, H, D = q.shape
-    _check(k_cache.shape[0] == B and k_cache.shape[1] == H and k_cache.shape[3] == D,
-           "KV cache shape must match q")
-    _check(not have_idx or (chunk_indices.shape[0] == B and chunk_indices.shape[1] == H),
-           "chunk_indices batch/head dimensions must match q")
-    _check(chunk_size > 0, "chunk_size must be positive")
+    if not (k_cache.shape[0] == B and k_cache.shape[1] == H and k_cache.shape[3] == D):
+        return "KV cache shape must match q"
+    if have_idx and not (chunk_indices.shape[0] == B and chunk_indices.shape[1] == H):
+        return "chunk_indices batch/head dimensions must match q"
+    if not chunk_size > 0:
+        return "chunk_size must be positive"
     if tiled:
-        _check(tile_size > 0, "tile_size must be positive")
-        _check(D <= 1024, "head_dim > 1024 is not supported by the tiled kernel")
-    else:
-        _check(D <= 1024, "head_dim > 1024 is not supported by the v1 kernel")
-    _check(q.dtype in _FLOATING, f"unsupported dtype {q.dtype}")
+        if not tile_size > 0:
+            return "tile_size must be positive"
+        if D > 1024:
+            return "head_dim > 1024 is not supported by the tiled kernel"
+    elif D > 1024:
+        return "head_dim > 1024 is not supported by the v1 kernel"
+    if q.dtype not in _FLOATING:
+        return f"unsupported dtype {q.dtype}"
+    return None
 
 
 @traced
@@ -419,13 +443,15 @@ def csa_decode_step(q, k_cache, v_cache, summary, chunk_size, top_k, tile_size: 
         idx = csa_select_topk(q, summary, top_k)
         return csa_decode_forward_tiled(q, k_cache, v_cache, idx, chunk_size, int(tile_size)), idx
     _csa_checks(q, k_cache, v_cache, None, chunk_size, tiled=False)
-    _check(summary.is_cuda and summary.is_contiguous() and summary.dtype == torch.float32 and summary.dim() == 4,
-           "summary must be a contiguous fp32 [batch, heads, chunks, head_dim] CUDA tensor")
+    if not (summary.is_cuda and summary.is_contiguous() and summary.dtype == torch.float32 and summary.dim() == 4):
+        raise RuntimeError("summary must be a contiguous fp32 [batch, heads, chunks, head_dim] CUDA tensor")
     B, H, D = q.shape
     S = k_cache.shape[2]
-    _check(summary.shape[0] == B and summary.shape[1] == H and summary.shape[3] == D, "summary shape must match q")
+    if not (summary.shape[0] == B and summary.shape[1] == H and summary.shape[3] == D):
+        raise RuntimeError("summary shape must match q")
     C = summary.shape[2]
-    _check(top_k >= 0, "top_k must be non-negative")
+    if top_k < 0:
+        raise RuntimeError("top_k must be non-negative")
     k = min(top_k, C)
     dev = q.get_device()
     if _MULTI_DEVICE:
@@ -757,55 +783,103 @@ _DSV4_HEAD_DIM = 512
 
 
 def _dsv4_common(q, cache, token_indices, topk_lengths, attn_sink, page_size, allow_empty: bool):
-    _check(_defined(topk_lengths) is False or topk_lengths.is_cuda, "topk_lengths must be CUDA when defined")
-    _check(_defined(attn_sink) is False or attn_sink.is_cuda, "attn_sink must be CUDA when defined")
-    _check(q.is_contiguous(), "q must be contiguous")
-    _check(cache.is_contiguous(), "paged_k_cache_u8 must be contiguous")
-    _check(token_indices.is_contiguous(), "token_indices must be contiguous")
-    _check(not _defined(topk_lengths) or topk_lengths.is_contiguous(), "topk_lengths must be contiguous")
-    _check(not _defined(attn_sink) or attn_sink.is_contiguous(), "attn_sink must be contiguous")
+    """The reference's TORCH_CHECKs of the DSV4 ops, in their order (inline
+    tests: they run on every eager call)."""
+    msg = _dsv4_common_error(q, cache, token_indices, topk_lengths, attn_sink, page_size)
+    if msg is not None:
+        raise RuntimeError(msg)
     if _MULTI_DEVICE:
         _same_device(q.get_device(), cache, token_indices, topk_lengths, attn_sink)
-    _check(q.dim() == 3, "q must be [num_queries, heads, 512]")
-    _check(q.shape[2] == _DSV4_HEAD_DIM, "q head_dim must be 512 for DSV4")
-    _check(cache.dim() == 2, "paged_k_cache_u8 must be [num_pages, bytes_per_page]")
-    _check(cache.dtype == torch.uint8, "paged_k_cache_u8 must be uint8")
-    _check(token_indices.dim() == 2, "token_indices must be [num_queries, topk_slots]")
-    _check(token_indices.dtype == torch.int32, "token_indices must be int32")
-    _check(not _defined(topk_lengths) or topk_lengths.dtype == torch.int32, "topk_lengths must be int32 when defined")
-    _check(not _defined(attn_sink) or attn_sink.dtype == torch.float32, "attn_sink must be float32 when defined")
-    _check(page_size > 0, "page_size must be positive")
-    _check(q.dtype in _FLOATING, f"unsupported dtype {q.dtype}")
+
+
+def _dsv4_common_error(q, cache, token_indices, topk_lengths, attn_sink, page_size):
+    has_len, has_sink = topk_lengths is not None, attn_sink is not None
+    if has_len and not topk_lengths.is_cuda:
+        return "topk_lengths must be CUDA when defined"
+    if has_sink and not attn_sink.is_cuda:
+        return "attn_sink must be CUDA when defined"
+    if not q.is_contiguous():
+        return "q must be contiguous"
+    if not cache.is_contiguous():
+        return "paged_k_cache_u8 must be contiguous"
+    if not token_indices.is_contiguous():
+        return "token_indices must be contiguous"
+    if has_len and not topk_lengths.is_contiguous():
+        return "topk_lengths must be contiguous"
+    if has_sink and not attn_sink.is_contiguous():
+        return "attn_sink must be contiguous"
+    if q.dim() != 3:
+        return "q must be [num_queries, heads, 512]"
+    if q.shape[2] != _DSV4_HEAD_DIM:
+        return "q head_dim must be 512 for DSV4"
+    if cache.dim() != 2:
+        return "paged_k_cache_u8 must be [num_pages, bytes_per_page]"
+    if cache.dtype != torch.uint8:
+        return "paged_k_cache_u8 must be uint8"
+    if token_indices.dim() != 2:
+        return "token_indices must be [num_queries, topk_slots]"
+    if token_indices.dtype != torch.int32:
+        return "token_indices must be int32"
+    if has_len and topk_lengths.dtype != torch.int32:
+        return "topk_lengths must be int32 when defined"
+    if has_sink and attn_sink.dtype != torch.float32:
+        return "attn_sink must be float32 when defined"
+    if not page_size > 0:
+        return "page_size must be positive"
+    if q.dtype not in _FLOATING:
+        return f"unsupported dtype {q.dtype}"
     nq, heads = q.shape[0], q.shape[1]
-    _check(token_indices.shape[0] == nq, "token_indices query dimension must match q")
+    if token_indices.shape[0] != nq:
+        return "token_indices query dimension must match q"
     # None and empty tensors both mean "absent" on every route (the reference's
     # untiled ops reject the empty tensors its own wrappers pass for None).
-    _check(not _present(topk_lengths) or topk_lengths.numel() == nq, "topk_lengths must have one value per query")
-    _check(not _present(attn_sink) or attn_sink.numel() == heads, "attn_sink must have one value per head")
-    bpp = cache.shape[1]
-    _check(bpp >= page_size * (576 + 8), "bytes_per_page is too small for DSV4 page layout")
+    if has_len and topk_lengths.numel() > 0 and topk_lengths.numel() != nq:
+        return "topk_lengths must have one value per query"
+    if has_sink and attn_sink.numel() > 0 and attn_sink.numel() != heads:
+        return "attn_sink must have one value per head"
+    if cache.shape[1] < page_size * (576 + 8):
+        return "bytes_per_page is too small for DSV4 page layout"
+    return None
 
 
 def _dsv4_extra_checks(extra_cache, extra_token_indices, extra_topk_lengths, nq, dev: int):
-    _check(extra_cache.is_cuda, "extra_paged_k_cache_u8 must be CUDA")
-    _check(extra_token_indices.is_cuda, "extra_token_indices must be CUDA")
-    _check(not _defined(extra_topk_lengths) or extra_topk_lengths.is_cuda,
-           "extra_topk_lengths must be CUDA when defined")
-    _check(extra_cache.is_contiguous(), "extra_paged_k_cache_u8 must be contiguous")
-    _check(extra_token_indices.is_contiguous(), "extra_token_indices must be contiguous")
-    _check(not _defined(extra_topk_lengths) or extra_topk_lengths.is_contiguous(),
-           "extra_topk_lengths must be contiguous")
-    _check(extra_cache.dim() == 2, "extra_paged_k_cache_u8 must be [num_pages, bytes_per_page]")
-    _check(extra_cache.dtype == torch.uint8, "extra_paged_k_cache_u8 must be uint8")
-    _check(extra_token_indices.dim() == 2, "extra_token_indices must be [num_queries, extra_topk_slots]")
-    _check(extra_token_indices.dtype == torch.int32, "extra_token_indices must be int32")
-    _check(not _present(extra_topk_lengths) or extra_topk_lengths.dtype == torch.int32,
-           "extra_topk_lengths must be int32 when defined")
-    _check(extra_token_indices.shape[0] == nq, "extra_token_indices query dimension must match q")
+    msg = _dsv4_extra_error(extra_cache, extra_token_indices, extra_topk_lengths, nq)
+    if msg is not None:
+        raise RuntimeError(msg)
     if _MULTI_DEVICE:
         _same_device(dev, extra_cache, extra_token_indices, extra_topk_lengths)
-    _check(not _present(extra_topk_lengths) or extra_topk_lengths.numel() == nq,
-           "extra_topk_lengths must have one value per query")
+
+
+def _dsv4_extra_error(extra_cache, extra_token_indices, extra_topk_lengths, nq):
+    has_len = extra_topk_lengths is not None
+    if not extra_cache.is_cuda:
+        return "extra_paged_k_cache_u8 must be CUDA"
+    if not extra_token_indices.is_cuda:
+        return "extra_token_indices must be CUDA"
+    if has_len and not extra_topk_lengths.is_cuda:
+        return "extra_topk_lengths must be CUDA when defined"
+    if not extra_cache.is_contiguous():
+        return "extra_paged_k_cache_u8 must be contiguous"
+    if not extra_token_indices.is_contiguous():
+        return "extra_token_indices must be contiguous"
+    if has_len and not extra_topk_lengths.is_contiguous():
+        return "extra_topk_lengths must be contiguous"
+    if extra_cache.dim() != 2:
+        return "extra_paged_k_cache_u8 must be [num_pages, bytes_per_page]"
+    if extra_cache.dtype != torch.uint8:
+        return "extra_paged_k_cache_u8 must be uint8"
+    if extra_token_indices.dim() != 2:
+        return "extra_token_indices must be [num_queries, extra_topk_slots]"
+    if extra_token_indices.dtype != torch.int32:
+        return "extra_token_indices must be int32"
+    len_present = has_len and extra_topk_lengths.numel() > 0
+    if len_present and extra_topk_lengths.dtype != torch.int32:
+        return "extra_topk_lengths must be int32 when defined"
+    if extra_token_indices.shape[0] != nq:
+        return "extra_token_indices query dimension must match q"
+    if len_present and extra_topk_lengths.numel() != nq:
+        return "extra_topk_lengths must have one value per query"
+    return None
 
 
 def _opt(t):
@@ -821,19 +895,21 @@ def dsv4_decode_forward_tiled(q, paged_k_cache_u8, token_indices, topk_lengths, 
     if not (q.is_cuda and paged_k_cache_u8.is_cuda and token_indices.is_cuda):
         raise RuntimeError("q, paged_k_cache_u8, and token_indices must be CUDA tensors")
     _dsv4_common(q, paged_k_cache_u8, token_indices, topk_lengths, attn_sink, page_size, allow_empty=True)
-    _check(paged_k_cache_u8.shape[1] % 4 == 0,
-           "tiled DSV4 kernel requires bytes_per_page divisible by 4 for vectorized loads")
+    if paged_k_cache_u8.shape[1] % 4 != 0:
+        raise RuntimeError("tiled DSV4 kernel requires bytes_per_page divisible by 4 for vectorized loads")
     nq, heads = q.shape[0], q.shape[1]
-    has_extra = (_defined(extra_paged_k_cache_u8) and extra_paged_k_cache_u8.numel() > 0
-                 and _defined(extra_token_indices) and extra_token_indices.numel() > 0)
+    has_extra = (extra_paged_k_cache_u8 is not None and extra_paged_k_cache_u8.numel() > 0
+                 and extra_token_indices is not None and extra_token_indices.numel() > 0)
     extra_slots = 0
     if has_extra:
         _dsv4_extra_checks(extra_paged_k_cache_u8, extra_token_indices, extra_topk_lengths, nq, q.get_device())
-        _check(extra_page_size > 0, "extra_page_size must be positive")
+        if extra_page_size <= 0:
+            raise RuntimeError("extra_page_size must be positive")
         ebpp = extra_paged_k_cache_u8.shape[1]
-        _check(ebpp >= extra_page_size * (576 + 8), "extra_bytes_per_page is too small for DSV4 page layout")
-        _check(ebpp % 4 == 0,
-               "tiled DSV4 kernel requires extra_bytes_per_page divisible by 4 for vectorized loads")
+        if ebpp < extra_page_size * (576 + 8):
+            raise RuntimeError("extra_bytes_per_page is too small for DSV4 page layout")
+        if ebpp % 4 != 0:
+            raise RuntimeError("tiled DSV4 kernel requires extra_bytes_per_page divisible by 4 for vectorized loads")
         extra_slots = extra_token_indices.shape[1]
     dev = q.get_device()
     if dev != _current_device():
