@@ -139,6 +139,32 @@ __device__ __forceinline__ uint32_t wait_tagged(const uint64_t* p, uint64_t w, u
   return static_cast<uint32_t>(w);
 }
 
+// Wait (bounded) until every valid word of a batch carries `tag`, re-reading
+// the whole batch each round: one round trip per round, whatever the number of
+// words that were not ready when the batch was first read (waiting on them one
+// at a time costs a round trip per word).  valid(j) tells the words of the
+// batch that exist (a prefix); addr(j) is the address of word j.  On time-out
+// the sticky status bit is set and `bad` raised.
+template <int N, typename Addr, typename Valid>
+__device__ __forceinline__ void wait_tagged_batch(Addr addr, Valid valid, uint64_t (&w)[N], uint32_t tag,
+                                                  uint32_t* status, uint32_t spin_limit, bool& bad) {
+  for (uint32_t it = 0;; ++it) {
+    bool ready = true;
+#pragma unroll
+    for (int j = 0; j < N; ++j) ready = ready && (!valid(j) || static_cast<uint32_t>(w[j] >> 32) == tag);
+    if (ready) return;
+    if (it >= spin_limit) {
+      __hip_atomic_fetch_or(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      bad = true;
+      return;
+    }
+    __builtin_amdgcn_s_sleep(1);
+    // (word 0 exists whenever any does: the others re-read it, unconditionally)
+#pragma unroll
+    for (int j = 0; j < N; ++j) w[j] = get_raw(addr(valid(j) ? j : 0));
+  }
+}
+
 // PIPE: walk several batches of rows double-buffered (an instantiation of its
 // own, so the batch-by-batch kernel keeps its code).  W: wavefronts per
 // workgroup (the wide instantiation serves a head from one workgroup of 8).
@@ -150,7 +176,7 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
   constexpr int SLPR = D / 4, SRPL = kWave / SLPR;  // fp32 summary rows
   constexpr int U = kStepAttendUnroll;
   constexpr int B8 = 8;                              // tagged key loads issued per batch
-  constexpr int kGather = 24;                        // tagged partial loads per thread per batch
+  constexpr int kGather = 8;                         // tagged partial loads per thread per batch
 
   // LDS: keys[max(Cs, P*(D+2))] (the head's keys, later the gathered
   //      partials; first, so that its address needs only preloaded arguments)
@@ -577,14 +603,16 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
       const int i = i0 + j * NT;
       w[j] = i < nw ? get_raw(ph + i) : 0;
     }
+    bool lost = false;
+    wait_tagged_batch<kGather>([&](int j) { return ph + i0 + j * NT; }, [&](int j) { return i0 + j * NT < nw; }, w,
+                               tag, a.status, a.spin_limit, lost);
 #pragma unroll
     for (int j = 0; j < kGather; ++j) {
       const int i = i0 + j * NT;
-      if (i < nw) {
-        bool late = false;
-        const uint32_t v = wait_tagged(ph + i, w[j], tag, a.status, a.spin_limit, late);
-        pb[i] = late ? __builtin_nanf("") : __uint_as_float(v);  // a lost word poisons what uses it
-      }
+      // a lost word poisons what uses it
+      if (i < nw)
+        pb[i] = static_cast<uint32_t>(w[j] >> 32) != tag ? __builtin_nanf("")
+                                                         : __uint_as_float(static_cast<uint32_t>(w[j]));
     }
   }
   __syncthreads();
