@@ -168,7 +168,13 @@ __device__ __forceinline__ void wait_tagged_batch(Addr addr, Valid valid, uint64
 // PIPE: walk several batches of rows double-buffered (an instantiation of its
 // own, so the batch-by-batch kernel keeps its code).  W: wavefronts per
 // workgroup (the wide instantiation serves a head from one workgroup of 8).
-template <typename T, int D, int TOPK_M, bool POS, bool PIPE = false, int W = kStepWaves>
+// MERGE: which merge of the P partials the instantiation holds -- kMergeRegs
+// (P <= kRegMergeP, the host guarantees it), kMergeLds (P > kRegMergeP) or
+// kMergeBoth (chosen by P at run time).  Leaving the other merge out keeps the
+// code of the latency-bound kernel smaller: without the LDS merge the B1 H8
+// S32768 top-8 step took 9.68 against 9.78 us (512 steps, same box).
+constexpr int kMergeRegs = 0, kMergeLds = 1, kMergeBoth = 2;
+template <typename T, int D, int TOPK_M, bool POS, bool PIPE = false, int W = kStepWaves, int MERGE = kMergeBoth>
 __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
   constexpr int NT = W * kWave;
   using L = AttendLayout<T, D>;
@@ -516,7 +522,7 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
   CSAHCA_STAMP(5);
   if (p != 0) return;
   const uint64_t* ph = a.part + h * a.part_stride;
-  if (P <= kRegMergeP) {
+  if (MERGE == kMergeRegs || (MERGE == kMergeBoth && P <= kRegMergeP)) {
     // Few partials: the thread of column d gathers every acc_j[d] itself, and
     // lane l of each wavefront one of the 16 words (m_j, l_j), j = (l % 16) / 2,
     // which the wavefront shares by lane permutes -- one batch of 9 tagged loads
@@ -592,59 +598,61 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
       __hip_atomic_store(&a.epoch[h], bad ? kPoisonEpoch : tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
-  // Gather all P partials ((m, l, acc[D]) each) into LDS in one batch of loads
-  // spread over the 256 threads, then merge from LDS.
-  float* pb = reinterpret_cast<float*>(keys_l);
-  const int nw = P * (D + 2);
-  for (int i0 = bad ? nw : tid; i0 < nw; i0 += NT * kGather) {
-    uint64_t w[kGather];
-#pragma unroll
-    for (int j = 0; j < kGather; ++j) {
-      const int i = i0 + j * NT;
-      w[j] = i < nw ? get_raw(ph + i) : 0;
+  if constexpr (MERGE != kMergeRegs) {
+    // Gather all P partials ((m, l, acc[D]) each) into LDS in one batch of loads
+    // spread over the 256 threads, then merge from LDS.
+    float* pb = reinterpret_cast<float*>(keys_l);
+    const int nw = P * (D + 2);
+    for (int i0 = bad ? nw : tid; i0 < nw; i0 += NT * kGather) {
+      uint64_t w[kGather];
+  #pragma unroll
+      for (int j = 0; j < kGather; ++j) {
+        const int i = i0 + j * NT;
+        w[j] = i < nw ? get_raw(ph + i) : 0;
+      }
+      bool lost = false;
+      wait_tagged_batch<kGather>([&](int j) { return ph + i0 + j * NT; }, [&](int j) { return i0 + j * NT < nw; }, w,
+                                 tag, a.status, a.spin_limit, lost);
+  #pragma unroll
+      for (int j = 0; j < kGather; ++j) {
+        const int i = i0 + j * NT;
+        // a lost word poisons what uses it
+        if (i < nw)
+          pb[i] = static_cast<uint32_t>(w[j] >> 32) != tag ? __builtin_nanf("")
+                                                           : __uint_as_float(static_cast<uint32_t>(w[j]));
+      }
     }
-    bool lost = false;
-    wait_tagged_batch<kGather>([&](int j) { return ph + i0 + j * NT; }, [&](int j) { return i0 + j * NT < nw; }, w,
-                               tag, a.status, a.spin_limit, lost);
-#pragma unroll
-    for (int j = 0; j < kGather; ++j) {
-      const int i = i0 + j * NT;
-      // a lost word poisons what uses it
-      if (i < nw)
-        pb[i] = static_cast<uint32_t>(w[j] >> 32) != tag ? __builtin_nanf("")
-                                                         : __uint_as_float(static_cast<uint32_t>(w[j]));
+    __syncthreads();
+    // Wavefront 0: one partial per lane -> weights 2^(m_j - M) (0 for empty
+    // partials) and the total L (NaN if any partial is poisoned); then every
+    // column is a branch-free dot product.
+    float* wts = comb;  // P weights, then L at [kStepMaxP]
+    if (wave == 0) {
+      const float mj = lane < P ? pb[lane * (D + 2)] : -INFINITY;
+      const float lj = lane < P ? pb[lane * (D + 2) + 1] : 0.f;
+      float mx = lj > 0.f ? mj : -INFINITY;
+  #pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, xor_lanes(mx, off));
+      const float w = (lj > 0.f && mx != -INFINITY) ? fast_exp2(mj - mx) : 0.f;
+      if (lane < P) wts[lane] = w;
+      const float Lt = wave_sum(w * lj);
+      const bool any_bad = __any(bad || mj != mj || lj != lj);
+      if (lane == 0) wts[kStepMaxP] = any_bad ? __builtin_nanf("") : Lt;
     }
+    __syncthreads();
+    const float LL = wts[kStepMaxP];
+    if (d < D) {
+      float AA = 0.f;
+  #pragma unroll 8
+      for (int j = 0; j < P; ++j) AA = fmaf(wts[j], pb[j * (D + 2) + 2 + d], AA);
+      out[d] = from_f32<T>(LL != LL ? LL : (LL > 0.f ? AA / LL : 0.f));
+    }
+    CSAHCA_STAMP(6);
+    __syncthreads();
+    // A lost or poisoned partial poisons the head (see the register merge above).
+    if (tid == 0)
+      __hip_atomic_store(&a.epoch[h], LL != LL ? kPoisonEpoch : tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  __syncthreads();
-  // Wavefront 0: one partial per lane -> weights 2^(m_j - M) (0 for empty
-  // partials) and the total L (NaN if any partial is poisoned); then every
-  // column is a branch-free dot product.
-  float* wts = comb;  // P weights, then L at [kStepMaxP]
-  if (wave == 0) {
-    const float mj = lane < P ? pb[lane * (D + 2)] : -INFINITY;
-    const float lj = lane < P ? pb[lane * (D + 2) + 1] : 0.f;
-    float mx = lj > 0.f ? mj : -INFINITY;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, xor_lanes(mx, off));
-    const float w = (lj > 0.f && mx != -INFINITY) ? fast_exp2(mj - mx) : 0.f;
-    if (lane < P) wts[lane] = w;
-    const float Lt = wave_sum(w * lj);
-    const bool any_bad = __any(bad || mj != mj || lj != lj);
-    if (lane == 0) wts[kStepMaxP] = any_bad ? __builtin_nanf("") : Lt;
-  }
-  __syncthreads();
-  const float LL = wts[kStepMaxP];
-  if (d < D) {
-    float AA = 0.f;
-#pragma unroll 8
-    for (int j = 0; j < P; ++j) AA = fmaf(wts[j], pb[j * (D + 2) + 2 + d], AA);
-    out[d] = from_f32<T>(LL != LL ? LL : (LL > 0.f ? AA / LL : 0.f));
-  }
-  CSAHCA_STAMP(6);
-  __syncthreads();
-  // A lost or poisoned partial poisons the head (see the register merge above).
-  if (tid == 0)
-    __hip_atomic_store(&a.epoch[h], LL != LL ? kPoisonEpoch : tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Every argument of the step, requested from the kernel-argument segment in
@@ -679,7 +687,7 @@ __host__ __device__ inline StepLead step_lead_of(const StepParams& a) {
   return StepLead{a.summary, a.q, a.epoch, a.Cs, a.c_dev, a.pos_dev, a.colo_bh, a.P};
 }
 
-template <typename T, int D, int TOPK_M, bool POS, bool PIPE = false, int W = kStepWaves>
+template <typename T, int D, int TOPK_M, bool POS, bool PIPE = false, int W = kStepWaves, int MERGE = kMergeBoth>
 __global__ __launch_bounds__(W * kWave) void csa_step_kernel(const float* summary, const void* q, uint32_t* epoch,
                                                              int64_t Cs, const int32_t* c_dev,
                                                              const int64_t* pos_dev, uint32_t colo_bh, int32_t P,
@@ -692,7 +700,7 @@ __global__ __launch_bounds__(W * kWave) void csa_step_kernel(const float* summar
   a.pos_dev = pos_dev;
   a.colo_bh = colo_bh;
   a.P = P;
-  csa_step_body<T, D, TOPK_M, POS, PIPE, W>(a, blockIdx.x);
+  csa_step_body<T, D, TOPK_M, POS, PIPE, W, MERGE>(a, blockIdx.x);
 }
 
 // The hybrid step: blocks [0, step_blocks) run the decode step above, the rest
@@ -762,23 +770,34 @@ using StepKernelFn = void (*)(const float*, const void*, uint32_t*, int64_t, con
 using HybridKernelFn = void (*)(StepParams, HcaPart, uint32_t);
 
 // The instantiation of the step kernel a call launches (m: top-k register rows).
-template <typename T>
-StepKernelFn step_kernel_for(int64_t head_dim, int m, bool pos) {
-#define CSAHCA_PICK(DD)                                                                            \
-  if (m == 8) return pos ? csa_step_kernel<T, DD, 8, true> : csa_step_kernel<T, DD, 8, false>;    \
-  if (m == 32) return pos ? csa_step_kernel<T, DD, 32, true> : csa_step_kernel<T, DD, 32, false>; \
-  return pos ? csa_step_kernel<T, DD, 0, true> : csa_step_kernel<T, DD, 0, false>;
+// (lds: the instantiation with the LDS merge, for P > kRegMergeP)
+template <typename T, int MG>
+StepKernelFn step_kernel_merge(int64_t head_dim, int m, bool pos) {
+#define CSAHCA_PICK(DD)                                                                                \
+  if (m == 8)                                                                                          \
+    return pos ? csa_step_kernel<T, DD, 8, true, false, kStepWaves, MG>                               \
+               : csa_step_kernel<T, DD, 8, false, false, kStepWaves, MG>;                             \
+  if (m == 32)                                                                                         \
+    return pos ? csa_step_kernel<T, DD, 32, true, false, kStepWaves, MG>                              \
+               : csa_step_kernel<T, DD, 32, false, false, kStepWaves, MG>;                            \
+  return pos ? csa_step_kernel<T, DD, 0, true, false, kStepWaves, MG>                                 \
+             : csa_step_kernel<T, DD, 0, false, false, kStepWaves, MG>;
   if (head_dim == 64) { CSAHCA_PICK(64) }
   if (head_dim == 128) { CSAHCA_PICK(128) }
   CSAHCA_PICK(256)
 #undef CSAHCA_PICK
 }
 
-StepKernelFn step_kernel_for_dtype(int dtype, int64_t head_dim, int m, bool pos) {
+template <typename T>
+StepKernelFn step_kernel_for(int64_t head_dim, int m, bool pos, bool lds) {
+  return lds ? step_kernel_merge<T, kMergeLds>(head_dim, m, pos) : step_kernel_merge<T, kMergeRegs>(head_dim, m, pos);
+}
+
+StepKernelFn step_kernel_for_dtype(int dtype, int64_t head_dim, int m, bool pos, bool lds) {
   switch (dtype) {
-    case CSAHCA_BF16: return step_kernel_for<bf16>(head_dim, m, pos);
-    case CSAHCA_F16: return step_kernel_for<f16>(head_dim, m, pos);
-    case CSAHCA_F32: return step_kernel_for<float>(head_dim, m, pos);
+    case CSAHCA_BF16: return step_kernel_for<bf16>(head_dim, m, pos, lds);
+    case CSAHCA_F16: return step_kernel_for<f16>(head_dim, m, pos, lds);
+    case CSAHCA_F32: return step_kernel_for<float>(head_dim, m, pos, lds);
     default: return nullptr;
   }
 }
@@ -799,7 +818,8 @@ StepKernelFn step_kernel_pipelined(int dtype, int64_t head_dim, int m) {
 }
 
 // The wide instantiation: a head's whole step in one workgroup of
-// kWideWaves wavefronts (P = 1, so nothing crosses workgroups), its summary and
+// kWideWaves wavefronts (P = 1, so nothing crosses workgroups and no merge
+// beyond the workgroup's own is compiled in), its summary and
 // K/V batches double-buffered.  bf16/f16, head_dim 128, count modes; nullptr
 // elsewhere.  (8 wavefronts: at 256 heads with top-32 selections 1-4% faster
 // than 16, whose extra loads in flight one CU cannot return any faster.)
@@ -807,13 +827,13 @@ constexpr int kWideWaves = 8;
 StepKernelFn step_kernel_wide(int dtype, int64_t head_dim, int m) {
   if (head_dim != 128) return nullptr;
   if (dtype == CSAHCA_BF16)
-    return m == 8    ? csa_step_kernel<bf16, 128, 8, false, true, kWideWaves>
-           : m == 32 ? csa_step_kernel<bf16, 128, 32, false, true, kWideWaves>
-                     : csa_step_kernel<bf16, 128, 0, false, true, kWideWaves>;
+    return m == 8    ? csa_step_kernel<bf16, 128, 8, false, true, kWideWaves, kMergeRegs>
+           : m == 32 ? csa_step_kernel<bf16, 128, 32, false, true, kWideWaves, kMergeRegs>
+                     : csa_step_kernel<bf16, 128, 0, false, true, kWideWaves, kMergeRegs>;
   if (dtype == CSAHCA_F16)
-    return m == 8    ? csa_step_kernel<f16, 128, 8, false, true, kWideWaves>
-           : m == 32 ? csa_step_kernel<f16, 128, 32, false, true, kWideWaves>
-                     : csa_step_kernel<f16, 128, 0, false, true, kWideWaves>;
+    return m == 8    ? csa_step_kernel<f16, 128, 8, false, true, kWideWaves, kMergeRegs>
+           : m == 32 ? csa_step_kernel<f16, 128, 32, false, true, kWideWaves, kMergeRegs>
+                     : csa_step_kernel<f16, 128, 0, false, true, kWideWaves, kMergeRegs>;
   return nullptr;
 }
 
@@ -1003,21 +1023,25 @@ int decode_step_impl(const void* q, const void* k_cache, const void* v_cache, co
     const bool hyb = hybrid != nullptr && head_dim == 128 && pos_dev == nullptr &&
                      (dtype == CSAHCA_BF16 || dtype == CSAHCA_F16);
     const HybridKernelFn hfn = hyb ? hybrid_kernel_for(dtype, m) : nullptr;
-    const StepKernelFn sfn = hyb ? nullptr : step_kernel_for_dtype(dtype, head_dim, m, pos_dev != nullptr);
-    const void* fn = hyb ? reinterpret_cast<const void*>(hfn) : reinterpret_cast<const void*>(sfn);
+    // (the step kernel with the merge P needs: from registers up to
+    // kRegMergeP partials, through LDS beyond)
+    auto step_fn = [&] { return step_kernel_for_dtype(dtype, head_dim, m, pos_dev != nullptr, P > kRegMergeP); };
+    StepKernelFn sfn = hyb ? nullptr : step_fn();
     auto launch_lds = [&] { return hyb ? std::max(lds, hybrid_lds) : lds; };
     // The P workgroups of a head wait on each other, so with P > 1 every step
     // workgroup of the grid must fit on the device at once (measured for the
     // instantiation launched, with its LDS); the step blocks of the hybrid
     // kernel come first in its grid.  Where they would not fit, P shrinks,
-    // down to 1 (no exchange at all).
-    if (P > 1) {
+    // down to 1 (no exchange at all), and the kernel is picked again for the
+    // new P (and checked again).
+    for (int pass = 0; P > 1 && pass < 4; ++pass) {
+      const void* fn = hyb ? reinterpret_cast<const void*>(hfn) : reinterpret_cast<const void*>(sfn);
       const int64_t cap = static_cast<int64_t>(resident_per_cu(fn, launch_lds())) * ncu;
-      if (bh * P > cap) {
-        P = cap / bh;
-        if (P < 2) P = 1;
-        lds = lds_for(P);
-      }
+      if (bh * P <= cap) break;
+      P = cap / bh;
+      if (P < 2) P = 1;
+      lds = lds_for(P);
+      if (!hyb) sfn = step_fn();
     }
     CSAHCA_REQUIRE(bh * P <= INT32_MAX, "too many heads in one call");
     StepParams pr;
