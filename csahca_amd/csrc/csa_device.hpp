@@ -289,6 +289,27 @@ __device__ bool wave_topk_regs(const uint32_t* keys, int C, int k, uint32_t* scr
   return true;
 }
 
+// Position of the largest key of keys[0, C) (C >= 1), larger key first and
+// equal keys by lower position: the first slot of every top-k above, found by
+// a maximum over the 64-bit composites key << 32 | ~position -- a scan and a
+// wavefront reduction, far shorter than the selection.
+__device__ __forceinline__ int32_t wave_top1(const uint32_t* keys, int C) {
+  const int lane = threadIdx.x & (kWave - 1);
+  unsigned long long best = 0ull;
+  for (int i = lane; i < C; i += kWave) {
+    const unsigned long long c = (static_cast<unsigned long long>(keys[i]) << 32) | static_cast<uint32_t>(~i);
+    best = c > best ? c : best;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const uint32_t lo = static_cast<uint32_t>(__shfl_xor(static_cast<int>(static_cast<uint32_t>(best)), off, kWave));
+    const uint32_t hi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(best >> 32), off, kWave));
+    const unsigned long long o = (static_cast<unsigned long long>(hi) << 32) | lo;
+    best = o > best ? o : best;
+  }
+  return static_cast<int32_t>(~static_cast<uint32_t>(best));
+}
+
 // Register-path size for a selection: keys per lane M (C <= 64 * M), or 0 for
 // the LDS radix path only.  Kernels take M as a template parameter so each
 // instantiation carries exactly one register path.
@@ -498,16 +519,33 @@ __device__ __forceinline__ void attend_block(WaveSoftmax<T, D>& st, const T* qp,
 // next one, so no load sits under a branch (a branch join would make the
 // compiler wait for every outstanding load).  q is loaded first.
 template <typename T, int D, int U, typename TokOf>
+__device__ __forceinline__ void attend_pipelined_from(WaveSoftmax<T, D>& st, AttendRows<U>& ra, const uint4& q16,
+                                                      float qscale, const T* __restrict__ kb,
+                                                      const T* __restrict__ vb, int base, int stride, int s1,
+                                                      int grp, TokOf tok_of);
+
+template <typename T, int D, int U, typename TokOf>
 __device__ __forceinline__ void attend_pipelined(WaveSoftmax<T, D>& st, const T* qp, float qscale,
                                                  const T* __restrict__ kb, const T* __restrict__ vb, int base,
                                                  int stride, int s1, int grp, TokOf tok_of) {
   if (base >= s1) return;
   const uint4 q16 = load_global_u4(qp);
+  AttendRows<U> ra;
+  attend_issue<T, D, U>(ra, kb, vb, base, s1, grp, tok_of);
+  attend_pipelined_from<T, D, U>(st, ra, q16, qscale, kb, vb, base, stride, s1, grp, tok_of);
+}
+
+// The same walk, its first batch (rows `base`..) and q already requested by
+// the caller into ra and q16.
+template <typename T, int D, int U, typename TokOf>
+__device__ __forceinline__ void attend_pipelined_from(WaveSoftmax<T, D>& st, AttendRows<U>& ra, const uint4& q16,
+                                                      float qscale, const T* __restrict__ kb,
+                                                      const T* __restrict__ vb, int base, int stride, int s1,
+                                                      int grp, TokOf tok_of) {
   // Two buffers in turn (no copy between them: a copy lets the compiler load
   // the next batch into the registers of the one still in flight, which makes
   // every load wait for its predecessor).
-  AttendRows<U> ra, rb;
-  attend_issue<T, D, U>(ra, kb, vb, base, s1, grp, tok_of);
+  AttendRows<U> rb;
   float qf[AttendLayout<T, D>::VEC];
   attend_q<T, D>(q16, qscale, qf);
   for (;;) {

@@ -417,6 +417,33 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
   }
   __syncthreads();
   CSAHCA_STAMP(2);
+  constexpr int kAttendStride = W * RPL * U;
+  // Double-buffered walk of a whole head (PIPE, P = 1, C <= 512): the first
+  // batch of phase C lies inside the best chunk, which every wavefront finds
+  // with one scan of the keys (exactly the top-k's first slot), so its rows
+  // are requested before the selection runs and their round trip overlaps it
+  // (B32 H8 top-8, iid keys: S8192 20.5 -> 20.0 us, S32768 28.9 -> 28.6 us;
+  // at C = 2048 the scan cost more than it hid).  The batch-by-batch
+  // instantiation keeps its code unchanged.
+  bool early = false;
+  AttendRows<U> r_first;
+  uint4 q_first;
+  if constexpr (PIPE && W == kStepWaves) {
+    const int ns = a.topk * a.chunk;  // this workgroup's slots [0, ns) at P = 1
+    early = P == 1 && C > 0 && C <= 512 && a.topk > 0 && a.chunk >= kAttendStride && ns > kAttendStride;
+    if (early) {
+      const int32_t c_first = wave_top1(keys_l, static_cast<int>(C));
+      auto first_id = [&](int) { return c_first; };
+      auto tok_first = [&](int s, int64_t& tok) {
+        return slot_token_of(first_id, s, a.chunk, a.chunk_shift, a.S, tok);
+      };
+      const int g = lane / LPR, cl = lane % LPR;
+      q_first = load_global_u4(q + cl * VEC);
+      attend_issue<T, D, U>(r_first, static_cast<const T*>(a.kcache) + h * a.S * D + cl * VEC,
+                            static_cast<const T*>(a.vcache) + h * a.S * D + cl * VEC, wave * RPL * U, ns, g,
+                            tok_first);
+    }
+  }
   if (wave == 0) {
     int32_t* io = a.idx_out + h * a.topk;
     const bool write_ids = (p == 0);
@@ -455,10 +482,12 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
   WaveSoftmax<T, D> st;
   st.init();
   // Batch by batch, or double-buffered when this workgroup has its CU alone.
-  constexpr int kAttendStride = W * RPL * U;
   if (!PIPE || s1 - s0 <= kAttendStride) {
     for (int blk = s0; blk < s1; blk += kAttendStride)
       attend_block<T, D, U>(st, qp, a.qscale, kb, vb, blk + wave * RPL * U, s1, grp, tok_of);
+  } else if (early) {
+    attend_pipelined_from<T, D, U>(st, r_first, q_first, a.qscale, kb, vb, s0 + wave * RPL * U, kAttendStride, s1,
+                                   grp, tok_of);
   } else {
     attend_pipelined<T, D, U>(st, qp, a.qscale, kb, vb, s0 + wave * RPL * U, kAttendStride, s1, grp, tok_of);
   }

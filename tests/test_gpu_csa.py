@@ -399,6 +399,37 @@ def test_fused_step_ties_and_planted_selections():
     assert all(v == 0 for v in native.csa_step_status().values())
 
 
+def test_pipelined_step_first_batch_follows_the_tie_break():
+    """At B32 H8 S8192 top-8 each head is one workgroup (P = 1, the
+    double-buffered instantiation), which requests the rows of its first slots
+    from a scan for the best chunk while the selection still runs.  With values
+    constant per chunk (every row of chunk c holds c) the output is the
+    softmax-weighted mean of the attended chunk ids, so a first batch read from
+    any chunk but the selection's first shows: all keys tied (ids 0..7, the
+    first chunk 0 and not the last tied one), then two planted chunks tied above
+    the rest (the lower id first)."""
+    B, H, S, D, chunk, k = 32, 8, 8192, 128, 64, 8
+    q = torch.ones(B, H, D, dtype=torch.bfloat16, device=DEV)
+    kc = torch.ones(B, H, S, D, dtype=torch.bfloat16, device=DEV)
+    ids = (torch.arange(S, device=DEV) // chunk).to(torch.bfloat16)
+    vc = ids[None, None, :, None].expand(B, H, S, D).contiguous()
+    for planted, first in ((), list(range(k))), ((77, 5), [5, 77, 0, 1, 2, 3, 4, 6]):
+        for c in planted:
+            kc[:, :, c * chunk:(c + 1) * chunk] = 2.0
+        out, idx = native.csa_decode_step(q, kc, vc, extension.csa_chunk_summary(kc, chunk), chunk, k)
+        want = torch.tensor(first, dtype=torch.int32).expand(B, H, k)
+        assert torch.equal(idx.cpu(), want)
+        tok = (idx.long().unsqueeze(-1) * chunk + torch.arange(chunk, device=DEV)).reshape(B, H, k * chunk, 1)
+        kg = torch.gather(kc, 2, tok.expand(-1, -1, -1, D)).cpu()
+        vg = torch.gather(vc, 2, tok.expand(-1, -1, -1, D)).cpu()
+        local = torch.arange(k, dtype=torch.int32).expand(B, H, k).contiguous()
+        ref = oracle.csa_attend(q.cpu(), kg, vg, local, chunk, prob_dtype=oracle.F32)
+        assert_close(out, ref, 2e-2, 1e-2, f"planted {planted}")
+    assert all(v == 0 for v in native.csa_step_status().values())
+    del q, kc, vc, out
+    torch.cuda.empty_cache()
+
+
 def test_fused_step_device_count_matches_oracle():
     B, H, S, D, chunk, k = 1, 8, 32768, 128, 64, 8
     case = make_synthetic_case(batch=B, heads=H, seq_len=S, head_dim=D, chunk_size=chunk, top_k=k, seed=6)
