@@ -289,25 +289,45 @@ __device__ bool wave_topk_regs(const uint32_t* keys, int C, int k, uint32_t* scr
   return true;
 }
 
-// Position of the largest key of keys[0, C) (C >= 1), larger key first and
-// equal keys by lower position: the first slot of every top-k above, found by
-// a maximum over the 64-bit composites key << 32 | ~position -- a scan and a
-// wavefront reduction, far shorter than the selection.
+// Position of the largest key of keys[0, C) (1 <= C <= 64 * M), larger key
+// first and equal keys by lower position: the first slot of every top-k
+// above.  Each lane reads its M keys in one batch (position 64 j + lane;
+// positions past C read as key 0 at a position above every real one, so they
+// never win a tie), keeps its best, and a butterfly of lane exchanges (DPP and
+// row swaps, no LDS) takes the best of all lanes in the same order: every
+// lane ends with the answer.  The whole wavefront must be active.
+template <int M>
 __device__ __forceinline__ int32_t wave_top1(const uint32_t* keys, int C) {
   const int lane = threadIdx.x & (kWave - 1);
-  unsigned long long best = 0ull;
-  for (int i = lane; i < C; i += kWave) {
-    const unsigned long long c = (static_cast<unsigned long long>(keys[i]) << 32) | static_cast<uint32_t>(~i);
-    best = c > best ? c : best;
-  }
+  uint32_t v[M];
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    const uint32_t lo = static_cast<uint32_t>(__shfl_xor(static_cast<int>(static_cast<uint32_t>(best)), off, kWave));
-    const uint32_t hi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(best >> 32), off, kWave));
-    const unsigned long long o = (static_cast<unsigned long long>(hi) << 32) | lo;
-    best = o > best ? o : best;
+  for (int j = 0; j < M; ++j) {
+    const int i = kWave * j + lane;
+    const uint32_t kv = keys[i < C ? i : C - 1];
+    v[j] = i < C ? kv : 0u;
   }
-  return static_cast<int32_t>(~static_cast<uint32_t>(best));
+  uint32_t bk = v[0], bp = static_cast<uint32_t>(lane);
+#pragma unroll
+  for (int j = 1; j < M; ++j) {  // positions rise with j: a later equal key loses
+    const bool take = v[j] > bk;
+    bk = take ? v[j] : bk;
+    bp = take ? static_cast<uint32_t>(kWave * j + lane) : bp;
+  }
+  // One 64-bit compare per exchange: key << 32 | ~position orders exactly so.
+  unsigned long long c = (static_cast<unsigned long long>(bk) << 32) | static_cast<uint32_t>(~bp);
+  auto step = [&](uint32_t hi, uint32_t lo) {
+    const unsigned long long o = (static_cast<unsigned long long>(hi) << 32) | lo;
+    c = o > c ? o : c;
+  };
+  auto hi = [&] { return static_cast<uint32_t>(c >> 32); };
+  auto lo = [&] { return static_cast<uint32_t>(c); };
+  step(lane_xor<1>(hi(), lane), lane_xor<1>(lo(), lane));
+  step(lane_xor<2>(hi(), lane), lane_xor<2>(lo(), lane));
+  step(lane_xor<4>(hi(), lane), lane_xor<4>(lo(), lane));
+  step(lane_xor<8>(hi(), lane), lane_xor<8>(lo(), lane));
+  step(lane_xor<16>(hi(), lane), lane_xor<16>(lo(), lane));
+  step(lane_xor<32>(hi(), lane), lane_xor<32>(lo(), lane));
+  return static_cast<int32_t>(~static_cast<uint32_t>(c));
 }
 
 // Register-path size for a selection: keys per lane M (C <= 64 * M), or 0 for
@@ -515,9 +535,9 @@ __device__ __forceinline__ void attend_block(WaveSoftmax<T, D>& st, const T* qp,
 // Several batches (base, base + stride, ... below s1), double-buffered: the
 // rows of batch i + 1 are requested before batch i is consumed, so a lane
 // keeps two batches in flight instead of waiting a memory round trip per
-// batch.  The last batch re-requests its own rows (cache hits) in place of a
-// next one, so no load sits under a branch (a branch join would make the
-// compiler wait for every outstanding load).  q is loaded first.
+// batch.  Every load is unconditional (a load under a branch makes the
+// compiler wait for every outstanding load at the join), and the last batch
+// is consumed in a tail of its own.  q is loaded first.
 template <typename T, int D, int U, typename TokOf>
 __device__ __forceinline__ void attend_pipelined_from(WaveSoftmax<T, D>& st, AttendRows<U>& ra, const uint4& q16,
                                                       float qscale, const T* __restrict__ kb,
@@ -544,19 +564,28 @@ __device__ __forceinline__ void attend_pipelined_from(WaveSoftmax<T, D>& st, Att
                                                       int grp, TokOf tok_of) {
   // Two buffers in turn (no copy between them: a copy lets the compiler load
   // the next batch into the registers of the one still in flight, which makes
-  // every load wait for its predecessor).
+  // every load wait for its predecessor).  The last batch is consumed in a
+  // tail of its own, so nothing is left in flight after the walk; base is
+  // made wavefront-uniform so the tests are scalar branches.
   AttendRows<U> rb;
   float qf[AttendLayout<T, D>::VEC];
   attend_q<T, D>(q16, qscale, qf);
+  base = __builtin_amdgcn_readfirstlane(base);
   for (;;) {
-    attend_issue<T, D, U>(rb, kb, vb, base + stride < s1 ? base + stride : base, s1, grp, tok_of);
+    if (base + stride >= s1) {
+      attend_consume<T, D, U>(st, ra, qf);
+      break;
+    }
+    attend_issue<T, D, U>(rb, kb, vb, base + stride, s1, grp, tok_of);
     attend_consume<T, D, U>(st, ra, qf);
     base += stride;
-    if (base >= s1) break;
-    attend_issue<T, D, U>(ra, kb, vb, base + stride < s1 ? base + stride : base, s1, grp, tok_of);
+    if (base + stride >= s1) {
+      attend_consume<T, D, U>(st, rb, qf);
+      break;
+    }
+    attend_issue<T, D, U>(ra, kb, vb, base + stride, s1, grp, tok_of);
     attend_consume<T, D, U>(st, rb, qf);
     base += stride;
-    if (base >= s1) break;
   }
 }
 

@@ -371,22 +371,31 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
       }
     } else {
       // Several batches, double-buffered: batch i + 1 is requested before batch
-      // i is scored; the last batch re-requests its own rows (cache hits) in
-      // place of a next one, so no load sits under a branch.
-      // The two buffers alternate without a copy (a copy lets the compiler load
-      // into the registers of the batch still in flight).
+      // i is scored.  The last batch is scored in a tail of its own, so no load
+      // sits under a branch (a join would make the compiler wait for every
+      // load in flight) and none is left in flight after the walk (its
+      // registers' next use would wait for it; the branches test the
+      // workgroup-uniform blk).  The two buffers alternate without a copy (a
+      // copy lets the compiler load into the registers of the batch still in
+      // flight).  Here c1 - c0 > kScoreStride: at least two batches.
       const uint4 q4 = load_q4();
       uint4 ra[US], rb[US];
       issue_rows(c0, ra);
       for (int64_t blk = c0;;) {
-        issue_rows(blk + kScoreStride < c1 ? blk + kScoreStride : blk, rb);
+        issue_rows(blk + kScoreStride, rb);
         score_rows(blk, ra, q4);
         blk += kScoreStride;
-        if (blk >= c1) break;
-        issue_rows(blk + kScoreStride < c1 ? blk + kScoreStride : blk, ra);
+        if (blk + kScoreStride >= c1) {
+          score_rows(blk, rb, q4);
+          break;
+        }
+        issue_rows(blk + kScoreStride, ra);
         score_rows(blk, rb, q4);
         blk += kScoreStride;
-        if (blk >= c1) break;
+        if (blk + kScoreStride >= c1) {
+          score_rows(blk, ra, q4);
+          break;
+        }
       }
     }
   }
@@ -432,7 +441,7 @@ __device__ __forceinline__ void csa_step_body(StepParams a, uint32_t block) {
     const int ns = a.topk * a.chunk;  // this workgroup's slots [0, ns) at P = 1
     early = P == 1 && C > 0 && C <= 512 && a.topk > 0 && a.chunk >= kAttendStride && ns > kAttendStride;
     if (early) {
-      const int32_t c_first = wave_top1(keys_l, static_cast<int>(C));
+      const int32_t c_first = wave_top1<8>(keys_l, static_cast<int>(C));
       auto first_id = [&](int) { return c_first; };
       auto tok_first = [&](int s, int64_t& tok) {
         return slot_token_of(first_id, s, a.chunk, a.chunk_shift, a.S, tok);
