@@ -526,20 +526,12 @@ GRID = [  # every point of the sweep B {1, 8, 32} x S {8192, 32768, 131072} x to
 ]
 
 
-@pytest.mark.parametrize("B,S,k", GRID)
-def test_sweep_grid_point_matches_oracle(B, S, k):
-    """The fused decode step at a config-1 grid point (H8 D128 chunk 64, bf16
-    N(0,1) drawn on the device) against the oracle: chunk summaries on the
-    first and last head, selection from the device summaries (ids bit-exact up
-    to 1e-5 score ties), and attention over the selected chunks' tokens, which
-    are gathered on the device so the oracle works on [B, H, k*64, D] copies.
-
-    The launch shape the host picks differs across the grid: P = 8 workgroups
-    per head with a head's workgroups on one XCD at B1 S32768 top-8; P = 1 and
-    the double-buffered instantiation at B32 top-8 (at S131072 over K and V of
-    2^32 elements, 8 GiB, each, so the byte offsets of the last heads pass
-    2^32); the 8-wavefront instantiation at B32 top-32."""
-    H, D, chunk = 8, 128, 64
+def _check_step_against_oracle(B, S, k, H=8, D=128, chunk=64):
+    """The fused decode step on N(0,1) bf16 inputs drawn on the device against
+    the oracle: chunk summaries on the first and last head, selections of
+    every head (bit-exact up to 1e-5 score ties), and the attention of every
+    head over the selected chunks' tokens, gathered on the device so the
+    oracle works on [B, H, k*chunk, D] copies."""
     g = torch.Generator(device=DEV).manual_seed(B * 31 + S // 1024 + k)
     q = torch.randn(B, H, D, device=DEV, generator=g).to(torch.bfloat16)
     kc = torch.randn(B, H, S, D, device=DEV, generator=g, dtype=torch.bfloat16)
@@ -560,6 +552,37 @@ def test_sweep_grid_point_matches_oracle(B, S, k):
     assert all(v == 0 for v in native.csa_step_status().values())
     del q, kc, vc, summ, out
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("B,S,k", GRID)
+def test_sweep_grid_point_matches_oracle(B, S, k):
+    """The fused decode step at a config-1 grid point (H8 D128 chunk 64, bf16
+    N(0,1) drawn on the device) against the oracle: chunk summaries on the
+    first and last head, selection from the device summaries (ids bit-exact up
+    to 1e-5 score ties), and attention over the selected chunks' tokens, which
+    are gathered on the device so the oracle works on [B, H, k*64, D] copies.
+
+    The launch shape the host picks differs across the grid: P = 8 workgroups
+    per head with a head's workgroups on one XCD at B1 S32768 top-8; P = 1 and
+    the double-buffered instantiation at B32 top-8 (at S131072 over K and V of
+    2^32 elements, 8 GiB, each, so the byte offsets of the last heads pass
+    2^32); the 8-wavefront instantiation at B32 top-32."""
+    _check_step_against_oracle(B, S, k)
+
+
+
+@pytest.mark.parametrize("B,S,k", [
+    (32, 12288, 5),  # 192 chunks: 3 summary batches; 320 slots: 5 attention batches, the first requested early
+    (32, 20480, 3),  # 320 chunks: 5 summary batches; 192 slots: 3 attention batches
+    (32, 16384, 1),  # 64 slots: one attention batch per wavefront (batch by batch)
+])
+def test_double_buffered_walks_end_in_either_buffer(B, S, k):
+    """At B32 H8 each head is one workgroup on the double-buffered
+    instantiation, whose walks consume their last batch in a tail of their own:
+    in the second buffer after an even number of batches (every config-1
+    point) and in the first after an odd number, which these shapes give to
+    both the summary walk and the attention walk."""
+    _check_step_against_oracle(B, S, k)
 
 
 def test_largest_sweep_point_properties():
