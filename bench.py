@@ -79,6 +79,9 @@ def parse_args():
     ap.add_argument("--dsv4-case", default=None, metavar="cR_nqN_hH",
                     help="run only this DSV4 case (e.g. c4_nq32_h64), --steps eager calls over 16 rotated caches, "
                          "print its timing and exit (a short program to profile)")
+    ap.add_argument("--large-batch-only", action="store_true",
+                    help="run only the large-batch leg (B32 H8 S131072 top-32: 4 warm-up and 40 timed dispatches "
+                         "over two cache copies), print its JSON and exit (a short program to profile)")
     ap.add_argument("--no-graph", action="store_true",
                     help="time eager launches only (for profiler counter passes, which serialise dispatches)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
@@ -1060,6 +1063,9 @@ def main():
         return
     if args.dsv4_case:
         print(json.dumps(dsv4_case_run(args.dsv4_case, args.steps)), flush=True)
+        return
+    if args.large_batch_only:
+        print(json.dumps({"large_batch": large_batch_bench()}), flush=True)
         return
     r = csa_bench(args, copies=args.copies, attend_only=True)
     ms = r["ms_per_step_eager"] if args.no_graph else r["ms_per_step_graph"]
