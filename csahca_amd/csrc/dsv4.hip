@@ -1218,6 +1218,13 @@ __global__ __launch_bounds__(W * kWave) void dsv4_query_kernel(const bf16* __res
 // block's MFMA chain is the same in every shape and dim-part count; the
 // softmax sum adds per-wavefront partial sums, so the two shapes can differ in
 // its last bits.
+// A zero latent row (and scale bytes) for the slots of the one-pass kernel
+// that are past their list's length or invalid: they load it in place of a
+// cache row, so their K and V values are exact zeros with no per-value select
+// (e4m3 0 at scale byte 0 is +0, the rope bf16 0 is +0); their scores are
+// masked to -inf all the same.
+__device__ __align__(16) uint8_t g_dsv4_zero_row[1024];
+
 constexpr int kOpMaxSlots = 256;  // the largest list of the one-pass shapes
 constexpr int kOpProw = 272;      // P^T row stride in bf16 (136 dwords = 8 mod 64 banks)
 
@@ -1319,8 +1326,8 @@ __global__ __launch_bounds__(NW * kWave) void dsv4_onepass_kernel(const int32_t*
   // for every load in flight at the join)
   const float sink_raw = load_global_raw<float>(g.sink ? static_cast<const void*>(g.sink + h0 + min(l16, nh - 1))
                                                        : anyp);
-  // The rows of invalid slots re-read a query row (>= 1 KiB, in bounds).
-  const uint8_t* dummy = reinterpret_cast<const uint8_t*>(q + (query * a.heads + h0) * kDim);
+  // The rows of invalid slots read the zero row.
+  const uint8_t* dummy = g_dsv4_zero_row;
   // The cache views the row addresses need, requested now, while the slot
   // indices are in flight (left to itself the compiler loads them where the
   // addresses are formed: one more dependent round trip after the indices).
@@ -1399,8 +1406,7 @@ __global__ __launch_bounds__(NW * kWave) void dsv4_onepass_kernel(const int32_t*
           lo = dequant8_bf16_hw(make_uint2(w.c[i].x, w.c[i].y), sbyte);
           hi = dequant8_bf16_hw(make_uint2(w.c[i].z, w.c[i].w), sbyte);
         }
-        if (!w.ok) lo = hi = make_uint4(0u, 0u, 0u, 0u);  // skipped slot: zero K and V
-        const int d = 16 * (grp + 4 * i);                 // nope dims d .. d + 15
+        const int d = 16 * (grp + 4 * i);  // nope dims d .. d + 15 (a skipped slot's row is zero)
         if (d >= DW * part && d < DW * (part + 1)) {
           *reinterpret_cast<uint4*>(trow + (d - DW * part)) = lo;
           *reinterpret_cast<uint4*>(trow + (d - DW * part) + 8) = hi;
@@ -1417,7 +1423,7 @@ __global__ __launch_bounds__(NW * kWave) void dsv4_onepass_kernel(const int32_t*
       nope(std::true_type{});
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const uint4 rope = w.ok ? w.c[7 + i] : make_uint4(0u, 0u, 0u, 0u);
+      const uint4 rope = w.c[7 + i];
       const int d = kNope + 8 * (grp + 4 * i);  // rope dims d .. d + 7
       if (d >= DW * part && d < DW * (part + 1)) *reinterpret_cast<uint4*>(trow + (d - DW * part)) = rope;
       if (i == 0)
