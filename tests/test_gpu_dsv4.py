@@ -141,6 +141,44 @@ def test_edges():
     assert torch.all(gpu_out(c) == 0)
 
 
+def _poison_rows(cache, locs, page_size):
+    """Rows (and scale bytes) of the given token locations made of NaN codes:
+    e4m3 0x7f, bf16 rope 0x7fc0, scale bytes 254 (2^127)."""
+    rows = dsv4_layout.NOPE_ROPE_BYTES
+    for loc in locs:
+        page, slot = divmod(int(loc), page_size)
+        base = slot * rows
+        cache[page, base:base + dsv4_layout.DIM_NOPE] = 0x7F
+        cache[page, base + dsv4_layout.DIM_NOPE:base + rows] = torch.tensor([0xC0, 0x7F], dtype=torch.uint8).repeat(
+            dsv4_layout.DIM_ROPE)
+        sb = page_size * rows + slot * dsv4_layout.SCALE_BYTES_PER_TOKEN
+        cache[page, sb:sb + dsv4_layout.NUM_SCALE_TILES] = 254
+
+
+def test_onepass_never_reads_the_rows_of_slots_past_the_lengths():
+    """The one-pass kernel (bf16 queries, lists of at most 256 slots) loads a
+    zero row for every slot past its list's length: the rows those slots
+    index are filled with NaN codes here (and are indexed by no counted slot),
+    so any read of them would reach the output through the PV product."""
+    c = make_dsv4_case(compress_ratio=4, num_queries=4, heads=16, num_tokens=256, top_k=64, page_size=64,
+                       extra_tokens=256, extra_top_k=32, seed=9, device="cpu")
+    for idx, lens, cache, ps in ((c.token_indices, c.topk_lengths, c.cache, c.page_size),
+                                 (c.extra_token_indices, c.extra_topk_lengths, c.extra_cache, c.extra_page_size)):
+        counted = {int(v) for q in range(idx.shape[0]) for v in idx[q, :max(int(lens[q]), 0)].tolist()}
+        past = {int(v) for q in range(idx.shape[0]) for v in idx[q, max(int(lens[q]), 0):].tolist()}
+        poison = sorted(l for l in past - counted if l >= 0)
+        assert poison, "the case leaves no row indexed only past a length"
+        _poison_rows(cache, poison, ps)
+    want = oracle_out(c)
+    assert np.isfinite(want).all()
+    for name in ("q", "cache", "token_indices", "topk_lengths", "extra_cache", "extra_token_indices",
+                 "extra_topk_lengths", "attn_sink"):
+        setattr(c, name, getattr(c, name).to(DEV))
+    got = gpu_out(c)
+    assert torch.isfinite(got.float()).all()
+    assert_close(got, want, what="rows past the lengths poisoned")
+
+
 def test_unaligned_bytes_per_page_scalar_path():
     c = make_dsv4_case(compress_ratio=0, num_queries=3, heads=8, num_tokens=256, top_k=32, page_size=64, seed=7)
     bpp = c.cache.shape[1]
