@@ -1046,6 +1046,16 @@ int decode_step_impl(const void* q, const void* k_cache, const void* v_cache, co
     // rows are many: at 256 heads, P = 1 beats P = 2 by 8-11% with 512 rows
     // (top-8 of 64) and loses by 6% with 2048 (top-32).
     if (bh >= ncu && k * chunk_size <= 1024) P = 1;
+    // Above 16 workgroups per head, where half as many still leave each
+    // workgroup a CU of its own and the double-buffered instantiation runs
+    // (bf16/f16, head_dim 128, no position mode, not the hybrid), half as many
+    // workgroups walking two batches each beat the one-batch split: the key
+    // exchange and the merge shrink with P.  Measured at B1 H8, P 32 -> 16:
+    // S32768 top-32 14.0 -> 13.1 us, S131072 top-8 15.0 -> 14.8, top-32
+    // 16.7 -> 16.6; S8192 top-32 level.
+    const bool pipe_ok = (dtype == CSAHCA_BF16 || dtype == CSAHCA_F16) && head_dim == 128 && pos_dev == nullptr &&
+                         hybrid == nullptr;
+    if (P > 16 && pipe_ok && bh * (P / 2) <= ncu) P /= 2;
   }
   P = std::min<int64_t>({P, rg.max_p, ceil_div(num_chunks, 8), ceil_div(k * chunk_size, 16)});
   P = std::max<int64_t>(1, P);
