@@ -847,15 +847,17 @@ __global__ __launch_bounds__(kMfmaThreads) void dsv4_mfma_kernel(const bf16* __r
 // MFMA lane layouts: 16x16x32 as above; 16x16x16: A lane l elem j =
 // A[l%16][4(l/16)+j], B lane l elem j = B[4(l/16)+j][l%16], C as 16x16x32.
 // ---------------------------------------------------------------------------
-// float_to_bf16_bits without a branch (the same bits: round to nearest even,
-// infinities unchanged, NaN quietened), so that no control flow sits between
-// the MFMAs whose accumulators it feeds.
-__device__ __forceinline__ uint32_t bf16_bits_nb(float x) {
-  const uint32_t u = __float_as_uint(x);
-  const uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-  return (u & 0x7fffffffu) > 0x7f800000u ? ((u >> 16) | 0x40u) : r;
+// Two floats to packed bf16 with gfx950's packed conversion (one
+// v_cvt_pk_bf16_f32, no branch between the MFMAs whose operands it forms):
+// round to nearest even, infinities unchanged, NaN quietened -- the bits of
+// float_to_bf16_bits for every one of the 2^32 fp32 inputs (compared
+// exhaustively on the device), so the results are those of the software
+// rounding it replaces.
+__device__ __forceinline__ uint32_t bf16x2_nb(float lo, float hi) {
+  typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+  const bf16x2_v v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
 }
-__device__ __forceinline__ uint32_t bf16x2_nb(float lo, float hi) { return bf16_bits_nb(lo) | (bf16_bits_nb(hi) << 16); }
 
 constexpr int kQSub = 16;                 // slots per sub-tile
 constexpr int kQHeads = 16;
